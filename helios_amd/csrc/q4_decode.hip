@@ -1,0 +1,406 @@
+// Decode-shape affine-Q4 matmul on gfx950: y[M,N] = x[M,K] . W^T for M <= 16.
+//
+// Bandwidth-bound: every weight byte is read once from HBM with 16-byte coalesced
+// loads (one 1 KiB tile per wave-load), scales/biases once per group, nibbles are
+// expanded in registers (two VALU ops per bf16 pair) and the products run on the
+// matrix cores: per group, two v_mfma_f32_16x16x32_bf16 give -X_g (x times a
+// constant -1 operand, already in the accumulator layout) and two more give
+// sum(x*(1+q/16)) - X_g seeded from it; the group's scale and bias are then applied
+// to the fp32 accumulators (q4_common.h).  M is padded to 16 inside the MFMA, which
+// costs nothing here: the matrix cores are far from busy at this arithmetic
+// intensity, and the VALU work per weight stays at ~1.2 ops.
+//
+// Work split: one workgroup per 16-row block; its WAVES waves split the group pairs
+// of K and meet in LDS for a split-K sum (no atomics, no second pass).
+#include "q4_common.h"
+#include "q4_kernels.h"
+
+namespace q4 {
+namespace {
+
+// Lane l of a 16x16 accumulator holds rows 4*(l/16)+r (r < 4) of column l%16, and
+// row i of an MFMA result depends only on row i of its A operand, so A rows >= M
+// may hold anything: they only feed accumulator rows that are never stored.
+//
+// XLDS = true (M <= 4, x small): the workgroup first copies x[M,K] into LDS with
+// one cooperative wave of loads issued before the weight loads, so the x operands
+// cost LDS reads instead of a chain of L2 round trips.  XLDS = false (M up to 16):
+// each wave reads its x operands from global memory, one group pair ahead.
+//
+// GPW: group pairs a wave handles per pass.  All of a pass's weight tiles and
+// scales are requested before any arithmetic (GPW KiB in flight per wave, one HBM
+// round trip).  Loads are bounded buffer loads, so pairs past the wave's range read
+// as zero without branches; zero tiles with zero scale/bias add nothing.
+template <int MT, int GPW, bool XLDS>
+__global__ __launch_bounds__(1024) void decode_kernel(
+    const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x,
+    void* __restrict__ y, int m_rows, int n_rows, int k, int gpairs, int waves, int out_f32) {
+    constexpr int R = MT < 4 ? MT : 4;
+    extern __shared__ uint4 xs_lds[];  // XLDS: x[M][K] as bf16, 16 B per entry
+    const int rb = blockIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15;
+    const int kq = lane >> 4;
+    const int gp0 = (wave * gpairs) / waves;
+    const int cnt = ((wave + 1) * gpairs) / waves - gp0;
+    const uint32_t xbytes = (uint32_t)m_rows * (uint32_t)k * 2u;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, xbytes);
+    const int arow = col < m_rows ? col : m_rows - 1;  // any valid row for A rows >= M
+
+    if constexpr (XLDS) {
+        // cooperative copy x -> LDS; these loads are issued first so that waiting for
+        // them leaves the weight loads below in flight
+        const int chunks = (int)(xbytes >> 4);
+        const int nthr = waves * 64;
+        uint4 tmp[4];
+        for (int c0 = 0; c0 < chunks; c0 += 4 * nthr) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = c0 + u * nthr + (int)threadIdx.x;
+                tmp[u] = buffer_load16(xrs, c < chunks ? (uint32_t)c * 16u : kOutOfRange);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = c0 + u * nthr + (int)threadIdx.x;
+                if (c < chunks) xs_lds[c] = tmp[u];
+            }
+        }
+    }
+
+    const uint4 neg1_bits = make_uint4(0xBF80BF80u, 0xBF80BF80u, 0xBF80BF80u, 0xBF80BF80u);
+    const bf16x8 neg1 = __builtin_bit_cast(bf16x8, neg1_bits);
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc = zero;
+    bool synced = !XLDS;
+
+    for (int base = 0; base < cnt; base += GPW) {
+        const int gpb = gp0 + base;
+        const int left = cnt - base;
+        // this pass's tiles and scales as bounded buffers: pairs i >= left read as zero
+        const long first = (long)rb * gpairs + gpb;
+        const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * 64, (uint32_t)left * 1024u);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * 16, (uint32_t)left * 128u);
+        // element offset of this lane's x operand at pair i, group 0, half 0
+        const int xel = arow * k + 8 * kq + gpb * 128;
+        const int kleft = k - gpb * 128;
+
+        uint4 wv[GPW];
+        uint2 sv[GPW];
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+            wv[i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * 1024));
+            sv[i] = buffer_load8<kNonTemporal>(srs, (uint32_t)(col * 8 + i * 128));
+        }
+        if (!synced) {
+            __syncthreads();  // x is in LDS
+            synced = true;
+        }
+
+        // x operands for one group pair: [group][half]; columns past the row (padding
+        // or beyond this pass's pairs) read as zero
+        uint4 a[2][4];
+        auto load_x = [&](uint4* dst, int i) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int kb = i * 128 + (q >> 1) * 64 + (q & 1) * 32;
+                const bool ok = kb < kleft && i < left;
+                if constexpr (XLDS) {
+                    dst[q] = ok ? xs_lds[(xel + kb) >> 3] : make_uint4(0, 0, 0, 0);
+                } else {
+                    dst[q] = buffer_load16(xrs, ok ? (uint32_t)(xel + kb) * 2u : kOutOfRange);
+                }
+            }
+        };
+        load_x(a[0], 0);
+
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+            if (i + 1 < GPW) load_x(a[(i + 1) & 1], i + 1);
+            const uint4* ax = a[i & 1];
+#pragma unroll
+            for (int gi = 0; gi < 2; ++gi) {
+                const bf16x8 x0 = __builtin_bit_cast(bf16x8, ax[2 * gi]);
+                const bf16x8 x1 = __builtin_bit_cast(bf16x8, ax[2 * gi + 1]);
+                f32x4 xn = mfma16x16x32(x0, neg1, zero);
+                xn = mfma16x16x32(x1, neg1, xn);  // -X_g for rows 4*kq + r
+                const bf16x8 b0 = expand_word(gi ? wv[i].z : wv[i].x);
+                const bf16x8 b1 = expand_word(gi ? wv[i].w : wv[i].y);
+                f32x4 p = mfma16x16x32(x0, b0, xn);
+                p = mfma16x16x32(x1, b1, p);  // sum(x*q)/16
+                const uint32_t sbv = gi ? sv[i].y : sv[i].x;
+                const float s16 = bf16_lo(sbv) * 16.0f;
+                const float bi = bf16_hi(sbv);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    acc[r] = __builtin_fmaf(s16, p[r], acc[r]);
+                    acc[r] = __builtin_fmaf(-bi, xn[r], acc[r]);
+                }
+            }
+        }
+    }
+    if (!synced) __syncthreads();  // (cnt == 0) keep barriers uniform
+
+    __shared__ float red[16][R * 64];
+#pragma unroll
+    for (int r = 0; r < R; ++r) red[wave][r * 64 + lane] = acc[r];
+    __syncthreads();
+    for (int t = threadIdx.x; t < R * 64; t += waves * 64) {
+        float v = 0.f;
+        for (int w = 0; w < waves; ++w) v += red[w][t];
+        const int r = t >> 6;
+        const int l = t & 63;
+        const int mrow = 4 * (l >> 4) + r;
+        const int n = rb * 16 + (l & 15);
+        if (mrow < m_rows && n < n_rows) {
+            const long o = (long)mrow * n_rows + n;
+            if (out_f32)
+                static_cast<float*>(y)[o] = v;
+            else
+                static_cast<uint16_t*>(y)[o] = f32_to_bf16(v);
+        }
+    }
+}
+
+// Persistent streaming variant for M <= 4 (x staged in LDS).  Each workgroup walks
+// row blocks blockIdx.x, blockIdx.x + gridDim.x, ...; its waves split K and stream
+// their weight tiles in chunks of GPW group pairs, double-buffered, so the loads for
+// the next chunk (possibly of the next row block) are in flight while the current
+// one is multiplied.  Per workgroup, once:
+//   * x[M][K] is copied to LDS, each row zero-padded by GPW pairs so that operand
+//     reads need no bounds tests (zero tiles past a wave's range meet finite x);
+//   * -X_g (the group sums of x, negated) is computed with two MFMAs per group and
+//     kept in LDS in accumulator layout, so each row block needs only the two
+//     products of the group, seeded from that table.
+// Per row block the waves meet once in LDS (ping-pong buffers, one barrier).
+template <int MT, int GPW>
+__global__ __launch_bounds__(512) void decode_stream_kernel(
+    const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x,
+    void* __restrict__ y, int m_rows, int n_rows, int k, int gpairs, int nblocks, int waves, int out_f32) {
+    constexpr int R = MT < 4 ? MT : 4;
+    constexpr int kPad = GPW * 128;  // zero columns after each x row
+    extern __shared__ uint4 lds[];
+    // layout: x rows [m_rows][k + kPad] bf16, then -X table [2*gpairs][16] fp32
+    __shared__ float red[2][8][R * 64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15;
+    const int kq = lane >> 4;
+    const int gp0 = (wave * gpairs) / waves;
+    const int cnt = ((wave + 1) * gpairs) / waves - gp0;  // >= 1 (host: waves <= gpairs)
+    const int passes = (cnt + GPW - 1) / GPW;
+    const int my_blocks = (nblocks - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int chunks = my_blocks * passes;
+    const int arow = col < m_rows ? col : m_rows - 1;  // any valid row for A rows >= M
+    const int row16 = (k + kPad) >> 3;                 // x row stride in 16-byte units
+    float* negx = reinterpret_cast<float*>(lds + m_rows * row16);
+
+    uint4 wa[GPW], wb[GPW];
+    uint2 sa[GPW], sbv2[GPW];
+    auto issue = [&](uint4* wv, uint2* sv, int c) {
+        const int rb = (int)blockIdx.x + (c / passes) * (int)gridDim.x;
+        const int pass = c % passes;
+        const int gpb = gp0 + pass * GPW;
+        const int left = cnt - pass * GPW;
+        const int n_in = left < GPW ? left : GPW;
+        const long first = (long)rb * gpairs + gpb;
+        const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * 64, (uint32_t)n_in * 1024u);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * 16, (uint32_t)n_in * 128u);
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+            wv[i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * 1024));
+            sv[i] = buffer_load8<kNonTemporal>(srs, (uint32_t)(col * 8 + i * 128));
+        }
+    };
+
+    // x -> LDS (loads issued before any weight load), zero padding after each row
+    {
+        const int xchunks = (m_rows * k) >> 3;
+        const int rowc = k >> 3;
+        const int nthr = waves * 64;
+        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)k * 2u);
+        for (int c0 = 0; c0 < xchunks; c0 += 4 * nthr) {
+            uint4 tmp[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = c0 + u * nthr + (int)threadIdx.x;
+                tmp[u] = buffer_load16(xrs, c < xchunks ? (uint32_t)c * 16u : kOutOfRange);
+            }
+            if (c0 == 0 && chunks > 0) issue(wa, sa, 0);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = c0 + u * nthr + (int)threadIdx.x;
+                if (c < xchunks) lds[(c / rowc) * row16 + (c % rowc)] = tmp[u];
+            }
+        }
+        for (int c = threadIdx.x; c < m_rows * (kPad >> 3); c += nthr)
+            lds[(c / (kPad >> 3)) * row16 + rowc + (c % (kPad >> 3))] = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+
+    const uint4 neg1_bits = make_uint4(0xBF80BF80u, 0xBF80BF80u, 0xBF80BF80u, 0xBF80BF80u);
+    const bf16x8 neg1 = __builtin_bit_cast(bf16x8, neg1_bits);
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    // -X_g for this wave's groups, in accumulator layout (rows 4*kq + r)
+    {
+        const int xb = arow * row16 + kq;
+        for (int g = 2 * gp0; g < 2 * (gp0 + cnt); ++g) {
+            const bf16x8 x0 = __builtin_bit_cast(bf16x8, lds[xb + g * 8]);
+            const bf16x8 x1 = __builtin_bit_cast(bf16x8, lds[xb + g * 8 + 4]);
+            f32x4 xn = mfma16x16x32(x0, neg1, zero);
+            xn = mfma16x16x32(x1, neg1, xn);
+            if (col == 0) *reinterpret_cast<f32x4*>(negx + g * 16 + 4 * kq) = xn;
+        }
+    }
+    __syncthreads();
+
+    f32x4 acc = zero;
+    int parity = 0;
+    auto compute = [&](const uint4* wv, const uint2* sv, int c) {
+        const int pass = c % passes;
+        const int gpb = gp0 + pass * GPW;
+        const uint4* xp = lds + arow * row16 + kq + gpb * 16;  // x operand, pair 0
+        const float* np = negx + gpb * 32 + 4 * kq;              // -X table, pair 0
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+#pragma unroll
+            for (int gi = 0; gi < 2; ++gi) {
+                const bf16x8 x0 = __builtin_bit_cast(bf16x8, xp[i * 16 + gi * 8]);
+                const bf16x8 x1 = __builtin_bit_cast(bf16x8, xp[i * 16 + gi * 8 + 4]);
+                f32x4 xn;
+                if constexpr (R == 1) {
+                    xn = zero;
+                    xn[0] = np[i * 32 + gi * 16];
+                } else {
+                    xn = *reinterpret_cast<const f32x4*>(np + i * 32 + gi * 16);
+                }
+                const bf16x8 b0 = expand_word(gi ? wv[i].z : wv[i].x);
+                const bf16x8 b1 = expand_word(gi ? wv[i].w : wv[i].y);
+                f32x4 p = mfma16x16x32(x0, b0, xn);
+                p = mfma16x16x32(x1, b1, p);  // sum(x*q)/16
+                const uint32_t sbw = gi ? sv[i].y : sv[i].x;
+                const float s16 = bf16_lo(sbw) * 16.0f;
+                const float bi = bf16_hi(sbw);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    acc[r] = __builtin_fmaf(s16, p[r], acc[r]);
+                    acc[r] = __builtin_fmaf(-bi, xn[r], acc[r]);
+                }
+            }
+        }
+        if (pass == passes - 1) {  // row block done: split-K sum across the waves
+            const int rb = (int)blockIdx.x + (c / passes) * (int)gridDim.x;
+#pragma unroll
+            for (int r = 0; r < R; ++r) red[parity][wave][r * 64 + lane] = acc[r];
+            __syncthreads();
+            for (int t = threadIdx.x; t < R * 64; t += waves * 64) {
+                float v = 0.f;
+                for (int w = 0; w < waves; ++w) v += red[parity][w][t];
+                const int r = t >> 6;
+                const int l = t & 63;
+                const int mrow = 4 * (l >> 4) + r;
+                const int n = rb * 16 + (l & 15);
+                if (mrow < m_rows && n < n_rows) {
+                    const long o = (long)mrow * n_rows + n;
+                    if (out_f32)
+                        static_cast<float*>(y)[o] = v;
+                    else
+                        static_cast<uint16_t*>(y)[o] = f32_to_bf16(v);
+                }
+            }
+            acc = zero;
+            parity ^= 1;
+        }
+    };
+
+    for (int c = 0; c < chunks; c += 2) {
+        if (c + 1 < chunks) issue(wb, sbv2, c + 1);
+        compute(wa, sa, c);
+        if (c + 1 < chunks) {
+            if (c + 2 < chunks) issue(wa, sa, c + 2);
+            compute(wb, sbv2, c + 1);
+        }
+    }
+}
+
+// Split of K's group pairs over the waves of a workgroup: an exact GPW x waves
+// factorisation when one exists (no zero passes), else 4 pairs per pass.  GPW = 6
+// only fits the 128-VGPR budget (16 waves per workgroup) for M <= 2.
+struct Split {
+    int gpw;
+    int waves;
+};
+
+inline Split choose_split(int gpairs, int mt) {
+    if (mt <= 2 && gpairs % 6 == 0 && gpairs / 6 <= 16) return {6, gpairs / 6};
+    if (gpairs % 4 == 0 && gpairs / 4 <= 16) return {4, gpairs / 4};
+    const int waves = (gpairs + 3) / 4 < 16 ? (gpairs + 3) / 4 : 16;
+    return {4, waves};
+}
+
+constexpr size_t kMaxXLds = 64 * 1024;  // LDS budget for staged x + the -X table
+
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cus[dev] = v;
+    }
+    return cus[dev];
+}
+
+template <int MT>
+hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
+                     bool out_f32, const Layout& l, hipStream_t stream) {
+    const int f32 = out_f32 ? 1 : 0;
+    const size_t xbytes = (size_t)m * l.k * 2;
+    constexpr int GPW = 4;
+    const size_t lds_bytes = (size_t)m * (l.k + GPW * 128) * 2 + (size_t)l.gp * 2 * 16 * 4;
+    if (MT <= 4 && lds_bytes <= kMaxXLds) {
+        // persistent streaming kernel: 4 pairs per chunk, up to 8 waves per workgroup
+        int waves = (l.gp + GPW - 1) / GPW;
+        if (waves > 8) waves = 8;
+        if (waves > l.gp) waves = l.gp;
+        const int capacity = device_cus() * (20 / waves > 0 ? 20 / waves : 1);
+        const int per_wg = (l.nb + capacity - 1) / capacity;
+        const int grid = (l.nb + per_wg - 1) / per_wg;
+        hipLaunchKernelGGL((decode_stream_kernel<MT, GPW>), dim3(grid), dim3(64 * waves), lds_bytes, stream, tiles,
+                           sb, x, y, m, l.n, l.k, l.gp, l.nb, waves, f32);
+        return hipGetLastError();
+    }
+    const Split sp = choose_split(l.gp, MT);
+    const dim3 grid(l.nb), block(64 * sp.waves);
+    if (sp.gpw == 6)
+        hipLaunchKernelGGL((decode_kernel<MT, 6, false>), grid, block, 0, stream, tiles, sb, x, y, m, l.n, l.k, l.gp, sp.waves, f32);
+    else
+        hipLaunchKernelGGL((decode_kernel<MT, 4, false>), grid, block, 0, stream, tiles, sb, x, y, m, l.n, l.k, l.gp, sp.waves, f32);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
+                         bool out_f32, const Layout& l, hipStream_t stream) {
+    const size_t ysz = out_f32 ? 4 : 2;
+    for (int m0 = 0; m0 < m; m0 += 16) {
+        const int mc = (m - m0) < 16 ? (m - m0) : 16;
+        const uint16_t* xs = x + (size_t)m0 * l.k;
+        void* ys = static_cast<char*>(y) + (size_t)m0 * l.n * ysz;
+        hipError_t e;
+        if (mc == 1)
+            e = launch_mt<1>(tiles, sb, xs, ys, mc, out_f32, l, stream);
+        else if (mc == 2)
+            e = launch_mt<2>(tiles, sb, xs, ys, mc, out_f32, l, stream);
+        else if (mc <= 4)
+            e = launch_mt<4>(tiles, sb, xs, ys, mc, out_f32, l, stream);
+        else
+            e = launch_mt<16>(tiles, sb, xs, ys, mc, out_f32, l, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace q4

@@ -1,0 +1,42 @@
+// Host-side launchers of the gfx950 affine-Q4 kernels (internal to libgemma4_qmm).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace q4 {
+
+struct Layout {
+    int n = 0;   // output features
+    int k = 0;   // input features
+    int g = 0;   // groups per row (k / 64)
+    int nb = 0;  // 16-row blocks
+    int gp = 0;  // group pairs (ceil(g / 2))
+    size_t tile_bytes() const { return (size_t)nb * gp * 64 * 16; }
+    size_t sb_bytes() const { return (size_t)nb * gp * 16 * 8; }
+};
+
+inline Layout make_layout(int n, int k) {
+    Layout l;
+    l.n = n;
+    l.k = k;
+    l.g = k / 64;
+    l.nb = (n + 15) / 16;
+    l.gp = (l.g + 1) / 2;
+    return l;
+}
+
+// MLX layout (device) -> tiled layout (device).
+hipError_t launch_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b, uint4* tiles,
+                         uint2* sb, const Layout& l, hipStream_t stream);
+
+// Tiled layout -> fp32 W[N,K] row-major, w = fma(s, q, b).
+hipError_t launch_dequantize(const uint4* tiles, const uint2* sb, float* out, const Layout& l,
+                             hipStream_t stream);
+
+// Decode path, M <= 16 rows per launch (the launcher walks larger M in 16-row slabs).
+hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
+                         bool out_f32, const Layout& l, hipStream_t stream);
+
+}  // namespace q4

@@ -1,0 +1,118 @@
+// Weight-layout kernels: MLX affine layout -> tiled MFMA layout, and the bit-exact
+// fp32 dequantize of the tiled layout (the check that the tiles hold every bit).
+#include "q4_common.h"
+#include "q4_kernels.h"
+
+namespace q4 {
+namespace {
+
+// MLX word (q[i] at bits 4i) -> tiled word (see q4_common.h): pairs (2p, 2p+1) go to
+// bits (4p, 16+4p), then the word is rotated left by 3.
+__device__ __forceinline__ uint32_t tile_word(uint32_t u) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        t |= ((u >> (8 * p)) & 0xFu) << (4 * p);
+        t |= ((u >> (8 * p + 4)) & 0xFu) << (16 + 4 * p);
+    }
+    return (t << 3) | (t >> 29);
+}
+
+__global__ void repack_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
+                              const uint16_t* __restrict__ b, uint4* __restrict__ tiles,
+                              uint2* __restrict__ sb, int n_rows, int k, int groups, int gpairs,
+                              long total) {
+    const long tid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tid >= total) return;
+    const int lane = (int)(tid & 63);
+    const long t = tid >> 6;
+    const int gp = (int)(t % gpairs);
+    const long rb = t / gpairs;
+    const int row = (int)(rb * 16 + (lane & 15));
+    const int kq = lane >> 4;
+    const int words_per_row = k / 8;
+    uint32_t out[4];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        const int g = 2 * gp + gi;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint32_t u = 0;
+            if (row < n_rows && g < groups) u = w[(long)row * words_per_row + 8 * g + 4 * h + kq];
+            out[2 * gi + h] = tile_word(u);
+        }
+    }
+    tiles[tid] = make_uint4(out[0], out[1], out[2], out[3]);
+    if (kq == 0) {
+        uint32_t v[2];
+#pragma unroll
+        for (int gi = 0; gi < 2; ++gi) {
+            const int g = 2 * gp + gi;
+            v[gi] = 0;
+            if (row < n_rows && g < groups) {
+                const long idx = (long)row * groups + g;
+                v[gi] = (uint32_t)s[idx] | ((uint32_t)b[idx] << 16);
+            }
+        }
+        sb[t * 16 + (lane & 15)] = make_uint2(v[0], v[1]);
+    }
+}
+
+__global__ void dequantize_kernel(const uint4* __restrict__ tiles, const uint2* __restrict__ sb,
+                                  float* __restrict__ out, int n_rows, int k, int groups, int gpairs,
+                                  long total) {
+    const long tid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tid >= total) return;
+    const int lane = (int)(tid & 63);
+    const long t = tid >> 6;
+    const int gp = (int)(t % gpairs);
+    const long rb = t / gpairs;
+    const int row = (int)(rb * 16 + (lane & 15));
+    const int kq = lane >> 4;
+    if (row >= n_rows) return;
+    const uint4 wv = tiles[tid];
+    const uint2 sv = sb[t * 16 + (lane & 15)];
+    const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        const int g = 2 * gp + gi;
+        if (g >= groups) continue;
+        const uint32_t sbv = gi ? sv.y : sv.x;
+        const float sc = bf16_lo(sbv);
+        const float bi = bf16_hi(sbv);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t u = words[2 * gi + h];
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(sc, (float)word_nibble(u, i), bi);
+            float4* dst = reinterpret_cast<float4*>(out + (long)row * k + 64 * g + 32 * h + 8 * kq);
+            dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+            dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b, uint4* tiles,
+                         uint2* sb, const Layout& l, hipStream_t stream) {
+    const long total = (long)l.nb * l.gp * 64;
+    const int block = 256;
+    const long grid = (total + block - 1) / block;
+    hipLaunchKernelGGL(repack_kernel, dim3((unsigned)grid), dim3(block), 0, stream, w, s, b, tiles, sb,
+                       l.n, l.k, l.g, l.gp, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequantize(const uint4* tiles, const uint2* sb, float* out, const Layout& l,
+                             hipStream_t stream) {
+    const long total = (long)l.nb * l.gp * 64;
+    const int block = 256;
+    const long grid = (total + block - 1) / block;
+    hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)grid), dim3(block), 0, stream, tiles, sb, out,
+                       l.n, l.k, l.g, l.gp, total);
+    return hipGetLastError();
+}
+
+}  // namespace q4

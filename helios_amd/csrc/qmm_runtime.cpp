@@ -1,0 +1,279 @@
+// C ABI of libgemma4_qmm (include/gemma4_qmm.h): handles, errors, dispatch.
+//
+// Mirrors the reference runtime's conventions (native/gemma4_mlx/src/runtime.cc):
+// status codes, a thread-local last-error buffer (runtime.cc:46, :116-133), magic
+// numbers on handles (runtime.cc:41-45), no exception across the ABI.
+#include "gemma4_qmm.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "q4_kernels.h"
+
+namespace {
+
+constexpr uint64_t kQLinearMagic = 0x47454d3451344c4eULL;  // "GEM4Q4LN"
+thread_local char g_last_error[512] = "";
+
+Gemma4Status fail(Gemma4Status status, const std::string& message) {
+    std::snprintf(g_last_error, sizeof(g_last_error), "%s", message.c_str());
+    return status;
+}
+
+Gemma4Status ok() {
+    g_last_error[0] = '\0';
+    return GEMMA4_OK;
+}
+
+Gemma4Status hip_fail(const char* where, hipError_t e) {
+    return fail(GEMMA4_ERR_RUNTIME, std::string(where) + ": " + hipGetErrorName(e) + " (" +
+                                        hipGetErrorString(e) + ")");
+}
+
+// Restores the caller's current device on scope exit.
+struct DeviceGuard {
+    int saved = -1;
+    bool changed = false;
+    hipError_t enter(int device) {
+        hipError_t e = hipGetDevice(&saved);
+        if (e != hipSuccess) return e;
+        if (saved != device) {
+            e = hipSetDevice(device);
+            changed = (e == hipSuccess);
+        }
+        return e;
+    }
+    ~DeviceGuard() {
+        if (changed) (void)hipSetDevice(saved);
+    }
+};
+
+}  // namespace
+
+struct Gemma4QLinear {
+    uint64_t magic = 0;
+    Gemma4QLinearDesc desc{};
+    q4::Layout layout;
+    int device = 0;
+    uint4* tiles = nullptr;
+    uint2* sb = nullptr;
+};
+
+namespace {
+
+Gemma4Status check_desc(const Gemma4QLinearDesc* desc, const char* fn) {
+    if (desc == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, std::string(fn) + " requires a non-null desc");
+    if (desc->out_features == 0 || desc->in_features == 0)
+        return fail(GEMMA4_ERR_INVALID_ARGUMENT, std::string(fn) + ": out_features and in_features must be > 0");
+    if (desc->bits != 4 || desc->group_size != 64)
+        return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
+                    std::string(fn) + ": only affine bits=4 group_size=64 is supported (got bits=" +
+                        std::to_string(desc->bits) + " group_size=" + std::to_string(desc->group_size) + ")");
+    if (desc->in_features % 64 != 0)
+        return fail(GEMMA4_ERR_INVALID_ARGUMENT, std::string(fn) + ": in_features must be a multiple of 64");
+    if (desc->out_features > (1u << 30) || desc->in_features > (1u << 24))
+        return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, std::string(fn) + ": shape exceeds the supported range");
+    return GEMMA4_OK;
+}
+
+void release(Gemma4QLinear* h) {
+    if (h->tiles) (void)hipFree(h->tiles);
+    if (h->sb) (void)hipFree(h->sb);
+    h->tiles = nullptr;
+    h->sb = nullptr;
+    h->magic = 0;
+}
+
+bool valid_handle(const Gemma4QLinear* h) { return h != nullptr && h->magic == kQLinearMagic; }
+
+// Allocates the tiled buffers and repacks from MLX-layout device arrays.
+Gemma4Status build_handle(const Gemma4QLinearDesc* desc, const uint32_t* w_dev, const uint16_t* s_dev,
+                          const uint16_t* b_dev, hipStream_t stream, Gemma4QLinear** out) {
+    Gemma4QLinear* h = new (std::nothrow) Gemma4QLinear();
+    if (h == nullptr) return fail(GEMMA4_ERR_MEMORY_GUARD, "gemma4_qlinear: host allocation failed");
+    h->desc = *desc;
+    h->layout = q4::make_layout((int)desc->out_features, (int)desc->in_features);
+    hipError_t e = hipGetDevice(&h->device);
+    if (e != hipSuccess) {
+        delete h;
+        return hip_fail("hipGetDevice", e);
+    }
+    e = hipMalloc(&h->tiles, h->layout.tile_bytes());
+    if (e == hipSuccess) e = hipMalloc(&h->sb, h->layout.sb_bytes());
+    if (e != hipSuccess) {
+        release(h);
+        delete h;
+        return fail(GEMMA4_ERR_MEMORY_GUARD, std::string("gemma4_qlinear: device allocation failed: ") +
+                                                 hipGetErrorString(e));
+    }
+    e = q4::launch_repack(w_dev, s_dev, b_dev, h->tiles, h->sb, h->layout, stream);
+    if (e != hipSuccess) {
+        release(h);
+        delete h;
+        return hip_fail("repack launch", e);
+    }
+    h->magic = kQLinearMagic;
+    *out = h;
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+Gemma4Status gemma4_qmm_runtime_version(Gemma4QmmVersionInfo* out) {
+    if (out == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qmm_runtime_version requires a non-null out pointer");
+    out->abi_version = GEMMA4_QMM_ABI_VERSION;
+    out->backend_name = "gemma4_qmm";
+    out->backend_version = "gfx950-hip-affine-q4";
+    return ok();
+}
+
+Gemma4Status gemma4_qmm_get_last_error(char* buffer, size_t buffer_len) {
+    if (buffer == nullptr || buffer_len == 0)
+        return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qmm_get_last_error requires a writable buffer");
+    std::snprintf(buffer, buffer_len, "%s", g_last_error);
+    return GEMMA4_OK;
+}
+
+Gemma4Status gemma4_qlinear_create(const Gemma4QLinearDesc* desc, const uint32_t* weight,
+                                   const uint16_t* scales, const uint16_t* biases, Gemma4QLinear** out) {
+    try {
+        if (out == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_create requires a non-null out pointer");
+        *out = nullptr;
+        Gemma4Status st = check_desc(desc, "gemma4_qlinear_create");
+        if (st != GEMMA4_OK) return st;
+        if (weight == nullptr || scales == nullptr || biases == nullptr)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_create requires non-null weight, scales and biases");
+        const size_t n = desc->out_features, k = desc->in_features;
+        const size_t wbytes = n * k / 2, sbytes = n * (k / 64) * 2;
+        void* staging = nullptr;
+        hipError_t e = hipMalloc(&staging, wbytes + 2 * sbytes);
+        if (e != hipSuccess)
+            return fail(GEMMA4_ERR_MEMORY_GUARD, std::string("gemma4_qlinear_create: staging allocation failed: ") +
+                                                     hipGetErrorString(e));
+        char* base = static_cast<char*>(staging);
+        e = hipMemcpy(base, weight, wbytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(base + wbytes, scales, sbytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(base + wbytes + sbytes, biases, sbytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(staging);
+            return hip_fail("gemma4_qlinear_create: upload", e);
+        }
+        st = build_handle(desc, reinterpret_cast<const uint32_t*>(base),
+                          reinterpret_cast<const uint16_t*>(base + wbytes),
+                          reinterpret_cast<const uint16_t*>(base + wbytes + sbytes), nullptr, out);
+        e = hipStreamSynchronize(nullptr);
+        (void)hipFree(staging);
+        if (st == GEMMA4_OK && e != hipSuccess) {
+            gemma4_qlinear_free(*out);
+            *out = nullptr;
+            return hip_fail("gemma4_qlinear_create: repack", e);
+        }
+        return st;
+    } catch (...) {
+        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_create: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qlinear_create_device(const Gemma4QLinearDesc* desc, const uint32_t* weight_dev,
+                                          const uint16_t* scales_dev, const uint16_t* biases_dev, void* stream,
+                                          Gemma4QLinear** out) {
+    try {
+        if (out == nullptr)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_create_device requires a non-null out pointer");
+        *out = nullptr;
+        Gemma4Status st = check_desc(desc, "gemma4_qlinear_create_device");
+        if (st != GEMMA4_OK) return st;
+        if (weight_dev == nullptr || scales_dev == nullptr || biases_dev == nullptr)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT,
+                        "gemma4_qlinear_create_device requires non-null weight, scales and biases");
+        hipStream_t st_h = static_cast<hipStream_t>(stream);
+        st = build_handle(desc, weight_dev, scales_dev, biases_dev, st_h, out);
+        if (st != GEMMA4_OK) return st;
+        const hipError_t e = hipStreamSynchronize(st_h);
+        if (e != hipSuccess) {
+            gemma4_qlinear_free(*out);
+            *out = nullptr;
+            return hip_fail("gemma4_qlinear_create_device: repack", e);
+        }
+        return ok();
+    } catch (...) {
+        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_create_device: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qlinear_free(Gemma4QLinear* linear) {
+    if (linear == nullptr) return ok();
+    if (!valid_handle(linear)) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_free received an invalid handle");
+    DeviceGuard guard;
+    (void)guard.enter(linear->device);
+    release(linear);
+    delete linear;
+    return ok();
+}
+
+Gemma4Status gemma4_qlinear_info(const Gemma4QLinear* linear, Gemma4QLinearInfo* out) {
+    if (out == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_info requires a non-null out pointer");
+    if (!valid_handle(linear)) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_info received an invalid handle");
+    std::memset(out, 0, sizeof(*out));
+    out->out_features = linear->desc.out_features;
+    out->in_features = linear->desc.in_features;
+    out->bits = linear->desc.bits;
+    out->group_size = linear->desc.group_size;
+    out->device_bytes = linear->layout.tile_bytes() + linear->layout.sb_bytes();
+    out->device = linear->device;
+    return ok();
+}
+
+Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
+                                    uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype) {
+    try {
+        if (!valid_handle(linear))
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_forward received an invalid handle");
+        if (y_dtype != GEMMA4_QMM_BF16 && y_dtype != GEMMA4_QMM_F32)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_forward: y_dtype must be BF16 or F32");
+        if (rows == 0) return ok();
+        if (x_dev == nullptr || y_dev == nullptr)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_forward requires non-null x and y");
+        if ((reinterpret_cast<uintptr_t>(x_dev) & 15u) != 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_forward: x must be 16-byte aligned");
+        const uintptr_t yalign = y_dtype == GEMMA4_QMM_F32 ? 3u : 1u;
+        if ((reinterpret_cast<uintptr_t>(y_dev) & yalign) != 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_forward: y is misaligned for its dtype");
+        if (rows > (1u << 24)) return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, "gemma4_qlinear_forward: rows exceeds 2^24");
+        DeviceGuard guard;
+        hipError_t e = guard.enter(linear->device);
+        if (e != hipSuccess) return hip_fail("gemma4_qlinear_forward: hipSetDevice", e);
+        e = q4::launch_decode(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, y_dtype == GEMMA4_QMM_F32,
+                              linear->layout, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_fail("gemma4_qlinear_forward: launch", e);
+        return ok();
+    } catch (...) {
+        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qlinear_dequantize(const Gemma4QLinear* linear, void* stream, float* w_dev) {
+    try {
+        if (!valid_handle(linear))
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_dequantize received an invalid handle");
+        if (w_dev == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_dequantize requires a non-null output");
+        if ((reinterpret_cast<uintptr_t>(w_dev) & 15u) != 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_dequantize: output must be 16-byte aligned");
+        DeviceGuard guard;
+        hipError_t e = guard.enter(linear->device);
+        if (e != hipSuccess) return hip_fail("gemma4_qlinear_dequantize: hipSetDevice", e);
+        e = q4::launch_dequantize(linear->tiles, linear->sb, w_dev, linear->layout, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_fail("gemma4_qlinear_dequantize: launch", e);
+        return ok();
+    } catch (...) {
+        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_dequantize: unexpected native exception");
+    }
+}
+
+}  // extern "C"

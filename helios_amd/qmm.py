@@ -1,0 +1,269 @@
+"""Host-side mirror of the reference's quantized-linear interface over libgemma4_qmm.
+
+The reference calls ``mlx::core::quantized_matmul(x, w, scales, biases,
+transpose=true, group_size, bits, "affine")`` for every projection
+(``native/gemma4_mlx/src/native_model.cc:349-362``, lm_head ``:1782-1795``) and
+``mlx::core::dequantize`` for the embedding (``:364-376``).  This module offers
+the same operations with the same argument meaning on device tensors:
+
+* :func:`quantized_matmul` / :func:`dequantize` — one-shot, MLX-style signatures;
+* :class:`QuantizedLinear` — the resident-weight form the call sites actually
+  need (weights loaded once, ``forward`` per step), one C-ABI handle each.
+
+Errors surface as :class:`Gemma4Error` carrying the C status and the native
+last-error text, as the reference's Rust wrapper does with ``check()``
+(``crates/gemma4d-ffi/src/lib.rs:1409-1433``).  Torch supplies device memory and
+the current stream only; all arithmetic runs in the HIP kernels.  There is no
+fallback: without the built library every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+
+import numpy as np
+
+from . import build as _build
+
+LIB_PATH = _build.LIB_PATH
+
+
+class Status(enum.IntEnum):
+    """Gemma4Status (native/gemma4_mlx/include/gemma4_mlx.h:12-21)."""
+
+    OK = 0
+    INVALID_ARGUMENT = 1
+    UNSUPPORTED_CONFIG = 2
+    MODEL_LOAD = 3
+    RUNTIME = 4
+    MEMORY_GUARD = 5
+    CACHE = 6
+    ADAPTER = 7
+
+
+class Gemma4Error(RuntimeError):
+    def __init__(self, status: int, message: str):
+        self.status = Status(status)
+        self.message = message
+        super().__init__(f"{self.status.name}: {message}")
+
+
+class _Desc(ctypes.Structure):
+    _fields_ = [("out_features", ctypes.c_uint32), ("in_features", ctypes.c_uint32),
+                ("bits", ctypes.c_uint32), ("group_size", ctypes.c_uint32)]
+
+
+class _Info(ctypes.Structure):
+    _fields_ = [("out_features", ctypes.c_uint32), ("in_features", ctypes.c_uint32),
+                ("bits", ctypes.c_uint32), ("group_size", ctypes.c_uint32),
+                ("device_bytes", ctypes.c_uint64), ("device", ctypes.c_int32),
+                ("reserved", ctypes.c_uint32)]
+
+
+class _Version(ctypes.Structure):
+    _fields_ = [("abi_version", ctypes.c_uint32), ("backend_name", ctypes.c_char_p),
+                ("backend_version", ctypes.c_char_p)]
+
+
+DTYPE_BF16 = 0
+DTYPE_F32 = 1
+
+_lib = None
+
+
+def load_library(path: str | None = None):
+    """Loads libgemma4_qmm.so (built by ``python -m helios_amd.build``)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    path = path or LIB_PATH
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with `python -m helios_amd.build`")
+    lib = ctypes.CDLL(path)
+    vp = ctypes.c_void_p
+    st = ctypes.c_int
+    sig = {
+        "gemma4_qmm_runtime_version": [ctypes.POINTER(_Version)],
+        "gemma4_qmm_get_last_error": [ctypes.c_char_p, ctypes.c_size_t],
+        "gemma4_qlinear_create": [ctypes.POINTER(_Desc), vp, vp, vp, ctypes.POINTER(vp)],
+        "gemma4_qlinear_create_device": [ctypes.POINTER(_Desc), vp, vp, vp, vp, ctypes.POINTER(vp)],
+        "gemma4_qlinear_free": [vp],
+        "gemma4_qlinear_info": [vp, ctypes.POINTER(_Info)],
+        "gemma4_qlinear_forward": [vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int],
+        "gemma4_qlinear_dequantize": [vp, vp, vp],
+    }
+    for name, args in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = st
+    if path == LIB_PATH:
+        _lib = lib
+    return lib
+
+
+def last_error(lib=None) -> str:
+    lib = lib or load_library()
+    buf = ctypes.create_string_buffer(512)
+    if lib.gemma4_qmm_get_last_error(buf, len(buf)) != 0:
+        return "native error unavailable"
+    return buf.value.decode("utf-8", "replace")
+
+
+def check(status: int, lib=None) -> None:
+    if status != Status.OK:
+        raise Gemma4Error(status, last_error(lib))
+
+
+def runtime_version() -> dict:
+    lib = load_library()
+    v = _Version()
+    check(lib.gemma4_qmm_runtime_version(ctypes.byref(v)), lib)
+    return {"abi_version": v.abi_version, "backend_name": v.backend_name.decode(),
+            "backend_version": v.backend_version.decode()}
+
+
+def _stream_ptr(stream):
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _dev_ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _check_spec(group_size: int, bits: int, mode: str, transpose: bool = True) -> None:
+    if mode != "affine":
+        raise Gemma4Error(Status.UNSUPPORTED_CONFIG, f"mode {mode!r} is not supported (affine only)")
+    if not transpose:
+        raise Gemma4Error(Status.UNSUPPORTED_CONFIG, "transpose=False is not supported (the call sites use y = x . W^T)")
+    if bits != 4 or group_size != 64:
+        raise Gemma4Error(Status.UNSUPPORTED_CONFIG,
+                          f"only bits=4 group_size=64 is supported (got bits={bits} group_size={group_size})")
+
+
+class QuantizedLinear:
+    """One projection's weight triple resident on the GPU (a ``Gemma4QLinear`` handle).
+
+    ``weight`` uint32/int32 [N, K/8], ``scales``/``biases`` bf16 [N, K/64] in MLX
+    layout — torch tensors on the current CUDA device, or numpy arrays on the host
+    (``uint32`` and ``uint16`` bit patterns)."""
+
+    def __init__(self, weight, scales, biases, group_size: int = 64, bits: int = 4, stream=None):
+        _check_spec(group_size, bits, "affine")
+        self._lib = load_library()
+        self._handle = ctypes.c_void_p()
+        n = int(weight.shape[0])
+        k = int(weight.shape[1]) * 32 // bits
+        desc = _Desc(n, k, bits, group_size)
+        if isinstance(weight, np.ndarray):
+            w = np.ascontiguousarray(weight, dtype=np.uint32)
+            s = np.ascontiguousarray(scales, dtype=np.uint16)
+            b = np.ascontiguousarray(biases, dtype=np.uint16)
+            if s.shape != (n, k // group_size) or b.shape != s.shape:
+                raise Gemma4Error(Status.INVALID_ARGUMENT, f"scales/biases must be [{n}, {k // group_size}]")
+            status = self._lib.gemma4_qlinear_create(ctypes.byref(desc), w.ctypes.data_as(ctypes.c_void_p),
+                                                     s.ctypes.data_as(ctypes.c_void_p),
+                                                     b.ctypes.data_as(ctypes.c_void_p),
+                                                     ctypes.byref(self._handle))
+        else:
+            import torch
+
+            w = weight.contiguous()
+            s = scales.contiguous()
+            b = biases.contiguous()
+            if w.dtype not in (torch.int32, torch.uint32) or s.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+                raise Gemma4Error(Status.INVALID_ARGUMENT, "weight must be int32/uint32 and scales/biases bfloat16")
+            if tuple(s.shape) != (n, k // group_size) or tuple(b.shape) != tuple(s.shape):
+                raise Gemma4Error(Status.INVALID_ARGUMENT, f"scales/biases must be [{n}, {k // group_size}]")
+            if not (w.is_cuda and s.is_cuda and b.is_cuda):
+                raise Gemma4Error(Status.INVALID_ARGUMENT, "device tensors must be on a CUDA (HIP) device")
+            with torch.cuda.device(w.device):
+                status = self._lib.gemma4_qlinear_create_device(
+                    ctypes.byref(desc), _dev_ptr(w), _dev_ptr(s), _dev_ptr(b), _stream_ptr(stream),
+                    ctypes.byref(self._handle))
+        check(status, self._lib)
+        self.out_features = n
+        self.in_features = k
+        self.group_size = group_size
+        self.bits = bits
+
+    def info(self) -> dict:
+        info = _Info()
+        check(self._lib.gemma4_qlinear_info(self._handle, ctypes.byref(info)), self._lib)
+        return {f: getattr(info, f) for f, _ in _Info._fields_ if f != "reserved"}
+
+    def forward(self, x, out=None, out_dtype=None, stream=None):
+        """y = x . W^T for x bf16 [..., K] on the device; returns [..., N]."""
+        import torch
+
+        if out_dtype is None:
+            out_dtype = out.dtype if out is not None else torch.bfloat16
+        if out_dtype not in (torch.bfloat16, torch.float32):
+            raise Gemma4Error(Status.INVALID_ARGUMENT, "out_dtype must be bfloat16 or float32")
+        if x.dtype != torch.bfloat16:
+            raise Gemma4Error(Status.INVALID_ARGUMENT, "x must be bfloat16")
+        if x.shape[-1] != self.in_features:
+            raise Gemma4Error(Status.INVALID_ARGUMENT, f"x last dim {x.shape[-1]} != in_features {self.in_features}")
+        lead = tuple(x.shape[:-1])
+        x2 = x.reshape(-1, self.in_features).contiguous()
+        rows = x2.shape[0]
+        if out is None:
+            out = torch.empty(lead + (self.out_features,), dtype=out_dtype, device=x.device)
+        elif out.dtype != out_dtype or tuple(out.shape) != lead + (self.out_features,) or not out.is_contiguous():
+            raise Gemma4Error(Status.INVALID_ARGUMENT, "out has the wrong dtype, shape or layout")
+        code = DTYPE_F32 if out_dtype == torch.float32 else DTYPE_BF16
+        check(self._lib.gemma4_qlinear_forward(self._handle, _stream_ptr(stream), _dev_ptr(x2), rows,
+                                               _dev_ptr(out), code), self._lib)
+        return out
+
+    __call__ = forward
+
+    def forward_raw(self, x_ptr: int, rows: int, y_ptr: int, f32: bool = False, stream_ptr: int = 0) -> None:
+        """Direct C-ABI call on raw device pointers (benchmark loops)."""
+        check(self._lib.gemma4_qlinear_forward(self._handle, ctypes.c_void_p(stream_ptr), ctypes.c_void_p(x_ptr),
+                                               rows, ctypes.c_void_p(y_ptr), DTYPE_F32 if f32 else DTYPE_BF16),
+              self._lib)
+
+    def dequantize(self, stream=None):
+        import torch
+
+        out = torch.empty((self.out_features, self.in_features), dtype=torch.float32, device="cuda")
+        check(self._lib.gemma4_qlinear_dequantize(self._handle, _stream_ptr(stream), _dev_ptr(out)), self._lib)
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None) is not None and self._handle.value:
+            check(self._lib.gemma4_qlinear_free(self._handle), self._lib)
+            self._handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def quantized_matmul(x, w, scales, biases, transpose: bool = True, group_size: int = 64, bits: int = 4,
+                     mode: str = "affine", out_dtype=None):
+    """MLX ``quantized_matmul`` with MLX's argument meaning; returns x's dtype by default."""
+    _check_spec(group_size, bits, mode, transpose)
+    lin = QuantizedLinear(w, scales, biases, group_size, bits)
+    try:
+        return lin.forward(x, out_dtype=out_dtype)
+    finally:
+        lin.close()
+
+
+def dequantize(w, scales, biases, group_size: int = 64, bits: int = 4, mode: str = "affine"):
+    """MLX ``dequantize(..., dtype=float32)``: fp32 [N, K] with w = s*q + b."""
+    _check_spec(group_size, bits, mode)
+    lin = QuantizedLinear(w, scales, biases, group_size, bits)
+    try:
+        return lin.dequantize()
+    finally:
+        lin.close()

@@ -1,0 +1,144 @@
+/*
+ * gemma4_qmm — MI355X (gfx950) affine 4-bit quantized linear layers behind a C ABI.
+ *
+ * Drop-in for the reference's quantized-linear call sites.  The reference issues
+ * every projection as
+ *     mlx::core::quantized_matmul(x, W, scales, biases, transpose=true,
+ *                                 group_size, bits, "affine")
+ * at native/gemma4_mlx/src/native_model.cc:349-362 (q/k/v/o and gate/up/down,
+ * call sites :802,813,821,892,934,939,949 prefill, :993,1005,1009,1128,1318-1321
+ * decode, :1158,1167,1171,1281,1366-1369 block/verify) and the lm_head at
+ * native_model.cc:1782-1795.  Those weights are loaded once and stay resident
+ * (native_model.cc:3550-3566), so the boundary here is a handle that owns the
+ * device copy of one projection's weight triple, plus a forward call per step.
+ *
+ * Conventions follow the reference C ABI (native/gemma4_mlx/include/gemma4_mlx.h,
+ * native/gemma4_mlx/src/runtime.cc):
+ *   - every entry point returns a Gemma4Status (gemma4_mlx.h:12-21);
+ *   - failures store a message in a thread-local buffer read back with
+ *     gemma4_qmm_get_last_error (runtime.cc:46, :116-133, :816-823);
+ *   - handles are opaque, carry a magic number checked on entry (runtime.cc:41-45),
+ *     and have an explicit free (runtime.cc:900-912);
+ *   - no C++ exception crosses the ABI (native_model.cc:3582-3588);
+ *   - pointers are null-checked and sizes validated before use
+ *     (spec/03-rust-mlx-ffi-contract.md "Safety checklist").
+ *
+ * Data formats (the MLX affine format, model_manifest.cc:101-162,
+ * native_model.cc:281-287):
+ *   weight  uint32 [N, K/8]  element k of a row is nibble k%8 of word k/8, lowest nibble first
+ *   scales  bf16   [N, K/64] (raw bit patterns as uint16)
+ *   biases  bf16   [N, K/64]
+ *   w[n,k] = scales[n,k/64] * q[n,k] + biases[n,k/64]
+ *   x       bf16   [M, K] row-major, device memory, 16-byte aligned
+ *   y       bf16 or fp32 [M, N] row-major, device memory;  y = x . W^T
+ * Only bits = 4 with group_size = 64 is accepted (the configuration every
+ * projection of the reference's Gemma 4 12B artifact uses, model_manifest.cc:148).
+ *
+ * Streams are hipStream_t values passed as void* (NULL = the null stream).  All
+ * device work is asynchronous on that stream.  A handle is immutable after
+ * create, so forward/dequantize may run concurrently on several streams and
+ * threads; create and free must not overlap use.
+ */
+#ifndef GEMMA4_QMM_H
+#define GEMMA4_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GEMMA4_QMM_ABI_VERSION 1u
+
+/* Same codes as the reference status enum (gemma4_mlx.h:12-21); defined here only
+ * when that header has not been included first. */
+#ifndef GEMMA4_MLX_H
+typedef enum Gemma4Status {
+    GEMMA4_OK = 0,
+    GEMMA4_ERR_INVALID_ARGUMENT = 1,
+    GEMMA4_ERR_UNSUPPORTED_CONFIG = 2,
+    GEMMA4_ERR_MODEL_LOAD = 3,
+    GEMMA4_ERR_RUNTIME = 4,
+    GEMMA4_ERR_MEMORY_GUARD = 5,
+    GEMMA4_ERR_CACHE = 6,
+    GEMMA4_ERR_ADAPTER = 7
+} Gemma4Status;
+#endif
+
+typedef struct Gemma4QLinear Gemma4QLinear;
+
+typedef enum Gemma4QmmDtype {
+    GEMMA4_QMM_BF16 = 0,
+    GEMMA4_QMM_F32 = 1
+} Gemma4QmmDtype;
+
+typedef struct Gemma4QmmVersionInfo {
+    uint32_t abi_version;
+    const char* backend_name;
+    const char* backend_version;
+} Gemma4QmmVersionInfo;
+
+/* Shape and quantization of one projection (the reference's QuantizationSpec,
+ * model_manifest.h:10-13, plus the weight's logical shape). */
+typedef struct Gemma4QLinearDesc {
+    uint32_t out_features; /* N */
+    uint32_t in_features;  /* K, a multiple of group_size */
+    uint32_t bits;         /* 4 */
+    uint32_t group_size;   /* 64 */
+} Gemma4QLinearDesc;
+
+typedef struct Gemma4QLinearInfo {
+    uint32_t out_features;
+    uint32_t in_features;
+    uint32_t bits;
+    uint32_t group_size;
+    uint64_t device_bytes; /* resident bytes of the tiled weight triple */
+    int32_t device;        /* HIP device ordinal that holds it */
+    uint32_t reserved;
+} Gemma4QLinearInfo;
+
+/* Replaces gemma4_runtime_version (runtime.cc:805-814) for this library. */
+Gemma4Status gemma4_qmm_runtime_version(Gemma4QmmVersionInfo* out);
+
+/* Replaces gemma4_get_last_error (runtime.cc:816-823): copies this thread's last
+ * error message (empty after a success) into buffer, NUL-terminated. */
+Gemma4Status gemma4_qmm_get_last_error(char* buffer, size_t buffer_len);
+
+/* Load one projection's weight triple from HOST memory in MLX layout onto the
+ * current HIP device (the per-prefix tensors the reference keeps in Impl::tensors,
+ * native_model.cc:84-104, :3550-3566).  The host arrays may be freed on return. */
+Gemma4Status gemma4_qlinear_create(const Gemma4QLinearDesc* desc, const uint32_t* weight,
+                                   const uint16_t* scales, const uint16_t* biases,
+                                   Gemma4QLinear** out);
+
+/* Same, from DEVICE memory in MLX layout on the current device (weights already
+ * uploaded by the caller).  The caller's buffers are read by a repack kernel on
+ * `stream`; the call waits for that stream, so they may be freed on return and
+ * the handle is usable on any stream. */
+Gemma4Status gemma4_qlinear_create_device(const Gemma4QLinearDesc* desc, const uint32_t* weight_dev,
+                                          const uint16_t* scales_dev, const uint16_t* biases_dev,
+                                          void* stream, Gemma4QLinear** out);
+
+/* Releases the device copy.  NULL is accepted (no-op), as for the reference frees. */
+Gemma4Status gemma4_qlinear_free(Gemma4QLinear* linear);
+
+Gemma4Status gemma4_qlinear_info(const Gemma4QLinear* linear, Gemma4QLinearInfo* out);
+
+/* y[M,N] = x[M,K] . W^T — replaces quantized_linear (native_model.cc:349-362) and the
+ * lm_head product (native_model.cc:1782-1795).  y_dtype BF16 is the model dtype;
+ * F32 is the GEMMA4D_NATIVE_FORCE_FLOAT32 output (model_dtype, native_model.cc:330-340).
+ * Accumulation is fp32.  rows == 0 is a no-op. */
+Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
+                                    uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype);
+
+/* Writes the fp32 dequantized weight W[N,K] = s*q + b (row-major) to w_dev —
+ * mlx::core::dequantize (native_model.cc:364-376) with a float32 result.  Bit-exact:
+ * the product s*q is exact in fp32, so the value is unique. */
+Gemma4Status gemma4_qlinear_dequantize(const Gemma4QLinear* linear, void* stream, float* w_dev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GEMMA4_QMM_H */

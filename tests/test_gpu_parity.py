@@ -1,0 +1,215 @@
+"""GPU parity: the gfx950 HIP path, called through the C ABI, against the CPU oracle.
+
+Bars (written here, applied in every test below):
+  * dequantize: bit-exact fp32 (w = s*q + b is unique in fp32);
+  * fp32 output: max |y - y_exact| <= 2e-3 * RMS(y_exact);
+  * bf16 output: max |y - y_exact| <= 1e-2 * RMS(y_exact) + ulp_bf16(y_exact)/2
+    (the half ulp is the rounding any bf16 output makes);
+  where y_exact is the oracle's float64 accumulation of exact products.
+The kernel's own error is far below these bars (fp32 accumulation of exact
+products); the tests also report the measured ratio.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import affine as A
+from oracle import c_oracle as C
+
+pytestmark = pytest.mark.gpu
+
+BF16_REL = 1e-2
+F32_REL = 2e-3
+
+# (N, K) of the reference's projections at the benchmark configurations
+PROJ = {
+    "q_proj": (4096, 3840),
+    "k_proj": (2048, 3840),
+    "v_proj": (2048, 3840),
+    "o_proj": (3840, 4096),
+    "gate_proj": (15360, 3840),
+    "up_proj": (15360, 3840),
+    "down_proj": (3840, 15360),
+}
+
+
+def dev_triple(wq, s, b):
+    import torch
+
+    return (torch.from_numpy(np.ascontiguousarray(wq).view(np.int32)).cuda(),
+            torch.from_numpy(np.ascontiguousarray(s).view(np.int16)).view(torch.bfloat16).cuda(),
+            torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(torch.bfloat16).cuda())
+
+
+def dev_x(x_bits):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x_bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def host_bits(t):
+    import torch
+
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def random_triple(n, k, seed, std=0.02):
+    rng = np.random.default_rng(seed)
+    w = A.round_to_bf16((rng.standard_normal((n, k)) * std).astype(np.float32))
+    return C.quantize(w)
+
+
+def assert_close(y_dev, y_exact, what=""):
+    import torch
+
+    if y_dev.dtype == torch.bfloat16:
+        ok, worst = A.check_bf16_output(host_bits(y_dev), y_exact, BF16_REL)
+    else:
+        ok, worst = A.check_f32_output(host_bits(y_dev), y_exact, F32_REL)
+    assert ok, f"{what}: worst error / RMS = {worst:.3e}"
+    return worst
+
+
+@pytest.mark.parametrize("n,k", [(16, 64), (48, 128), (40, 192), (33, 640), (4096, 3840)])
+def test_dequantize_bit_exact(gpu_lib, n, k):
+    wq, s, b = random_triple(n, k, seed=n * 7 + k)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    got = lin.dequantize().cpu().numpy()
+    want = C.dequantize(wq, s, b)
+    assert got.shape == (n, k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    lin.close()
+
+
+def test_dequantize_host_create_edge_groups(gpu_lib):
+    """Host-pointer create path, with negative scales, eps scales, zero groups and
+    a group spanning every code."""
+    k = 256
+    w = np.zeros((20, k), np.float32)
+    w[0] = np.arange(k) / 4.0
+    w[1] = -np.arange(k) / 4.0
+    w[2] = 0.5
+    w[3, :64] = 1e-6 * np.arange(64)
+    w[4] = np.where(np.arange(k) % 2 == 0, 3.0, -5.0)
+    rng = np.random.default_rng(3)
+    w[5:] = rng.standard_normal((15, k)) * 0.05
+    wq, s, b = C.quantize(A.round_to_bf16(w))
+    lin = gpu_lib.QuantizedLinear(wq, s, b)  # numpy -> gemma4_qlinear_create
+    got = lin.dequantize().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), C.dequantize(wq, s, b).view(np.uint32))
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 12, 16, 17, 40])
+@pytest.mark.parametrize("f32", [False, True])
+def test_forward_small_shapes(gpu_lib, m, f32):
+    import torch
+
+    n, k = 40, 384  # N not a multiple of 16, 6 groups
+    wq, s, b = random_triple(n, k, seed=100 + m)
+    x = A.make_activations(m, k, seed=200 + m, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    y = lin.forward(dev_x(x), out_dtype=torch.float32 if f32 else torch.bfloat16)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (m, n)
+    assert_close(y, C.qmm_f64(x, wq, s, b), f"m={m}")
+
+
+def test_forward_odd_group_count_and_3d_input(gpu_lib):
+    import torch
+
+    n, k = 64, 320  # 5 groups: the last group pair is half padding
+    wq, s, b = random_triple(n, k, seed=7)
+    x = A.make_activations(6, k, seed=8)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    y = lin.forward(dev_x(x).reshape(1, 6, k), out_dtype=torch.float32)
+    assert tuple(y.shape) == (1, 6, n)
+    assert_close(y.reshape(6, n), C.qmm_f64(x, wq, s, b))
+
+
+@pytest.mark.parametrize("proj", sorted(PROJ))
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_forward_decode_projections(gpu_lib, proj, m):
+    """Config shapes at full size: decoder projections at decode batch M."""
+    import torch
+
+    n, k = PROJ[proj]
+    wq, s, b = A.make_weights(n, k, seed=20260630 + 1000 + sorted(PROJ).index(proj))
+    x = A.make_activations(m, k, seed=777 + m)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    xd = dev_x(x)
+    y_bf = lin.forward(xd)
+    y_f32 = lin.forward(xd, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    y_exact = C.qmm_f64(x, wq, s, b)
+    assert_close(y_bf, y_exact, f"{proj} m={m} bf16")
+    worst = assert_close(y_f32, y_exact, f"{proj} m={m} f32")
+    assert worst < 1e-4  # exact products + fp32 accumulation: far inside the bar
+    lin.close()
+
+
+def test_lm_head_decode(gpu_lib):
+    import torch
+
+    n, k = 262144, 3840
+    wq, s, b = A.make_weights(n, k, seed=20260630 + 3000)
+    x = A.make_activations(1, k, seed=31)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    y = lin.forward(dev_x(x))
+    torch.cuda.synchronize()
+    assert_close(y, C.qmm_f64(x, wq, s, b), "lm_head m=1")
+    lin.close()
+
+
+def test_host_and_device_create_agree_and_properties(gpu_lib):
+    """Same bytes through both create paths give identical outputs; linearity in x
+    and zero input hold at the gate_proj size."""
+    import torch
+
+    n, k = PROJ["gate_proj"]
+    wq, s, b = A.make_weights(n, k, seed=5)
+    lin_h = gpu_lib.QuantizedLinear(wq, s, b)
+    lin_d = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    x1 = dev_x(A.make_activations(4, k, seed=1))
+    x2 = dev_x(A.make_activations(4, k, seed=2))
+    ya = lin_h.forward(x1, out_dtype=torch.float32)
+    yb = lin_d.forward(x1, out_dtype=torch.float32)
+    assert torch.equal(ya, yb)
+    # linearity: y(x1) + y(x2) vs y(x1 + x2) (x1 + x2 rounded to bf16 -> compare to oracle)
+    x12 = (x1.float() + x2.float()).bfloat16()
+    y12 = lin_d.forward(x12, out_dtype=torch.float32)
+    y2 = lin_d.forward(x2, out_dtype=torch.float32)
+    resid = (y12 - ya - y2).abs().max().item()
+    rms = y12.pow(2).mean().sqrt().item()
+    assert resid <= 2e-2 * rms  # bf16 rounding of x1 + x2 dominates
+    z = lin_d.forward(torch.zeros_like(x1), out_dtype=torch.float32)
+    assert torch.count_nonzero(z).item() == 0
+    # deterministic: same call twice gives identical bits
+    assert torch.equal(lin_d.forward(x1), lin_d.forward(x1))
+
+
+def test_forward_rejects_misaligned_x(gpu_lib):
+    import torch
+
+    wq, s, b = random_triple(16, 128, seed=9)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    buf = torch.zeros(2 * 128 + 8, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(gpu_lib.Gemma4Error) as e:
+        lin.forward_raw(buf.data_ptr() + 2, 1, buf.data_ptr())
+    assert e.value.status == gpu_lib.Status.INVALID_ARGUMENT and "aligned" in e.value.message
+
+
+@pytest.mark.parametrize("m", [1, 3, 4])
+def test_forward_many_row_blocks_per_workgroup(gpu_lib, m):
+    """Tall, narrow weights: far more 16-row blocks than resident workgroups, so the
+    persistent decode path walks many row blocks per workgroup."""
+    import torch
+
+    n, k = 131072 + 48, 128
+    wq, s, b = random_triple(n, k, seed=41 + m)
+    x = A.make_activations(m, k, seed=42 + m, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    y = lin.forward(dev_x(x), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close(y, C.qmm_f64(x, wq, s, b), f"tall m={m}")

@@ -169,9 +169,10 @@ __global__ __launch_bounds__(1024) void decode_kernel(
 // one is multiplied.  Per workgroup, once:
 //   * x[M][K] is copied to LDS, each row zero-padded by GPW pairs so that operand
 //     reads need no bounds tests (zero tiles past a wave's range meet finite x);
-//   * -X_g (the group sums of x, negated) is computed with two MFMAs per group and
-//     kept in LDS in accumulator layout, so each row block needs only the two
-//     products of the group, seeded from that table.
+//   * -X_g (the group sums of x, negated) is summed while x is copied and kept in
+//     LDS in accumulator layout, so each row block needs only the two products of
+//     the group, seeded from that table.  Table rows >= M are never written: they
+//     only reach accumulator rows that are never stored.
 // Per row block the waves meet once in LDS (ping-pong buffers, one barrier).
 template <int MT, int GPW>
 __global__ __launch_bounds__(512) void decode_stream_kernel(
@@ -213,7 +214,9 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
         }
     };
 
-    // x -> LDS (loads issued before any weight load), zero padding after each row
+    // x -> LDS (loads issued before any weight load), zero padding after each row,
+    // and -X_g for every (group, row) into the table: each thread sums its eight
+    // values, eight consecutive lanes hold one group (K/8 is a multiple of 8)
     {
         const int xchunks = (m_rows * k) >> 3;
         const int rowc = k >> 3;
@@ -226,11 +229,24 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
                 const int c = c0 + u * nthr + (int)threadIdx.x;
                 tmp[u] = buffer_load16(xrs, c < xchunks ? (uint32_t)c * 16u : kOutOfRange);
             }
-            if (c0 == 0 && chunks > 0) issue(wa, sa, 0);
+            if (c0 == 0) {  // both weight buffers requested before anything waits
+                if (chunks > 0) issue(wa, sa, 0);
+                if (chunks > 1) issue(wb, sbv2, 1);
+            }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = c0 + u * nthr + (int)threadIdx.x;
-                if (c < xchunks) lds[(c / rowc) * row16 + (c % rowc)] = tmp[u];
+                const int row = c / rowc;
+                const int cr = c - row * rowc;
+                if (c < xchunks) lds[row * row16 + cr] = tmp[u];
+                const uint32_t w4[4] = {tmp[u].x, tmp[u].y, tmp[u].z, tmp[u].w};
+                float sum = 0.f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sum += bf16_lo(w4[j]) + bf16_hi(w4[j]);
+                sum += __shfl_xor(sum, 1);
+                sum += __shfl_xor(sum, 2);
+                sum += __shfl_xor(sum, 4);
+                if (c < xchunks && (lane & 7) == 0) negx[(cr >> 3) * 16 + row] = -sum;
             }
         }
         for (int c = threadIdx.x; c < m_rows * (kPad >> 3); c += nthr)
@@ -238,22 +254,7 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
     }
     __syncthreads();
 
-    const uint4 neg1_bits = make_uint4(0xBF80BF80u, 0xBF80BF80u, 0xBF80BF80u, 0xBF80BF80u);
-    const bf16x8 neg1 = __builtin_bit_cast(bf16x8, neg1_bits);
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    // -X_g for this wave's groups, in accumulator layout (rows 4*kq + r)
-    {
-        const int xb = arow * row16 + kq;
-        for (int g = 2 * gp0; g < 2 * (gp0 + cnt); ++g) {
-            const bf16x8 x0 = __builtin_bit_cast(bf16x8, lds[xb + g * 8]);
-            const bf16x8 x1 = __builtin_bit_cast(bf16x8, lds[xb + g * 8 + 4]);
-            f32x4 xn = mfma16x16x32(x0, neg1, zero);
-            xn = mfma16x16x32(x1, neg1, xn);
-            if (col == 0) *reinterpret_cast<f32x4*>(negx + g * 16 + 4 * kq) = xn;
-        }
-    }
-    __syncthreads();
-
     f32x4 acc = zero;
     int parity = 0;
     auto compute = [&](const uint4* wv, const uint2* sv, int c) {
@@ -313,12 +314,13 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
         }
     };
 
+    // two chunks in flight: compute one buffer, then refill it two chunks ahead
     for (int c = 0; c < chunks; c += 2) {
-        if (c + 1 < chunks) issue(wb, sbv2, c + 1);
         compute(wa, sa, c);
+        if (c + 2 < chunks) issue(wa, sa, c + 2);
         if (c + 1 < chunks) {
-            if (c + 2 < chunks) issue(wa, sa, c + 2);
             compute(wb, sbv2, c + 1);
+            if (c + 3 < chunks) issue(wb, sbv2, c + 3);
         }
     }
 }
@@ -338,7 +340,7 @@ inline Split choose_split(int gpairs, int mt) {
     return {4, waves};
 }
 
-constexpr size_t kMaxXLds = 64 * 1024;  // LDS budget for staged x + the -X table
+constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950 LDS per CU (and per workgroup)
 
 int device_cus() {
     static int cus[64] = {0};
@@ -358,13 +360,18 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, voi
     const int f32 = out_f32 ? 1 : 0;
     const size_t xbytes = (size_t)m * l.k * 2;
     constexpr int GPW = 4;
+    constexpr int R = MT < 4 ? MT : 4;
+    const size_t static_lds = 2 * 8 * R * 64 * sizeof(float);
     const size_t lds_bytes = (size_t)m * (l.k + GPW * 128) * 2 + (size_t)l.gp * 2 * 16 * 4;
-    if (MT <= 4 && lds_bytes <= kMaxXLds) {
+    if (lds_bytes + static_lds <= kLdsPerCu) {
         // persistent streaming kernel: 4 pairs per chunk, up to 8 waves per workgroup
         int waves = (l.gp + GPW - 1) / GPW;
         if (waves > 8) waves = 8;
         if (waves > l.gp) waves = l.gp;
-        const int capacity = device_cus() * (20 / waves > 0 ? 20 / waves : 1);
+        int per_cu = 20 / waves > 0 ? 20 / waves : 1;
+        const int lds_fit = (int)(kLdsPerCu / (lds_bytes + static_lds));
+        if (per_cu > lds_fit) per_cu = lds_fit;
+        const int capacity = device_cus() * per_cu;
         const int per_wg = (l.nb + capacity - 1) / capacity;
         const int grid = (l.nb + per_wg - 1) / per_wg;
         hipLaunchKernelGGL((decode_stream_kernel<MT, GPW>), dim3(grid), dim3(64 * waves), lds_bytes, stream, tiles,

@@ -20,7 +20,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 LIB_NAME = "libgemma4_qmm.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-SOURCES = ["qmm_runtime.cpp", "q4_layout.hip", "q4_decode.hip"]
+SOURCES = ["qmm_runtime.cpp", "q4_layout.hip", "q4_decode.hip", "q4_gemm.hip"]
 ARCH = "gfx950"
 
 
@@ -43,6 +43,9 @@ def build(verbose: bool = False) -> str:
         "-shared",
         "-Wall",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA results in arch VGPRs: the GEMM's fp32 accumulators are updated by
+        # VALU FMAs every group, which cannot read AGPRs
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-I", os.path.join(ROOT, "include"),
         "-o", tmp,
     ] + [os.path.join(CSRC, s) for s in SOURCES]

@@ -59,8 +59,11 @@ __device__ __forceinline__ uint2 stream_load(const uint2* p) {
 
 // Raw buffer loads: an offset at or beyond num_records reads as zero with no memory
 // traffic, which replaces per-lane branches around loads (gfx9 resource word 3).
+// Every buffer resource covers at most kMaxBufferBytes, so kOutOfRange is always
+// past num_records (the host refuses larger buffers).
 constexpr int kBufferFlags = 0x00020000;
 constexpr uint32_t kOutOfRange = 0x80000000u;
+constexpr size_t kMaxBufferBytes = (size_t)1 << 31;
 constexpr int kNonTemporal = 2;  // aux bit 1: nt
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

@@ -181,7 +181,7 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
     constexpr int R = MT < 4 ? MT : 4;
     constexpr int kPad = GPW * 128;  // zero columns after each x row
     extern __shared__ uint4 lds[];
-    // layout: x rows [m_rows][k + kPad] bf16, then -X table [2*gpairs][16] fp32
+    // layout: x rows [m_rows][k + kPad] bf16, then -X table [2*(gpairs+GPW)][16] fp32
     __shared__ float red[2][8][R * 64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -194,7 +194,8 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
     const int chunks = my_blocks * passes;
     const int arow = col < m_rows ? col : m_rows - 1;  // any valid row for A rows >= M
     const int row16 = (k + kPad) >> 3;                 // x row stride in 16-byte units
-    float* negx = reinterpret_cast<float*>(lds + m_rows * row16);
+    const int groups = k >> 6;
+    float* negx = reinterpret_cast<float*>(lds + m_rows * row16);  // [2 * (gpairs + GPW)][16]
 
     uint4 wa[GPW], wb[GPW];
     uint2 sa[GPW], sbv2[GPW];
@@ -251,6 +252,9 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
         }
         for (int c = threadIdx.x; c < m_rows * (kPad >> 3); c += nthr)
             lds[(c / (kPad >> 3)) * row16 + rowc + (c % (kPad >> 3))] = make_uint4(0, 0, 0, 0);
+        // table entries of groups past K (padding, and pairs past a wave's range) are
+        // read by zero weight slots: they must be finite, so zero them
+        for (int t = groups * 16 + (int)threadIdx.x; t < 2 * (gpairs + GPW) * 16; t += nthr) negx[t] = 0.f;
     }
     __syncthreads();
 
@@ -358,11 +362,10 @@ template <int MT>
 hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
                      bool out_f32, const Layout& l, hipStream_t stream) {
     const int f32 = out_f32 ? 1 : 0;
-    const size_t xbytes = (size_t)m * l.k * 2;
     constexpr int GPW = 4;
     constexpr int R = MT < 4 ? MT : 4;
     const size_t static_lds = 2 * 8 * R * 64 * sizeof(float);
-    const size_t lds_bytes = (size_t)m * (l.k + GPW * 128) * 2 + (size_t)l.gp * 2 * 16 * 4;
+    const size_t lds_bytes = (size_t)m * (l.k + GPW * 128) * 2 + (size_t)(l.gp + GPW) * 2 * 16 * 4;
     if (lds_bytes + static_lds <= kLdsPerCu) {
         // persistent streaming kernel: 4 pairs per chunk, up to 8 waves per workgroup
         int waves = (l.gp + GPW - 1) / GPW;

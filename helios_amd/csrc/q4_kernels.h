@@ -39,4 +39,13 @@ hipError_t launch_dequantize(const uint4* tiles, const uint2* sb, float* out, co
 hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
                          bool out_f32, const Layout& l, hipStream_t stream);
 
+// Prefill path: fp32-exact factored GEMM on the matrix cores.  `workspace` holds the
+// group sums of x (gemm_workspace_bytes(m, l) bytes, device memory, 16-byte aligned).
+size_t gemm_workspace_bytes(int m, const Layout& l);
+hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, bool out_f32,
+                       const Layout& l, void* workspace, hipStream_t stream);
+
+// Rows at or above which forward uses the GEMM path.
+constexpr int kGemmMinRows = 32;
+
 }  // namespace q4

@@ -9,9 +9,11 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
+#include "q4_common.h"
 #include "q4_kernels.h"
 
 namespace {
@@ -32,6 +34,38 @@ Gemma4Status ok() {
 Gemma4Status hip_fail(const char* where, hipError_t e) {
     return fail(GEMMA4_ERR_RUNTIME, std::string(where) + ": " + hipGetErrorName(e) + " (" +
                                         hipGetErrorString(e) + ")");
+}
+
+// Per-device stream-ordered memory pool for per-call scratch (the GEMM's group sums
+// of x).  Its release threshold is unlimited, so after the first calls allocations
+// are served from memory the pool keeps; it is separate from the device's default
+// pool, so callers' own allocators are untouched.  Allocations are stream-ordered,
+// which keeps forward reentrant across streams.
+std::mutex g_pool_mu;
+hipMemPool_t g_pools[64] = {};
+
+hipError_t scratch_pool(int device, hipMemPool_t* out) {
+    if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    if (g_pools[device] == nullptr) {
+        hipMemPoolProps props{};
+        props.allocType = hipMemAllocationTypePinned;
+        props.handleTypes = hipMemHandleTypeNone;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = device;
+        hipMemPool_t pool = nullptr;
+        hipError_t e = hipMemPoolCreate(&pool, &props);
+        if (e != hipSuccess) return e;
+        uint64_t keep = UINT64_MAX;
+        e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+        if (e != hipSuccess) {
+            (void)hipMemPoolDestroy(pool);
+            return e;
+        }
+        g_pools[device] = pool;
+    }
+    *out = g_pools[device];
+    return hipSuccess;
 }
 
 // Restores the caller's current device on scope exit.
@@ -77,6 +111,10 @@ Gemma4Status check_desc(const Gemma4QLinearDesc* desc, const char* fn) {
         return fail(GEMMA4_ERR_INVALID_ARGUMENT, std::string(fn) + ": in_features must be a multiple of 64");
     if (desc->out_features > (1u << 30) || desc->in_features > (1u << 24))
         return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, std::string(fn) + ": shape exceeds the supported range");
+    const q4::Layout l = q4::make_layout((int)desc->out_features, (int)desc->in_features);
+    if (l.tile_bytes() > q4::kMaxBufferBytes || l.sb_bytes() > q4::kMaxBufferBytes)
+        return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
+                    std::string(fn) + ": weights exceed 2 GiB per projection (split it along out_features)");
     return GEMMA4_OK;
 }
 
@@ -246,12 +284,33 @@ Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, c
         if ((reinterpret_cast<uintptr_t>(y_dev) & yalign) != 0)
             return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_forward: y is misaligned for its dtype");
         if (rows > (1u << 24)) return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, "gemma4_qlinear_forward: rows exceeds 2^24");
+        if ((size_t)rows * linear->layout.k * 2 > q4::kMaxBufferBytes)
+            return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
+                        "gemma4_qlinear_forward: x exceeds 2 GiB (split the rows into several calls)");
         DeviceGuard guard;
         hipError_t e = guard.enter(linear->device);
         if (e != hipSuccess) return hip_fail("gemma4_qlinear_forward: hipSetDevice", e);
-        e = q4::launch_decode(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, y_dtype == GEMMA4_QMM_F32,
-                              linear->layout, static_cast<hipStream_t>(stream));
-        if (e != hipSuccess) return hip_fail("gemma4_qlinear_forward: launch", e);
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        const bool f32 = y_dtype == GEMMA4_QMM_F32;
+        if ((int)rows < q4::kGemmMinRows) {
+            e = q4::launch_decode(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, f32, linear->layout, st);
+            if (e != hipSuccess) return hip_fail("gemma4_qlinear_forward: decode launch", e);
+            return ok();
+        }
+        // group sums of x live in a stream-ordered scratch allocation for this call
+        const size_t ws_bytes = q4::gemm_workspace_bytes((int)rows, linear->layout);
+        hipMemPool_t pool = nullptr;
+        e = scratch_pool(linear->device, &pool);
+        if (e != hipSuccess) return hip_fail("gemma4_qlinear_forward: scratch pool", e);
+        void* ws = nullptr;
+        e = hipMallocFromPoolAsync(&ws, ws_bytes, pool, st);
+        if (e != hipSuccess)
+            return fail(GEMMA4_ERR_MEMORY_GUARD, std::string("gemma4_qlinear_forward: workspace allocation failed: ") +
+                                                     hipGetErrorString(e));
+        e = q4::launch_gemm(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, f32, linear->layout, ws, st);
+        const hipError_t ef = hipFreeAsync(ws, st);
+        if (e != hipSuccess) return hip_fail("gemma4_qlinear_forward: gemm launch", e);
+        if (ef != hipSuccess) return hip_fail("gemma4_qlinear_forward: workspace release", ef);
         return ok();
     } catch (...) {
         return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward: unexpected native exception");

@@ -213,3 +213,72 @@ def test_forward_many_row_blocks_per_workgroup(gpu_lib, m):
     y = lin.forward(dev_x(x), out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert_close(y, C.qmm_f64(x, wq, s, b), f"tall m={m}")
+
+
+# ---------------------------------------------------------------- prefill (GEMM path)
+
+@pytest.mark.parametrize("n,k,m", [(40, 384, 33), (256, 640, 300), (130, 320, 257), (512, 3840, 64)])
+@pytest.mark.parametrize("f32", [False, True])
+def test_gemm_small_shapes(gpu_lib, n, k, m, f32):
+    """GEMM path (M >= 32): ragged M and N, odd group counts, outlier activations."""
+    import torch
+
+    wq, s, b = random_triple(n, k, seed=n + k + m)
+    x = A.make_activations(m, k, seed=m, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    y = lin.forward(dev_x(x), out_dtype=torch.float32 if f32 else torch.bfloat16)
+    torch.cuda.synchronize()
+    worst = assert_close(y, C.qmm_f64(x, wq, s, b), f"gemm n={n} k={k} m={m}")
+    if f32:
+        # exact products and fp32 accumulation; the group sums X_g enter the bias term
+        # as two bf16 parts (about 16 bits), which outlier rows make the largest term
+        assert worst < 5e-4
+
+
+@pytest.mark.parametrize("proj", ["q_proj", "k_proj", "o_proj", "gate_proj", "down_proj"])
+def test_gemm_prefill_projections_m512(gpu_lib, proj):
+    import torch
+
+    n, k = PROJ[proj]
+    triple = A.make_weights(n, k, seed=20260630 + 2000 + sorted(PROJ).index(proj))
+    x = A.make_activations(512, k, seed=512, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*triple))
+    xd = dev_x(x)
+    y_bf = lin.forward(xd)
+    y_f = lin.forward(xd, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    # full-size prefill is too large for the float64 CPU oracle in full: sample rows
+    rows = np.random.default_rng(1).choice(512, 24, replace=False)
+    rows.sort()
+    y_exact = C.qmm_f64(np.ascontiguousarray(x[rows]), *triple)
+    assert_close(y_bf[torch.from_numpy(rows).cuda()], y_exact, f"{proj} m=512 bf16")
+    worst = assert_close(y_f[torch.from_numpy(rows).cuda()], y_exact, f"{proj} m=512 f32")
+    assert worst < 5e-4
+    # every row block of the output is written (no stale tiles): compare the f32 and
+    # bf16 results everywhere, which agree to bf16 rounding
+    diff = (y_bf.float() - y_f).abs()
+    assert torch.all(diff <= y_f.abs() * 2**-8 + 1e-6).item()
+
+
+def test_gemm_prefill_chain_m2048_geglu(gpu_lib):
+    """Chunked-prefill chain at M=2048: gate and up, GeGLU on the host (identical bf16
+    bytes to both sides), then down_proj; sampled rows against the oracle."""
+    import torch
+
+    m = 2048
+    tri = {p: A.make_weights(*PROJ[p], seed=20260630 + 2000 + sorted(PROJ).index(p)) for p in
+           ("gate_proj", "up_proj", "down_proj")}
+    x = A.make_activations(m, 3840, seed=2048, outliers=True)
+    lins = {p: gpu_lib.QuantizedLinear(*dev_triple(*t)) for p, t in tri.items()}
+    xd = dev_x(x)
+    g = lins["gate_proj"].forward(xd)
+    u = lins["up_proj"].forward(xd)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(2).choice(m, 16, replace=False))
+    rt = torch.from_numpy(rows).cuda()
+    assert_close(g[rt], C.qmm_f64(np.ascontiguousarray(x[rows]), *tri["gate_proj"]), "gate m=2048")
+    assert_close(u[rt], C.qmm_f64(np.ascontiguousarray(x[rows]), *tri["up_proj"]), "up m=2048")
+    h = A.gelu_tanh_times(host_bits(g), host_bits(u))
+    d = lins["down_proj"].forward(dev_x(h))
+    torch.cuda.synchronize()
+    assert_close(d[rt], C.qmm_f64(np.ascontiguousarray(h[rows]), *tri["down_proj"]), "down m=2048")

@@ -19,7 +19,13 @@ launch from graph replays of back-to-back launches), every projection at M = 1, 
 8, the lm_head at M = 1, 8, 16, the prefill GEMM at M=2048, and the CPU baseline
 (the oracle's fp32 loop on the host cores, on a bounded sample of the same work).
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-gemm]
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--quick]
+    python bench.py --roofline-only   # the dominant kernel and a 1 GiB copy only (for rocprofv3)
+
+`roofline.traffic` is the HBM bytes one launch of the dominant kernel moves, from
+rocprofv3 FETCH_SIZE and WRITE_SIZE passes over `--roofline-only`, each scaled by
+what the same counter reads for the 1 GiB copy; it is read from
+profiles/gate_up_decode_m1_traffic.json when that file describes the same launch.
 """
 
 from __future__ import annotations
@@ -55,6 +61,8 @@ STEP = [("qkv_proj", ("q_proj", "k_proj", "v_proj")), ("o_proj", ("o_proj",)),
         ("gate_up_proj", ("gate_proj", "up_proj")), ("down_proj", ("down_proj",))]
 SEED_BASE = 20260630
 ROTATE_BYTES = 512 << 20
+COPY_BYTES = 1 << 30
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_decode_m1_traffic.json")
 
 
 def algo_bytes(m: int, n: int, k: int, y_bytes: int = 2) -> int:
@@ -135,6 +143,140 @@ def kernel_us(torch, Q, triple, m: int, k: int, n: int, xdev, reps_per_graph: in
     return ms * 1e3 / launches
 
 
+def copy_gbs(torch, nbytes: int = COPY_BYTES, reps: int = 20) -> float:
+    """Practical HBM rate: a plain device-to-device copy of nbytes (read + write
+    counted), timed with events on the current stream."""
+    src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    del src, dst
+    return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
+def dense_gemm_tflops(torch, m: int, n: int, k: int, reps: int = 20) -> float:
+    """Practical bf16 MFMA rate on the same GEMM shape: torch's bf16 linear (hipBLASLt)
+    on a dense bf16 weight."""
+    a = torch.randn(m, k, dtype=torch.bfloat16, device="cuda")
+    w = torch.randn(n, k, dtype=torch.bfloat16, device="cuda")
+    for _ in range(3):
+        torch.nn.functional.linear(a, w)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        torch.nn.functional.linear(a, w)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    del a, w
+    return algo_flops(m, n, k) / (ms * 1e-3) / 1e12
+
+
+def recorded_traffic(kernel: str, algo: int):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    counter passes, if they describe this launch."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None, None
+    if t.get("kernel") != kernel or t.get("algo_bytes_per_launch") != algo:
+        return None, None
+    return t.get("traffic_bytes_per_launch"), t
+
+
+def _csv_rows(d: str, suffix: str):
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True))
+    if not files:
+        raise SystemExit(f"no *{suffix} under {d}")
+    with open(files[0], newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def summarize_profiles(stats_dir: str, fetch_dir: str, write_dir: str, line_file: str, command: str) -> None:
+    """Turns rocprofv3 output over `bench.py --roofline-only` into the committed
+    summaries: the kernel-trace statistics (average launch duration of the dominant
+    kernel, to compare with the bench's own HIP-event figure) and the HBM traffic per
+    launch from the FETCH_SIZE / WRITE_SIZE passes, each scaled by what the same
+    counter reads for the 1 GiB copy."""
+    with open(line_file) as f:
+        line = json.loads([l for l in f if l.startswith("{")][-1])
+    stats = _csv_rows(stats_dir, "kernel_stats.csv")
+
+    def short(name: str) -> str:
+        return name.replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0][:90]
+
+    def per_dispatch(rows, counter, match):
+        vals = [float(r["Counter_Value"]) for r in rows if r["Counter_Name"] == counter and match(r["Kernel_Name"])]
+        if not vals:
+            raise SystemExit(f"no {counter} rows for the kernel")
+        return sum(vals) / len(vals), len(vals)
+
+    is_dom = lambda n: "decode_stream_kernel" in n  # noqa: E731
+    is_copy = lambda n: "copy" in n.lower()  # noqa: E731
+    fetch_rows = _csv_rows(fetch_dir, "counter_collection.csv")
+    write_rows = _csv_rows(write_dir, "counter_collection.csv")
+    f_dom, n_fd = per_dispatch(fetch_rows, "FETCH_SIZE", is_dom)
+    f_cpy, n_fc = per_dispatch(fetch_rows, "FETCH_SIZE", is_copy)
+    w_dom, n_wd = per_dispatch(write_rows, "WRITE_SIZE", is_dom)
+    w_cpy, n_wc = per_dispatch(write_rows, "WRITE_SIZE", is_copy)
+    f_scale = line["copy_bytes"] / (f_cpy * 1024)
+    w_scale = line["copy_bytes"] / (w_cpy * 1024)
+    fetch_b = f_dom * 1024 * f_scale
+    write_b = w_dom * 1024 * w_scale
+    dom_stats = [r for r in stats if is_dom(r["Name"])]
+    avg_ns = float(dom_stats[0]["AverageNs"]) if dom_stats else None
+    traffic = {
+        "kernel": line["kernel"],
+        "algo_bytes_per_launch": line["algo_bytes_per_launch"],
+        "traffic_bytes_per_launch": int(round(fetch_b + write_b)),
+        "fetch_bytes_per_launch": int(round(fetch_b)),
+        "write_bytes_per_launch": int(round(write_b)),
+        "traffic_over_algo": round((fetch_b + write_b) / line["algo_bytes_per_launch"], 4),
+        "fetch_size_kib_per_dispatch": round(f_dom, 1),
+        "write_size_kib_per_dispatch": round(w_dom, 1),
+        "copy_fetch_kib": round(f_cpy, 1),
+        "copy_write_kib": round(w_cpy, 1),
+        "fetch_scale": round(f_scale, 5),
+        "write_scale": round(w_scale, 5),
+        "dispatches": {"fetch": n_fd, "write": n_wd, "copy_fetch": n_fc, "copy_write": n_wc},
+        "rocprof_avg_launch_us": round(avg_ns / 1e3, 3) if avg_ns else None,
+        "bench_avg_launch_us": line["avg_launch_us"],
+        "source": "rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE over bench.py --roofline-only",
+        "command": command,
+    }
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(traffic, f, indent=1)
+        f.write("\n")
+    md = [f"# Dominant decode kernel: {line['kernel']}", "", "Command (from the repository root):", "",
+          "```", command, "```", "", "bench.py --roofline-only line:", "", "```", json.dumps(line), "```", "",
+          "rocprofv3 --kernel-trace --stats (kernel_stats.csv):", "",
+          "| kernel | calls | avg us | min us | max us |", "|---|---:|---:|---:|---:|"]
+    for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))[:8]:
+        md.append(f"| {short(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
+                  f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} |")
+    md += ["", "HBM traffic per launch (FETCH_SIZE, WRITE_SIZE in KiB per dispatch, scaled by the 1 GiB copy):", "",
+           "```", json.dumps(traffic, indent=1), "```", ""]
+    with open(os.path.join(ROOT, "profiles", "gate_up_decode_m1.md"), "w") as f:
+        f.write("\n".join(md))
+    print(json.dumps(traffic))
+
+
 def cpu_baseline(host, target_s: float = 12.0) -> dict:
     """The oracle's fp32 qmm loop (OpenMP over rows) on this host's cores, on a
     bounded sample: whole decoder-layer steps at M=1, repeated until ~target_s."""
@@ -150,15 +292,22 @@ def cpu_baseline(host, target_s: float = 12.0) -> dict:
         for name, n, k in LAYER:
             C.qmm_f32(xs[k], *host[name], threads=threads, out=outs[name])
 
-    one_step()
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
+    def timed(target):
         one_step()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= target_s or reps >= 2000:
-            break
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            one_step()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= target or reps >= 2000:
+                return reps, el
+
+    reps, el = timed(target_s)
+    nthreads_all = threads
+    threads = 1
+    reps1, el1 = timed(target_s / 3)
+    threads = nthreads_all
     return {
         "value": round(step_bytes * reps / el / 1e9, 3),
         "unit": "GB/s",
@@ -166,6 +315,9 @@ def cpu_baseline(host, target_s: float = 12.0) -> dict:
         "kind": "port",
         "sample": f"{reps} decoder-layer steps (7 projections, M=1) in {el:.1f} s; C restatement of the "
                   f"fp32 dequantize-and-dot loop (oracle/q4_oracle.c), OpenMP over rows, {threads} threads",
+        "value_1_core": round(step_bytes * reps1 / el1 / 1e9, 3),
+        "sample_1_core": f"{reps1} of the same steps in {el1:.1f} s on 1 thread",
+        "host_cpus": os.cpu_count(),
     }
 
 
@@ -177,7 +329,14 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (skip the per-shape sweeps)")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="time only the dominant kernel and a 1 GiB copy (the program rocprofv3 passes run)")
+    ap.add_argument("--summarize-profiles", nargs=5, metavar=("STATS_DIR", "FETCH_DIR", "WRITE_DIR", "LINE", "CMD"),
+                    help="write the profiles/ summaries from rocprofv3 output over --roofline-only (no GPU)")
     args = ap.parse_args()
+    if args.summarize_profiles:
+        summarize_profiles(*args.summarize_profiles)
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         return 2
@@ -195,13 +354,24 @@ def main() -> int:
     fused = {name: fused_triple(host, parts) for name, parts in STEP}
     fused_nk = {name: (sum(dict((l[0], l[1]) for l in LAYER)[p] for p in parts), dict((l[0], l[2]) for l in LAYER)[parts[0]])
                 for name, parts in STEP}
+    xs = {k: torch.from_numpy(A.make_activations(16, k, seed=SEED_BASE + k).view(np.int16)).view(torch.bfloat16).cuda()
+          for k in {k for _, _, k in LAYER}}
+    n_gu, k_gu = fused_nk["gate_up_proj"]
+    gu_bytes = algo_bytes(1, n_gu, k_gu)
+    gu_kernel = f"decode_stream_kernel<1,4> gate|up fused N={n_gu} K={k_gu} M=1"
+
+    if args.roofline_only:
+        us_gu = kernel_us(torch, Q, fused["gate_up_proj"], 1, k_gu, n_gu, xs[k_gu])
+        cgbs = copy_gbs(torch)
+        print(json.dumps({"kernel": gu_kernel, "algo_bytes_per_launch": gu_bytes, "avg_launch_us": round(us_gu, 3),
+                          "achieved_GBps": round(gu_bytes / (us_gu * 1e-6) / 1e9, 1),
+                          "copy_bytes": COPY_BYTES, "copy_GBps": round(cgbs, 1)}), flush=True)
+        return 0
+
     layer_w_bytes = sum(n * k // 2 + 4 * n * (k // 64) for _, n, k in LAYER)
     copies = max(2, -(-ROTATE_BYTES // layer_w_bytes))
     log(f"uploading {copies} copies of the layer ({copies * layer_w_bytes / 2**20:.0f} MiB)")
     layers = [{name: Q.QuantizedLinear(*fused[name]) for name, _ in STEP} for _ in range(copies)]
-
-    xs = {k: torch.from_numpy(A.make_activations(16, k, seed=SEED_BASE + k).view(np.int16)).view(torch.bfloat16).cuda()
-          for k in {k for _, _, k in LAYER}}
     ys = {name: torch.empty((16, n), dtype=torch.bfloat16, device="cuda") for name, (n, _) in fused_nk.items()}
 
     def step_fn(m):
@@ -228,21 +398,22 @@ def main() -> int:
     del layers
 
     # --- dominant kernel: fused gate|up GEMV at M=1 ---
-    n_gu, k_gu = fused_nk["gate_up_proj"]
     us_gu = kernel_us(torch, Q, fused["gate_up_proj"], 1, k_gu, n_gu, xs[k_gu])
-    gu_bytes = algo_bytes(1, n_gu, k_gu)
     gu_gbs = gu_bytes / (us_gu * 1e-6) / 1e9
+    traffic, traffic_rec = recorded_traffic(gu_kernel, gu_bytes)
     roofline = {
         "bound": "hbm",
         "achieved": round(gu_gbs, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-        "traffic": None,
-        "kernel": f"decode_stream_kernel<1,4> gate|up fused N={n_gu} K={k_gu} M=1",
+        "traffic": traffic,
+        "kernel": gu_kernel,
         "algo_bytes_per_launch": gu_bytes,
         "avg_launch_us": round(us_gu, 3),
     }
+    if traffic_rec is not None:
+        roofline["traffic_source"] = traffic_rec.get("source")
 
     per_proj = {}
     lm = None
@@ -273,18 +444,34 @@ def main() -> int:
         except Exception as e:  # memory or build problems should not hide the headline
             lm = {"error": str(e)}
 
-    # --- prefill GEMM at M=2048 (gate shape) ---
+    # --- prefill GEMM: the seven projections at M = 512, 2048 (gate at M=2048 headlines) ---
     gemm = None
+    peaks = None
     if not args.no_gemm:
-        xm = torch.from_numpy(A.make_activations(2048, HIDDEN, seed=SEED_BASE + 2, outliers=True).view(np.int16)) \
-            .view(torch.bfloat16).cuda()
-        ym = torch.empty((2048, 15360), dtype=torch.bfloat16, device="cuda")
-        lin = Q.QuantizedLinear(*host["gate_proj"])
-        ms = graph_ms(torch, lambda: lin.forward(xm, out=ym), replays=5, warmup=1)
-        lin.close()
-        tflops = algo_flops(2048, 15360, HIDDEN) / (ms * 1e-3) / 1e12
-        gemm = {"shape": "gate_proj M=2048 N=15360 K=3840", "ms": round(ms, 4), "TFLOPS": round(tflops, 1),
-                "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
+        gemm = {}
+        shapes = LAYER if not args.quick else [l for l in LAYER if l[0] == "gate_proj"]
+        for m in ((512, 2048) if not args.quick else (2048,)):
+            xk = {k: torch.from_numpy(A.make_activations(m, k, seed=SEED_BASE + 2 + k, outliers=True).view(np.int16))
+                  .view(torch.bfloat16).cuda() for k in {k for _, _, k in shapes}}
+            for name, n, k in shapes:
+                ym = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+                lin = Q.QuantizedLinear(*host[name])
+                ms = graph_ms(torch, lambda: lin.forward(xk[k], out=ym), replays=10, warmup=2)
+                lin.close()
+                tflops = algo_flops(m, n, k) / (ms * 1e-3) / 1e12
+                gemm[f"{name}_m{m}"] = {"us": round(ms * 1e3, 1), "TFLOPS": round(tflops, 1),
+                                        "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
+                del ym
+            del xk
+        head = gemm["gate_proj_m2048"]
+        gemm["headline"] = {"shape": "gate_proj M=2048 N=15360 K=3840", **head}
+        if not args.quick:
+            log("practical peaks: 1 GiB copy, dense bf16 GEMM (hipBLASLt) on the gate shape")
+            dense = dense_gemm_tflops(torch, 2048, 15360, HIDDEN)
+            cg = copy_gbs(torch)
+            peaks = {"copy_GBps": round(cg, 1), "dense_bf16_gemm_TFLOPS_gate_m2048": round(dense, 1),
+                     "roofline_frac_of_copy": round(gu_gbs / cg, 4),
+                     "gemm_frac_of_dense": round(head["TFLOPS"] / dense, 4)}
 
     cpu = None
     if not args.no_cpu:
@@ -318,6 +505,7 @@ def main() -> int:
         "decode_per_projection": per_proj,
         "lm_head": lm,
         "prefill_gemm": gemm,
+        "practical_peaks": peaks,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -35,6 +35,22 @@ constexpr int kXChunks = kBM * 8;     // 16-byte chunks of one x group tile (256
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// 16-byte-per-lane DMA into LDS: lane i's 16 bytes land at lds + 16 i, read from
+// voff + soff.  Only voff is checked against the buffer's size (a resource of size
+// 0 reads zeros for any offset); callers keep voff + soff inside the buffer for
+// in-range lanes and put the rest at kOutOfRange.  Issued as
+// inline asm, so the compiler does not track it: it would otherwise insert waits for
+// all outstanding DMAs before LDS reads it cannot tell apart from them (it keeps at
+// most eight DMA records), undoing the prefetch.  Ordering is this kernel's own: every
+// DMA'd slot is read only after an explicit vmcnt wait and a barrier.  M0 (the LDS
+// address) is an operand, so the compiler knows it is written; the s_nop is the one
+// wait state an M0 write needs before an LDS DMA.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, const void* lds, uint32_t voff, uint32_t soff = 0) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);  // LDS offset: low half of the generic address
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0)
+                 : "memory");
+}
+
 // ---------------------------------------------------------------------------
 // X_g = sum of x over each 64-wide group, as the augmented-K MFMA A operand:
 // xaug[m16][octet][lane] (16 B), lane (m = l%16, kq = l/16), element e ->
@@ -99,20 +115,25 @@ __device__ __forceinline__ void tile_of(int id, int nwg, int mtiles, int ntiles,
     nt = r / bm;
 }
 
-// LDS ring buffers, three slots each (group g uses slot g % 3; the loads for g+2 are
-// in flight while g is multiplied).  Each slot is its own object so the compiler
-// can tell a DMA into one slot from reads of another (a shared array would make it
-// wait for every DMA before every read).
+// LDS rings.  x: three slots of one group each (group g in slot g % 3; the loads for
+// g+2 are in flight while g is multiplied).  Weights: two slots of one group pair
+// each (pair p in slot p % 2, loaded with the x of its first group), holding the
+// tiled words of the workgroup's 16 row blocks [row block][lane] (16 KiB) followed
+// by their scale/bias words [row block][row] as uint2 (2 KiB).  Every load is a
+// 16-byte-per-lane DMA: 4-byte LDS DMAs cost the load pipe about twice the cycles
+// for a quarter of the bytes.  Each slot is its own object so the compiler can tell
+// a DMA into one slot from reads of another (a shared array would make it wait for
+// every DMA before every read); it tells apart at most eight such objects.
+constexpr int kWPair = kRB * 64;          // uint4: tiled words of the pair
+constexpr int kSPair = kRB * 16 / 2;      // uint4: scale/bias words of the pair
 __shared__ uint4 g_xs0[kXChunks];          // x group tile, 256 rows x 64 (32 KiB)
 __shared__ uint4 g_xs1[kXChunks];
 __shared__ uint4 g_xs2[kXChunks];
-__shared__ uint32_t g_wt0[kRB * 2 * 64];   // the group's weight words: [row block][half][lane] (8 KiB)
-__shared__ uint32_t g_wt1[kRB * 2 * 64];
-__shared__ uint32_t g_wt2[kRB * 2 * 64];
-__shared__ uint32_t g_sb0[kRB * 16];       // the group's scale/bias words: [row block][column] (1 KiB)
-__shared__ uint32_t g_sb1[kRB * 16];
-__shared__ uint32_t g_sb2[kRB * 16];
-__shared__ uint4 g_xa[16 * 64];            // bias-MFMA A operands of the 256 rows for one octet (16 KiB)
+__shared__ uint4 g_wp0[kWPair + kSPair];   // 18 KiB
+__shared__ uint4 g_wp1[kWPair + kSPair];
+// one octet's bias operands: A side for the 256 rows [m16][lane] (16 KiB), then the
+// scale/bias words as uint2 [row block][pair][column] (8 KiB)
+__shared__ uint4 g_xab[16 * 64 + kRB * 4 * 16 / 2];
 
 // s_waitcnt with vmcnt(n) only (expcnt / lgkmcnt left free), n < 64
 template <int N>
@@ -153,52 +174,61 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
 
     // ---- DMA issue, per wave and group: x 4, weight words 4, scale words 1; bias
     // operands 2 per octet ----
-    uint32_t xoff[4];
+    // DMA issue.  Per lane, the offsets are fixed for the whole K loop (rows past M and
+    // row blocks past N at kOutOfRange) and computed once here; the step moves them by
+    // a scalar offset (group x 128 bytes of x, pair x 1 KiB of tiles, pair x 128 bytes
+    // of scale words), which stays inside the buffer for every in-range lane.  Past the
+    // last group or pair the resource is swapped for an empty one: zeros, into slots
+    // nobody reads again.  Branch-free, so they can sit anywhere in the product stream.
+    const __amdgpu_buffer_rsrc_t zrs = make_rsrc(x, 0u);
+    uint32_t xv[4];  // x of a group, part u: 16-byte chunk q of the 256 x 64 tile, row r,
+                     // chunk c of the row, stored at position c ^ ((r >> 1) & 7) of its LDS
+                     // row (swizzle: conflict-free MFMA operand reads)
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        const int q = (8 * u + wave) * 64 + lane;  // 16-byte chunk of the 256 x 64 tile
+        const int q = (8 * u + wave) * 64 + lane;
         const int r = q >> 3;
-        const int c = (q & 7) ^ ((r >> 1) & 7);  // swizzled: chunk c of row r sits at position c ^ ((r>>1)&7)
+        const int c = (q & 7) ^ ((r >> 1) & 7);
         const int row = mt * kBM + r;
-        xoff[u] = row < m_rows ? (uint32_t)(row * k + 8 * c) * 2u : kOutOfRange;
+        xv[u] = row < m_rows ? ((uint32_t)row * (uint32_t)k + (uint32_t)(8 * c)) * 2u : kOutOfRange;
     }
-    auto dma = [&](int g, uint4* xdst, uint32_t* wdst, uint32_t* sdst) {
-        const uint32_t gofs = (uint32_t)g * 128u;
+    uint32_t wv[2];  // tiled words of a pair, part t: row block 2w + t, one 16-byte word per lane
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t off = xoff[u] == kOutOfRange ? kOutOfRange : xoff[u] + gofs;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_ptr_t)(xdst + (8 * u + wave) * 64), 16, off, 0, 0, 0);
-        }
-        // weight words of the group: row block rbl = 2w + t, half h -> tile word 2*(g&1) + h
-        const int gp = g >> 1;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int rbl = 2 * wave + t;
-            const int rb = rbw + rbl;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t off =
-                    rb < nblocks ? (uint32_t)((((long)rb * gpairs + gp) * 64 + lane) * 16 + (2 * (g & 1) + h) * 4)
-                                 : kOutOfRange;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(trs, (lds_ptr_t)(wdst + (rbl * 2 + h) * 64), 4, off, 0, 0, 0);
-            }
-        }
-        if (lane < 32) {  // 32 lanes x 4 B: scale words of row blocks 2w, 2w+1
-            const int rbl = 2 * wave + (lane >> 4);
-            const int rb = rbw + rbl;
-            const uint32_t off =
-                rb < nblocks ? (uint32_t)((((long)rb * gpairs + gp) * 16 + (lane & 15)) * 8 + (g & 1) * 4)
-                             : kOutOfRange;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_ptr_t)(sdst + 32 * wave), 4, off, 0, 0, 0);
-        }
+    for (int t = 0; t < 2; ++t) {
+        const int rb = rbw + 2 * wave + t;
+        wv[t] = rb < nblocks ? ((uint32_t)rb * (uint32_t)gpairs * 64u + (uint32_t)lane) * 16u : kOutOfRange;
+    }
+    uint32_t sv;  // scale words of a pair (waves 0, 1): row block 8w + l/8, chunk l%8 of its 128 bytes
+    {
+        const int rb = rbw + 8 * wave + (lane >> 3);
+        sv = rb < nblocks ? (uint32_t)rb * (uint32_t)gpairs * 128u + (uint32_t)(lane & 7) * 16u : kOutOfRange;
+    }
+    auto dma_x = [&](int g, int part, uint4* xdst) {
+        dma16(g < groups ? xrs : zrs, xdst + (8 * part + wave) * 64, xv[part], (uint32_t)g * 128u);
     };
+    auto dma_w = [&](int p, int part, uint4* wdst) {
+        dma16(p < gpairs ? trs : zrs, wdst + (2 * wave + part) * 64, wv[part], (uint32_t)p * 1024u);
+    };
+    auto dma_s = [&](int p, uint4* wdst) {
+        dma16(p < gpairs ? srs : zrs, wdst + kWPair + 64 * wave, sv, (uint32_t)p * 128u);
+    };
+    auto dma_xa_part = [&](int o, int u) {
+        const int m16 = 2 * wave + u;
+        dma16(ars, g_xab + m16 * 64, (uint32_t)lane * 16u, (uint32_t)(((mt * 16 + m16) * octets + o) * 1024));
+    };
+    // bias operands of octet o: the A side (two 16-byte loads) and the scale/bias words
+    // of its four group pairs for row blocks 2w, 2w+1 (lane l: row block 2w + l/32,
+    // 16-byte chunk l%32 of the row block's 512 contiguous bytes)
     auto dma_xa = [&](int o) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int m16 = 2 * wave + u;
-            const uint32_t off = (uint32_t)((((long)mt * 16 + m16) * octets + o) * 1024 + lane * 16);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (lds_ptr_t)(g_xa + m16 * 64), 16, off, 0, 0, 0);
-        }
+        int ln = threadIdx.x & 63;
+        asm volatile("" : "+v"(ln));
+        dma_xa_part(o, 0);
+        dma_xa_part(o, 1);
+        const int rb = rbw + 2 * wave + (ln >> 5);
+        const int chunk = ln & 31;
+        const bool ok = (rb < nblocks) & (4 * o + (chunk >> 3) < gpairs);
+        const uint32_t raw = ((uint32_t)rb * (uint32_t)gpairs + 4u * (uint32_t)o) * 128u + (uint32_t)chunk * 16u;
+        dma16(srs, g_xab + (16 * 64 + wave * 64), ok ? raw : kOutOfRange);
     };
 
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -209,95 +239,153 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         for (int j = 0; j < kNT; ++j) acc[i][j] = zero;
 
     // one 64-wide group from LDS slots
-    auto compute = [&](const uint4* xs, const uint32_t* wt, const uint32_t* sbl) {
+    // hook(t) runs after the products of tile t are issued: the next group's DMA
+    // instructions are spread through the product stream that way, so the CU's
+    // address unit takes them while the matrix cores work (issued in one burst, all
+    // eight waves would stall on it together)
+    auto compute = [&](const uint4* xs, const uint4* wp, int gpar, auto&& hook) {
+        // The slot arrays sit above the 64 KiB reach of a ds_read immediate offset, so
+        // every (slot, constant) address would become its own register, hoisted out of
+        // the loop for every slot.  An opaque lane index keeps them per step.
+        int ln = threadIdx.x & 63;
+        asm volatile("" : "+v"(ln));
+        const int lcol = ln & 15, lkq = ln >> 4;
         bf16x8 bq[kNT][2];
         float s16[kNT];
+        const uint2* sbl = reinterpret_cast<const uint2*>(wp + kWPair);
 #pragma unroll
         for (int j = 0; j < kNT; ++j) {
             const int rbl = wn * kNT + j;
-            bq[j][0] = expand_word(wt[(rbl * 2 + 0) * 64 + lane]);
-            bq[j][1] = expand_word(wt[(rbl * 2 + 1) * 64 + lane]);
-            s16[j] = bf16_lo(sbl[rbl * 16 + col]) * 16.0f;
+            const uint4 t = wp[rbl * 64 + ln];
+            bq[j][0] = expand_word(gpar ? t.z : t.x);
+            bq[j][1] = expand_word(gpar ? t.w : t.y);
+            const uint2 sw = sbl[rbl * 16 + lcol];
+            s16[j] = bf16_lo(gpar ? sw.y : sw.x) * 16.0f;
         }
         auto a_frag = [&](int i, int h) {
-            const int r = wm * kWM + 16 * i + col;
-            return __builtin_bit_cast(bf16x8, xs[r * 8 + ((4 * h + kq) ^ ((r >> 1) & 7))]);
+            const int r = wm * kWM + 16 * i + lcol;
+            return __builtin_bit_cast(bf16x8, xs[r * 8 + ((4 * h + lkq) ^ ((r >> 1) & 7))]);
         };
+        // the wave's 32 tiles in one stream, software-pipelined: tile t's two products
+        // are issued, then tile t-2's scale FMAs, which do not wait for them, so the
+        // matrix core and the VALU work at the same time
+        constexpr int kTiles = kMT * kNT;
+        constexpr int kLag = 2;
+        f32x4 p[kLag + 1];
+        bf16x8 a0, a1;
 #pragma unroll
-        for (int i = 0; i < kMT; ++i) {
-            const bf16x8 a0 = a_frag(i, 0), a1 = a_frag(i, 1);
-            f32x4 p[kNT];
+        for (int t = 0; t < kTiles + kLag; ++t) {
+            if (t < kTiles) {
+                const int i = t / kNT, j = t % kNT;
+                if (j == 0) {
+                    a0 = a_frag(i, 0);
+                    a1 = a_frag(i, 1);
+                }
+                p[t % (kLag + 1)] = mfma16x16x32(a0, bq[j][0], zero);
+                p[t % (kLag + 1)] = mfma16x16x32(a1, bq[j][1], p[t % (kLag + 1)]);
+                hook(t);
+            }
+            if (t >= kLag) {
+                const int u = t - kLag;
+                const int i = u / kNT, j = u % kNT;
 #pragma unroll
-            for (int j = 0; j < kNT; ++j) p[j] = mfma16x16x32(a0, bq[j][0], zero);
-#pragma unroll
-            for (int j = 0; j < kNT; ++j) p[j] = mfma16x16x32(a1, bq[j][1], p[j]);
-#pragma unroll
-            for (int j = 0; j < kNT; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[i][j][e] = __builtin_fmaf(s16[j], p[j][e], acc[i][j][e]);
+                for (int e = 0; e < 4; ++e)
+                    acc[i][j][e] = __builtin_fmaf(s16[j], p[u % (kLag + 1)][e], acc[i][j][e]);
+            }
         }
     };
-    // bias term of octet o: A operands from g_xa, B from the scale words (global)
-    auto bias = [&](const uint2* bw) {
+    // bias term of the octet: A operands and scale/bias words from g_xab
+    auto bias = [&]() {
         bf16x8 bb[kNT];
 #pragma unroll
-        for (int j = 0; j < kNT; ++j) bb[j] = bias_operand(bw[j]);
+        for (int j = 0; j < kNT; ++j) bb[j] = bias_operand(reinterpret_cast<const uint2*>(g_xab + 16 * 64)[((wn * kNT + j) * 4 + kq) * 16 + col]);
 #pragma unroll
         for (int i = 0; i < kMT; ++i) {
-            const bf16x8 aa = __builtin_bit_cast(bf16x8, g_xa[(wm * kMT + i) * 64 + lane]);
+            const bf16x8 aa = __builtin_bit_cast(bf16x8, g_xab[(wm * kMT + i) * 64 + lane]);
 #pragma unroll
             for (int j = 0; j < kNT; ++j) acc[i][j] = mfma16x16x32(aa, bb[j], acc[i][j]);
         }
     };
-    auto load_bias_words = [&](int o, uint2* bw) {
-#pragma unroll
-        for (int j = 0; j < kNT; ++j) {
-            const int rb = rbw + wn * kNT + j;
-            const int gp = 4 * o + kq;
-            const bool ok = rb < nblocks && gp < gpairs;
-            bw[j] = buffer_load8(srs, ok ? (uint32_t)(((long)rb * gpairs + gp) * 128 + col * 8) : kOutOfRange);
-        }
-    };
 
-    // Step g: (1) wait until this wave's DMAs for group g (issued at step g-2 in the
-    // order x, weights, scales; bias operands at the octet start) are done, leaving in
-    // flight only what was issued after them; (2) barrier: everyone's data for g is in
-    // LDS and everyone is done with the slot refilled next; (3) issue the DMAs for
-    // group g+2 (and at octet starts the octet's bias operands); (4) multiply.
-    auto issues = [&](int g) { return g + 2 < groups; };
-    auto issues_xa = [&](int g) { return (g & 7) == 0 && g > 0; };
-    auto step = [&](int g, const uint4* xs, const uint32_t* wt, const uint32_t* sbl, uint4* xs2, uint32_t* wt2,
-                    uint32_t* sb2) {
-        const int after = (g >= 2 && issues_xa(g - 2) ? 2 : 0) +
-                          (g >= 1 ? (issues(g - 1) ? 9 : 0) + (issues_xa(g - 1) ? 2 : 0) : 0);
-        switch (after) {
-            case 0: wait_vm_lds<0>(); break;
-            case 2: wait_vm_lds<2>(); break;
-            case 9: wait_vm_lds<9>(); break;
-            case 11: wait_vm_lds<11>(); break;
-            case 13: wait_vm_lds<13>(); break;
-            default: wait_vm_lds<0>(); break;  // (not reached) safe fallback
+    // Step g: (1) wait until this wave's loads for group g (issued during step g-2:
+    // x of g and, for even g, the pair g/2) are done, leaving in flight only the loads
+    // of step g-1 (its x, for even g-1 its pair, and the bias operands it may have
+    // issued first); (2) barrier: everyone's data for g is in LDS and everyone is done
+    // with the slots refilled next; (3) at g = 8o + 8, the bias term of octet o (its
+    // operands were loaded at step 8o + 1 and have been waited for since); at
+    // g = 8o + 1, the bias operands of octet o (the barrier above follows the last
+    // read of the previous octet's); (4) multiply, with the loads for group g+2 (and
+    // pair (g+2)/2) spread through the products.  Every step issues the same loads
+    // (past the end they read zeros), so the counts are fixed.
+    auto issues_xa = [&](int g) { return (g & 7) == 1 && g > 1; };
+    auto issued = [&](int g) {  // loads this wave issues at step g
+        return 4 + ((g & 1) == 0 ? 2 + (wave < 2 ? 1 : 0) : 0) + (issues_xa(g) ? 3 : 0);
+    };
+    auto step = [&](int g, const uint4* xs, const uint4* wp, uint4* xs2, uint4* wp2) {
+        if (g == 0) {
+            wait_vm_lds<0>();
+        } else {
+            switch (issued(g - 1)) {
+                case 4: wait_vm_lds<4>(); break;
+                case 6: wait_vm_lds<6>(); break;
+                case 7: wait_vm_lds<7>(); break;
+                case 9: wait_vm_lds<9>(); break;
+                case 10: wait_vm_lds<10>(); break;
+                default: wait_vm_lds<0>(); break;  // (not reached) safe fallback
+            }
         }
         __builtin_amdgcn_s_barrier();
-        const bool octet_end = (g & 7) == 7 || g == groups - 1;
-        uint2 bw[kNT];
-        if (octet_end) load_bias_words(g >> 3, bw);  // before this step's DMAs: waiting on it skips them
-        if (issues(g)) dma(g + 2, xs2, wt2, sb2);
+        if ((g & 7) == 0 && g > 0) bias();
         if (issues_xa(g)) dma_xa(g >> 3);
-        compute(xs, wt, sbl);
-        if (octet_end) bias(bw);
+        const bool pair = (g & 1) == 0;
+        compute(xs, wp, g & 1, [&](int t) {
+            if (t == 1 || t == 3 || t == 5 || t == 7) dma_x(g + 2, t >> 1, xs2);
+            if (pair && (t == 9 || t == 11)) dma_w((g + 2) >> 1, (t - 9) >> 1, wp2);
+            if (pair && t == 13 && wave < 2) dma_s((g + 2) >> 1, wp2);
+        });
     };
 
-    // prologue: groups 0 and 1, bias operands of octet 0
-    dma(0, g_xs0, g_wt0, g_sb0);
-    if (groups > 1) dma(1, g_xs1, g_wt1, g_sb1);
+    // prologue: x of groups 0 and 1, pair 0, bias operands of octet 0
+#pragma unroll
+    for (int part = 0; part < 4; ++part) {
+        dma_x(0, part, g_xs0);
+        dma_x(1, part, g_xs1);
+    }
+    dma_w(0, 0, g_wp0);
+    dma_w(0, 1, g_wp0);
+    if (wave < 2) dma_s(0, g_wp0);
     dma_xa(0);
     wait_vm<0>();
 
-    for (int g = 0; g < groups; g += 3) {
-        step(g, g_xs0, g_wt0, g_sb0, g_xs2, g_wt2, g_sb2);
-        if (g + 1 < groups) step(g + 1, g_xs1, g_wt1, g_sb1, g_xs0, g_wt0, g_sb0);
-        if (g + 2 < groups) step(g + 2, g_xs2, g_wt2, g_sb2, g_xs1, g_wt1, g_sb1);
+    // twelve steps per iteration: the x ring turns every 3 groups, the pair ring every 4
+    for (int g = 0; g < groups; g += 12) {
+        step(g, g_xs0, g_wp0, g_xs2, g_wp1);
+        if (g + 1 < groups) step(g + 1, g_xs1, g_wp0, g_xs0, g_wp1);
+        if (g + 2 < groups) step(g + 2, g_xs2, g_wp1, g_xs1, g_wp0);
+        if (g + 3 < groups) step(g + 3, g_xs0, g_wp1, g_xs2, g_wp0);
+        if (g + 4 < groups) step(g + 4, g_xs1, g_wp0, g_xs0, g_wp1);
+        if (g + 5 < groups) step(g + 5, g_xs2, g_wp0, g_xs1, g_wp1);
+        if (g + 6 < groups) step(g + 6, g_xs0, g_wp1, g_xs2, g_wp0);
+        if (g + 7 < groups) step(g + 7, g_xs1, g_wp1, g_xs0, g_wp0);
+        if (g + 8 < groups) step(g + 8, g_xs2, g_wp0, g_xs1, g_wp1);
+        if (g + 9 < groups) step(g + 9, g_xs0, g_wp0, g_xs2, g_wp1);
+        if (g + 10 < groups) step(g + 10, g_xs1, g_wp1, g_xs0, g_wp0);
+        if (g + 11 < groups) step(g + 11, g_xs2, g_wp1, g_xs1, g_wp0);
+    }
+    // the last octet's bias term.  Its operands were loaded at step 8o + 1, except for
+    // a last octet of one group (no such step): then they are loaded here, once every
+    // wave is past the previous octet's bias term.  The drain also lands the
+    // zero-reading loads past the last group before the workgroup ends.
+    {
+        const int o = (groups - 1) >> 3;
+        wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+        if (o > 0 && 8 * o + 1 >= groups) {
+            dma_xa(o);
+            wait_vm<0>();
+            __builtin_amdgcn_s_barrier();
+        }
+        bias();
     }
 
     // store: lane holds rows 4*kq + e of column col of each 16x16 tile

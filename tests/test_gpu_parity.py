@@ -217,7 +217,9 @@ def test_forward_many_row_blocks_per_workgroup(gpu_lib, m):
 
 # ---------------------------------------------------------------- prefill (GEMM path)
 
-@pytest.mark.parametrize("n,k,m", [(40, 384, 33), (256, 640, 300), (130, 320, 257), (512, 3840, 64)])
+# K = 64, 576, 1088: one group, and a last octet of one group (9, 17 groups)
+@pytest.mark.parametrize("n,k,m", [(40, 384, 33), (256, 640, 300), (130, 320, 257), (512, 3840, 64), (16, 64, 33),
+                                   (48, 576, 40), (130, 1088, 300)])
 @pytest.mark.parametrize("f32", [False, True])
 def test_gemm_small_shapes(gpu_lib, n, k, m, f32):
     """GEMM path (M >= 32): ragged M and N, odd group counts, outlier activations."""

@@ -31,21 +31,40 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP toolchain is required to build libgemma4_qmm")
 
 
+# device code flags shared by the library build and the assembly checks
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in arch VGPRs: the GEMM's fp32 accumulators are updated by
+    # VALU FMAs every group, which cannot read AGPRs
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
+]
+
+
+def device_asm(source: str) -> str:
+    """gfx950 assembly of one source file, compiled with the library's flags."""
+    import tempfile
+
+    with tempfile.TemporaryDirectory() as d:
+        out = os.path.join(d, "out.s")
+        cmd = [hipcc()] + DEVICE_FLAGS + ["--offload-device-only", "-S", "-I", os.path.join(ROOT, "include"),
+                                          "-o", out, os.path.join(CSRC, source)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc -S failed ({res.returncode}):\n{res.stderr}")
+        with open(out) as f:
+            return f.read()
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB_PATH + ".tmp"
-    cmd = [
-        hipcc(),
-        f"--offload-arch={ARCH}",
-        "-O3",
-        "-std=c++17",
+    cmd = [hipcc()] + DEVICE_FLAGS + [
         "-fPIC",
         "-shared",
         "-Wall",
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        # MFMA results in arch VGPRs: the GEMM's fp32 accumulators are updated by
-        # VALU FMAs every group, which cannot read AGPRs
-        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-I", os.path.join(ROOT, "include"),
         "-o", tmp,
     ] + [os.path.join(CSRC, s) for s in SOURCES]

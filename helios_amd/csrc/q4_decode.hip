@@ -346,17 +346,6 @@ inline Split choose_split(int gpairs, int mt) {
 
 constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950 LDS per CU (and per workgroup)
 
-int device_cus() {
-    static int cus[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        cus[dev] = v;
-    }
-    return cus[dev];
-}
 
 template <int MT>
 hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
@@ -391,6 +380,18 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, voi
 }
 
 }  // namespace
+
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cus[dev] = v;
+    }
+    return cus[dev];
+}
 
 hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
                          bool out_f32, const Layout& l, hipStream_t stream) {

@@ -43,11 +43,14 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // all outstanding DMAs before LDS reads it cannot tell apart from them (it keeps at
 // most eight DMA records), undoing the prefetch.  Ordering is this kernel's own: every
 // DMA'd slot is read only after an explicit vmcnt wait and a barrier.  M0 (the LDS
-// address) is an operand, so the compiler knows it is written; the s_nop is the one
-// wait state an M0 write needs before an LDS DMA.
+// address) is an operand, so the compiler knows it is written.  The compiler's hazard
+// checks cannot see into the asm, so it opens with the wait states the load may need:
+// 5 after a VALU write of an SGPR it reads (under register pressure the compiler
+// reloads resource and offset SGPRs from VGPR lanes with v_readlane right before it),
+// which also covers the 1 an M0 write needs.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, const void* lds, uint32_t voff, uint32_t soff = 0) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);  // LDS offset: low half of the generic address
-    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0)
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0)
                  : "memory");
 }
 
@@ -153,9 +156,14 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
                                                    const uint16_t* __restrict__ x, const uint4* __restrict__ xaug,
                                                    void* __restrict__ y, int m_rows, int n_rows, int k, int groups,
                                                    int gpairs, int mtiles, int ntiles, int octets, uint32_t tile_bytes,
-                                                   uint32_t sb_bytes) {
+                                                   uint32_t sb_bytes, int g_split, long split_stride) {
     int mt, nt;
     tile_of((int)blockIdx.x, (int)gridDim.x, mtiles, ntiles, mt, nt);
+    // split of K: groups [g_begin, g_end), whole octets; with several splits each
+    // writes fp32 partial sums to its own [M, N] plane of y
+    const int g_begin = (int)blockIdx.y * g_split;
+    const int g_end = groups - g_begin < g_split ? groups : g_begin + g_split;
+    const int p_end = (g_end + 1) >> 1;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int col = lane & 15;
@@ -172,8 +180,6 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, sb_bytes);
     const __amdgpu_buffer_rsrc_t ars = make_rsrc(xaug, (uint32_t)(mtiles * 16 * octets) * 1024u);
 
-    // ---- DMA issue, per wave and group: x 4, weight words 4, scale words 1; bias
-    // operands 2 per octet ----
     // DMA issue.  Per lane, the offsets are fixed for the whole K loop (rows past M and
     // row blocks past N at kOutOfRange) and computed once here; the step moves them by
     // a scalar offset (group x 128 bytes of x, pair x 1 KiB of tiles, pair x 128 bytes
@@ -204,13 +210,13 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         sv = rb < nblocks ? (uint32_t)rb * (uint32_t)gpairs * 128u + (uint32_t)(lane & 7) * 16u : kOutOfRange;
     }
     auto dma_x = [&](int g, int part, uint4* xdst) {
-        dma16(g < groups ? xrs : zrs, xdst + (8 * part + wave) * 64, xv[part], (uint32_t)g * 128u);
+        dma16(g < g_end ? xrs : zrs, xdst + (8 * part + wave) * 64, xv[part], (uint32_t)g * 128u);
     };
     auto dma_w = [&](int p, int part, uint4* wdst) {
-        dma16(p < gpairs ? trs : zrs, wdst + (2 * wave + part) * 64, wv[part], (uint32_t)p * 1024u);
+        dma16(p < p_end ? trs : zrs, wdst + (2 * wave + part) * 64, wv[part], (uint32_t)p * 1024u);
     };
     auto dma_s = [&](int p, uint4* wdst) {
-        dma16(p < gpairs ? srs : zrs, wdst + kWPair + 64 * wave, sv, (uint32_t)p * 128u);
+        dma16(p < p_end ? srs : zrs, wdst + kWPair + 64 * wave, sv, (uint32_t)p * 128u);
     };
     auto dma_xa_part = [&](int o, int u) {
         const int m16 = 2 * wave + u;
@@ -317,12 +323,12 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     // read of the previous octet's); (4) multiply, with the loads for group g+2 (and
     // pair (g+2)/2) spread through the products.  Every step issues the same loads
     // (past the end they read zeros), so the counts are fixed.
-    auto issues_xa = [&](int g) { return (g & 7) == 1 && g > 1; };
+    auto issues_xa = [&](int g) { return (g & 7) == 1 && g > g_begin + 1; };
     auto issued = [&](int g) {  // loads this wave issues at step g
         return 4 + ((g & 1) == 0 ? 2 + (wave < 2 ? 1 : 0) : 0) + (issues_xa(g) ? 3 : 0);
     };
     auto step = [&](int g, const uint4* xs, const uint4* wp, uint4* xs2, uint4* wp2) {
-        if (g == 0) {
+        if (g == g_begin) {
             wait_vm_lds<0>();
         } else {
             switch (issued(g - 1)) {
@@ -335,7 +341,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
             }
         }
         __builtin_amdgcn_s_barrier();
-        if ((g & 7) == 0 && g > 0) bias();
+        if ((g & 7) == 0 && g > g_begin) bias();
         if (issues_xa(g)) dma_xa(g >> 3);
         const bool pair = (g & 1) == 0;
         compute(xs, wp, g & 1, [&](int t) {
@@ -345,42 +351,43 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         });
     };
 
-    // prologue: x of groups 0 and 1, pair 0, bias operands of octet 0
+    // prologue: x of the split's first two groups, its first pair, bias operands of its
+    // first octet
 #pragma unroll
     for (int part = 0; part < 4; ++part) {
-        dma_x(0, part, g_xs0);
-        dma_x(1, part, g_xs1);
+        dma_x(g_begin, part, g_xs0);
+        dma_x(g_begin + 1, part, g_xs1);
     }
-    dma_w(0, 0, g_wp0);
-    dma_w(0, 1, g_wp0);
-    if (wave < 2) dma_s(0, g_wp0);
-    dma_xa(0);
+    dma_w(g_begin >> 1, 0, g_wp0);
+    dma_w(g_begin >> 1, 1, g_wp0);
+    if (wave < 2) dma_s(g_begin >> 1, g_wp0);
+    dma_xa(g_begin >> 3);
     wait_vm<0>();
 
     // twelve steps per iteration: the x ring turns every 3 groups, the pair ring every 4
-    for (int g = 0; g < groups; g += 12) {
+    for (int g = g_begin; g < g_end; g += 12) {
         step(g, g_xs0, g_wp0, g_xs2, g_wp1);
-        if (g + 1 < groups) step(g + 1, g_xs1, g_wp0, g_xs0, g_wp1);
-        if (g + 2 < groups) step(g + 2, g_xs2, g_wp1, g_xs1, g_wp0);
-        if (g + 3 < groups) step(g + 3, g_xs0, g_wp1, g_xs2, g_wp0);
-        if (g + 4 < groups) step(g + 4, g_xs1, g_wp0, g_xs0, g_wp1);
-        if (g + 5 < groups) step(g + 5, g_xs2, g_wp0, g_xs1, g_wp1);
-        if (g + 6 < groups) step(g + 6, g_xs0, g_wp1, g_xs2, g_wp0);
-        if (g + 7 < groups) step(g + 7, g_xs1, g_wp1, g_xs0, g_wp0);
-        if (g + 8 < groups) step(g + 8, g_xs2, g_wp0, g_xs1, g_wp1);
-        if (g + 9 < groups) step(g + 9, g_xs0, g_wp0, g_xs2, g_wp1);
-        if (g + 10 < groups) step(g + 10, g_xs1, g_wp1, g_xs0, g_wp0);
-        if (g + 11 < groups) step(g + 11, g_xs2, g_wp1, g_xs1, g_wp0);
+        if (g + 1 < g_end) step(g + 1, g_xs1, g_wp0, g_xs0, g_wp1);
+        if (g + 2 < g_end) step(g + 2, g_xs2, g_wp1, g_xs1, g_wp0);
+        if (g + 3 < g_end) step(g + 3, g_xs0, g_wp1, g_xs2, g_wp0);
+        if (g + 4 < g_end) step(g + 4, g_xs1, g_wp0, g_xs0, g_wp1);
+        if (g + 5 < g_end) step(g + 5, g_xs2, g_wp0, g_xs1, g_wp1);
+        if (g + 6 < g_end) step(g + 6, g_xs0, g_wp1, g_xs2, g_wp0);
+        if (g + 7 < g_end) step(g + 7, g_xs1, g_wp1, g_xs0, g_wp0);
+        if (g + 8 < g_end) step(g + 8, g_xs2, g_wp0, g_xs1, g_wp1);
+        if (g + 9 < g_end) step(g + 9, g_xs0, g_wp0, g_xs2, g_wp1);
+        if (g + 10 < g_end) step(g + 10, g_xs1, g_wp1, g_xs0, g_wp0);
+        if (g + 11 < g_end) step(g + 11, g_xs2, g_wp1, g_xs1, g_wp0);
     }
     // the last octet's bias term.  Its operands were loaded at step 8o + 1, except for
     // a last octet of one group (no such step): then they are loaded here, once every
     // wave is past the previous octet's bias term.  The drain also lands the
     // zero-reading loads past the last group before the workgroup ends.
     {
-        const int o = (groups - 1) >> 3;
+        const int o = (g_end - 1) >> 3;
         wait_vm<0>();
         __builtin_amdgcn_s_barrier();
-        if (o > 0 && 8 * o + 1 >= groups) {
+        if (o > (g_begin >> 3) && 8 * o + 1 >= g_end) {
             dma_xa(o);
             wait_vm<0>();
             __builtin_amdgcn_s_barrier();
@@ -400,7 +407,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
                 if (m < m_rows && n < n_rows) {
                     const long o = (long)m * n_rows + n;
                     if (F32OUT)
-                        static_cast<float*>(y)[o] = acc[i][j][e];
+                        static_cast<float*>(y)[(long)blockIdx.y * split_stride + o] = acc[i][j][e];
                     else
                         static_cast<uint16_t*>(y)[o] = f32_to_bf16(acc[i][j][e]);
                 }
@@ -409,20 +416,103 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     }
 }
 
+// y = sum over splits of the fp32 partial planes, in split order (deterministic)
+template <bool F32OUT>
+__global__ void split_reduce_kernel(const float* __restrict__ part, void* __restrict__ y, long elems, int splits) {
+    const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i >= elems) return;
+    if (i + 4 <= elems) {
+        f32x4 v = *reinterpret_cast<const f32x4*>(part + i);
+        for (int s = 1; s < splits; ++s) {
+            const f32x4 w = *reinterpret_cast<const f32x4*>(part + (long)s * elems + i);
+            v[0] += w[0];
+            v[1] += w[1];
+            v[2] += w[2];
+            v[3] += w[3];
+        }
+        if (F32OUT) {
+            float* yf = static_cast<float*>(y) + i;
+            if ((reinterpret_cast<uintptr_t>(yf) & 15) == 0) {
+                *reinterpret_cast<f32x4*>(yf) = v;
+            } else {
+                yf[0] = v[0];
+                yf[1] = v[1];
+                yf[2] = v[2];
+                yf[3] = v[3];
+            }
+        } else {
+            uint16_t* yb = static_cast<uint16_t*>(y) + i;
+            const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+            const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+            if ((reinterpret_cast<uintptr_t>(yb) & 7) == 0) {
+                *reinterpret_cast<uint2*>(yb) = make_uint2(lo, hi);
+            } else {
+                yb[0] = (uint16_t)lo;
+                yb[1] = (uint16_t)(lo >> 16);
+                yb[2] = (uint16_t)hi;
+                yb[3] = (uint16_t)(hi >> 16);
+            }
+        }
+    } else {
+        for (long j = i; j < elems; ++j) {
+            float v = part[j];
+            for (int s = 1; s < splits; ++s) v += part[(long)s * elems + j];
+            if (F32OUT)
+                static_cast<float*>(y)[j] = v;
+            else
+                static_cast<uint16_t*>(y)[j] = f32_to_bf16(v);
+        }
+    }
+}
+
 }  // namespace
 
-size_t gemm_workspace_bytes(int m, const Layout& l) {
+// Split of K over workgroups when the output tiles alone leave CUs idle: the count
+// (whole octets per split) minimises rounds-of-workgroups x octets-per-split, plus
+// the partial sums' extra traffic.
+GemmPlan plan_gemm(int m, const Layout& l) {
+    GemmPlan p;
+    const int octets = (l.g + 7) / 8;
+    const long tiles = (long)((m + kBM - 1) / kBM) * ((l.n + kBN - 1) / kBN);
+    const long cus = device_cus();
+    const double step_us = 2.0, bytes_per_us = 4.0e6;
+    double best = 0;
+    for (int s = 1; s <= octets && s <= kMaxSplits; ++s) {
+        const int per = (octets + s - 1) / s;
+        const int used = (octets + per - 1) / per;  // splits that get work
+        if (used != s) continue;
+        const size_t part = s > 1 ? (size_t)s * m * l.n * 4 : 0;
+        if (part > kMaxPartialBytes) break;
+        const double rounds = (double)((tiles * s + cus - 1) / cus);
+        const double t = rounds * per * 8 * step_us + (s > 1 ? 3.0 + 2.0 * part / bytes_per_us : 0.0);
+        if (s == 1 || t < best) {
+            best = t;
+            p.splits = s;
+            p.g_split = per * 8;
+            p.part_bytes = part;
+        }
+    }
     const size_t m16 = ((size_t)m + kBM - 1) / kBM * (kBM / 16);
-    const size_t octets = ((size_t)l.g + 7) / 8;
-    return m16 * octets * 64 * 16;
+    p.xaug_bytes = m16 * octets * 64 * 16;
+    return p;
+}
+
+size_t gemm_workspace_bytes(int m, const Layout& l) {
+    const GemmPlan p = plan_gemm(m, l);
+    return p.xaug_bytes + p.part_bytes;
 }
 
 hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, bool out_f32,
                        const Layout& l, void* workspace, hipStream_t stream) {
+    const GemmPlan plan = plan_gemm(m, l);
     const int octets = (l.g + 7) / 8;
     const int mtiles = (m + kBM - 1) / kBM;
     const int ntiles = (l.n + kBN - 1) / kBN;
     uint4* xaug = static_cast<uint4*>(workspace);
+    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.xaug_bytes);
+    if (l.tile_bytes() > kMaxBufferBytes || l.sb_bytes() > kMaxBufferBytes ||
+        (size_t)m * l.k * 2 > kMaxBufferBytes || plan.xaug_bytes > kMaxBufferBytes)
+        return hipErrorInvalidValue;
     {
         const long total = (long)mtiles * (kBM / 16) * octets * 64;
         const int block = 256;
@@ -431,17 +521,30 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    const dim3 grid((unsigned)(mtiles * ntiles)), block(64 * kWaves);
-    if (l.tile_bytes() > kMaxBufferBytes || l.sb_bytes() > kMaxBufferBytes ||
-        (size_t)m * l.k * 2 > kMaxBufferBytes)
-        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(mtiles * ntiles), (unsigned)plan.splits), block(64 * kWaves);
     const uint32_t tb = (uint32_t)l.tile_bytes(), sbb = (uint32_t)l.sb_bytes();
+    const long elems = (long)m * l.n;
+    if (plan.splits > 1) {
+        hipLaunchKernelGGL((gemm_kernel<true>), grid, block, 0, stream, tiles, sb, x, xaug, (void*)part, m, l.n, l.k, l.g,
+                           l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, elems);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int rblock = 256;
+        const unsigned rgrid = (unsigned)(((elems + 3) / 4 + rblock - 1) / rblock);
+        if (out_f32)
+            hipLaunchKernelGGL((split_reduce_kernel<true>), dim3(rgrid), dim3(rblock), 0, stream, part, y, elems,
+                               plan.splits);
+        else
+            hipLaunchKernelGGL((split_reduce_kernel<false>), dim3(rgrid), dim3(rblock), 0, stream, part, y, elems,
+                               plan.splits);
+        return hipGetLastError();
+    }
     if (out_f32)
         hipLaunchKernelGGL((gemm_kernel<true>), grid, block, 0, stream, tiles, sb, x, xaug, y, m, l.n, l.k, l.g, l.gp,
-                           mtiles, ntiles, octets, tb, sbb);
+                           mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L);
     else
         hipLaunchKernelGGL((gemm_kernel<false>), grid, block, 0, stream, tiles, sb, x, xaug, y, m, l.n, l.k, l.g, l.gp,
-                           mtiles, ntiles, octets, tb, sbb);
+                           mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L);
     return hipGetLastError();
 }
 

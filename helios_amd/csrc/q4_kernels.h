@@ -40,8 +40,21 @@ hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x,
                          bool out_f32, const Layout& l, hipStream_t stream);
 
 // Prefill path: fp32-exact factored GEMM on the matrix cores.  `workspace` holds the
-// group sums of x (gemm_workspace_bytes(m, l) bytes, device memory, 16-byte aligned).
+// group sums of x and, when K is split over workgroups, the fp32 partial sums
+// (gemm_workspace_bytes(m, l) bytes, device memory, 16-byte aligned).
+struct GemmPlan {
+    int splits = 1;          // workgroups along K per output tile
+    int g_split = 0;         // groups per split (whole octets)
+    size_t xaug_bytes = 0;   // group sums of x
+    size_t part_bytes = 0;   // splits x M x N fp32 partial sums (0 when unsplit)
+};
+constexpr int kMaxSplits = 16;
+constexpr size_t kMaxPartialBytes = (size_t)1 << 30;
+GemmPlan plan_gemm(int m, const Layout& l);
 size_t gemm_workspace_bytes(int m, const Layout& l);
+
+// Compute units of the current device (cached per device).
+int device_cus();
 hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, bool out_f32,
                        const Layout& l, void* workspace, hipStream_t stream);
 

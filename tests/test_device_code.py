@@ -1,0 +1,74 @@
+"""Checks on the compiled gfx950 code of the GEMM (CPU only: hipcc cross-compiles).
+
+The GEMM issues its LDS DMAs (`buffer_load_dwordx4 ... lds`) from inline asm, which
+the compiler's hazard recognizer cannot see into.  A VALU write of an SGPR (for
+example a `v_readlane` reloading a spilled resource or offset SGPR) needs 5 wait
+states before a vector memory instruction reads that SGPR; the asm supplies them
+itself.  Missing wait states made loads use stale offsets (wrong results at
+k/q_proj M=512 in an earlier build), so every such pair is checked here, along with
+the properties the kernel's manual ordering relies on.
+"""
+
+import re
+
+import pytest
+
+from helios_amd import build as hbuild
+
+WAIT_STATES = 5
+
+
+def _kernels(asm: str):
+    for m in re.finditer(r"\n(_ZN\S*gemm_kernel\S*):[^\n]*\n", asm):
+        body = asm[m.end():asm.index("s_endpgm", m.end())]
+        lines = [l.strip() for l in body.splitlines()
+                 if l.strip() and not l.strip().startswith((";", "."))]
+        yield m.group(1), lines
+
+
+def _sgprs(tok: str):
+    m = re.match(r"s\[(\d+):(\d+)\]$", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"s(\d+)$", tok)
+    if m:
+        return {int(m.group(1))}
+    return {"m0"} if tok == "m0" else set()
+
+
+@pytest.fixture(scope="module")
+def gemm_asm():
+    return hbuild.device_asm("q4_gemm.hip")
+
+
+def test_lds_dma_sgpr_hazards_covered(gemm_asm):
+    kernels = list(_kernels(gemm_asm))
+    assert len(kernels) == 2  # bf16 and fp32 outputs
+    for name, lines in kernels:
+        dmas = 0
+        for i, line in enumerate(lines):
+            if not (line.startswith("buffer_load_dwordx4") and " lds" in line):
+                continue
+            dmas += 1
+            used = set().union(*[_sgprs(t.strip(",")) for t in line.split()[1:]]) | {"m0"}
+            waits, j = 0, i - 1
+            while j >= 0 and waits < WAIT_STATES:
+                op = lines[j].split()[0]
+                if op == "s_nop":
+                    waits += int(lines[j].split()[1]) + 1
+                else:
+                    if op.startswith("v_"):
+                        dst = lines[j].split()[1].rstrip(",")
+                        assert not (_sgprs(dst) & used), f"{name}: {lines[j]!r} feeds {line!r} within {waits} wait states"
+                    waits += 1
+                j -= 1
+        assert dmas > 0, name
+
+
+def test_no_spills_and_lds_budget(gemm_asm):
+    # scratch spills would be VMEM loads counted by the kernel's manual vmcnt waits
+    for field in ("vgpr_spill_count", "private_segment_fixed_size"):
+        vals = [int(v) for v in re.findall(rf"\.{field}:\s+(\d+)", gemm_asm)]
+        assert vals and max(vals) == 0, (field, vals)
+    lds = [int(v) for v in re.findall(r"\.group_segment_fixed_size:\s+(\d+)", gemm_asm)]
+    assert max(lds) <= 160 * 1024

@@ -284,3 +284,32 @@ def test_gemm_prefill_chain_m2048_geglu(gpu_lib):
     d = lins["down_proj"].forward(dev_x(h))
     torch.cuda.synchronize()
     assert_close(d[rt], C.qmm_f64(np.ascontiguousarray(h[rows]), *tri["down_proj"]), "down m=2048")
+
+
+@pytest.mark.parametrize("f32", [False, True])
+def test_gemm_split_k_deterministic_and_unaligned_y(gpu_lib, f32):
+    """k_proj at M=512 runs with K split over workgroups (fp32 partial planes summed in
+    a fixed order): repeated calls give identical bits, and an output that is only
+    element-aligned (not 16-byte aligned) gets the same values."""
+    import torch
+
+    n, k = PROJ["k_proj"]
+    m = 512
+    wq, s, b = A.make_weights(n, k, seed=21)
+    x_bits = A.make_activations(m, k, seed=22, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    x = dev_x(x_bits)
+    dt = torch.float32 if f32 else torch.bfloat16
+    y1 = lin.forward(x, out_dtype=dt)
+    y2 = lin.forward(x, out_dtype=dt)
+    assert torch.equal(y1, y2)
+    buf = torch.zeros(m * n + 8, dtype=dt, device="cuda")
+    lin.forward_raw(x.data_ptr(), m, buf.data_ptr() + buf.element_size(), f32=f32,
+                    stream_ptr=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    y3 = buf[1:1 + m * n].view(m, n)
+    assert torch.equal(y1, y3)
+    assert buf[0].item() == 0 and torch.count_nonzero(buf[1 + m * n:]).item() == 0
+    rows = np.arange(0, m, 37)
+    assert_close(y1[rows], C.qmm_f64(x_bits[rows], wq, s, b), "k_proj m=512 split-K")
+    lin.close()

@@ -63,6 +63,9 @@ SEED_BASE = 20260630
 ROTATE_BYTES = 512 << 20
 COPY_BYTES = 1 << 30
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_decode_m1_traffic.json")
+# the kernel that runs the fused gate|up projection at M = 1 (30720 rows: one wave per
+# 16-row block)
+DOM_KERNEL = "decode_rows_kernel"
 
 
 def algo_bytes(m: int, n: int, k: int, y_bytes: int = 2) -> int:
@@ -226,7 +229,7 @@ def summarize_profiles(stats_dir: str, fetch_dir: str, write_dir: str, line_file
             raise SystemExit(f"no {counter} rows for the kernel")
         return sum(vals) / len(vals), len(vals)
 
-    is_dom = lambda n: "decode_stream_kernel" in n  # noqa: E731
+    is_dom = lambda n: DOM_KERNEL in n  # noqa: E731
     is_copy = lambda n: "copy" in n.lower()  # noqa: E731
     fetch_rows = _csv_rows(fetch_dir, "counter_collection.csv")
     write_rows = _csv_rows(write_dir, "counter_collection.csv")
@@ -358,7 +361,7 @@ def main() -> int:
           for k in {k for _, _, k in LAYER}}
     n_gu, k_gu = fused_nk["gate_up_proj"]
     gu_bytes = algo_bytes(1, n_gu, k_gu)
-    gu_kernel = f"decode_stream_kernel<1,4> gate|up fused N={n_gu} K={k_gu} M=1"
+    gu_kernel = f"{DOM_KERNEL}<1,4,3> gate|up fused N={n_gu} K={k_gu} M=1"
 
     if args.roofline_only:
         us_gu = kernel_us(torch, Q, fused["gate_up_proj"], 1, k_gu, n_gu, xs[k_gu])

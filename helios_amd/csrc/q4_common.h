@@ -113,16 +113,141 @@ __device__ __forceinline__ uint32_t word_nibble(uint32_t u, int i) {
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
 
-// fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet: the hardware conversion
+// (v_cvt_pk_bf16_f32), branch-free.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+// ---------------------------------------------------------------------------
+// Output stage: plain projection (bf16 or fp32) or a gate|up pair with GeGLU
+// ---------------------------------------------------------------------------
+// A gate|up pair is tiled as one projection whose 16-row block j holds gate rows
+// 8j..8j+7 in columns 0..7 and the same up rows in columns 8..15, so each output
+// h[m, 8j + c] = geglu(gate, up) combines columns c and c + 8 of one block.
+enum OutMode : int {
+    kOutBf16 = 0,       // y bf16 [M, N]
+    kOutF32 = 1,        // y fp32 [M, N] (also the split-K partial planes)
+    kOutGegluBf16 = 2,  // h bf16 [M, F], the bf16 model dtype's GeGLU
+    kOutGegluF32 = 3,   // h fp32 [M, F], the float32 override's GeGLU
+};
+
+__device__ __forceinline__ float round_bf16(float v) { return (float)(__bf16)v; }
+
+// GeGLU of native_model.cc:378-386, op by op as the reference's array ops evaluate
+// it: 0.5*g*(1+tanh(c1*(g+c2*g^3)))*up, each op one fp32 operation.  In the bf16
+// model dtype the qmm outputs, the constants (model_scalar) and every intermediate
+// are bf16, so each op's result is rounded to bf16; under the float32 override all
+// stay fp32.  Contraction is off: an FMA would skip the rounding of a product (hipcc
+// contracts by default, also across the header's __fmul_rn / __fadd_rn, which are
+// plain operators).  g^3 is g*g*g: exact in fp32 for a bf16 g (at most 24
+// significant bits), and within an ulp of the reference's pow(g, 3) for an fp32 g.
+__device__ __forceinline__ float geglu_bf16(float gate, float up) {
+#pragma clang fp contract(off)
+    const float c_tanh = 0.796875f;           // bf16(0.7978845608028654)
+    const float c_cubic = 0.044677734375f;    // bf16(0.044715)
+    const float g = round_bf16(gate), u = round_bf16(up);
+    const float g3 = round_bf16(g * g * g);
+    const float a = round_bf16(g + round_bf16(c_cubic * g3));
+    const float t = round_bf16(tanhf(round_bf16(c_tanh * a)));
+    const float gelu = round_bf16(round_bf16(0.5f * g) * round_bf16(1.0f + t));
+    return round_bf16(gelu * u);
+}
+
+__device__ __forceinline__ float geglu_f32(float g, float u) {
+#pragma clang fp contract(off)
+    const float c_tanh = 0.7978845608028654f, c_cubic = 0.044715f;
+    const float g3 = g * g * g;
+    const float a = g + c_cubic * g3;
+    const float t = tanhf(c_tanh * a);
+    const float gelu = (0.5f * g) * (1.0f + t);
+    return gelu * u;
+}
+
+// The value of lane (l ^ 8) within each 16-lane row (DPP row_ror:8).  Every lane of
+// the wave must execute it.
+__device__ __forceinline__ float row_swap8(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+}
+
+// Writes accumulator v of output row m, column 16*rb + col.  All lanes of the wave
+// call it together (the GeGLU modes read the partner column from lane col ^ 8);
+// n_rows bounds a plain projection's N, n_out a pair's F.
+__device__ __forceinline__ void store_out(void* y, int mode, int m, int m_rows, int rb, int col, int n_rows,
+                                          int n_out, float v) {
+    if (mode < kOutGegluBf16) {
+        const int n = rb * 16 + col;
+        if (m < m_rows && n < n_rows) {
+            const long o = (long)m * n_rows + n;
+            if (mode == kOutF32)
+                static_cast<float*>(y)[o] = v;
+            else
+                static_cast<uint16_t*>(y)[o] = f32_to_bf16(v);
+        }
+    } else {
+        const float up = row_swap8(v);
+        const int hn = rb * 8 + col;
+        if (col < 8 && m < m_rows && hn < n_out) {
+            const long o = (long)m * n_out + hn;
+            if (mode == kOutGegluF32)
+                static_cast<float*>(y)[o] = geglu_f32(v, up);
+            else
+                static_cast<uint16_t*>(y)[o] = f32_to_bf16(geglu_bf16(v, up));
+        }
+    }
 }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// LDS DMA (buffer_load ... lds) issued from asm, and explicit vmcnt waits
+// ---------------------------------------------------------------------------
+// 16-byte-per-lane DMA into LDS: lane i's 16 bytes land at lds + 16 i, read from
+// voff + soff.  Only voff is checked against the buffer's size (a resource of size
+// 0 reads zeros for any offset); callers keep voff + soff inside the buffer for
+// in-range lanes and put the rest at kOutOfRange.  Issued as
+// inline asm, so the compiler does not track it: it would otherwise insert waits for
+// all outstanding DMAs before LDS reads it cannot tell apart from them (it keeps at
+// most eight DMA records), undoing the prefetch.  Ordering is this kernel's own: every
+// DMA'd slot is read only after an explicit vmcnt wait and a barrier.  M0 (the LDS
+// address) is an operand, so the compiler knows it is written.  The compiler's hazard
+// checks cannot see into the asm, so it opens with the wait states the load may need:
+// 5 after a VALU write of an SGPR it reads (under register pressure the compiler
+// reloads resource and offset SGPRs from VGPR lanes with v_readlane right before it),
+// which also covers the 1 an M0 write needs.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, const void* lds, uint32_t voff, uint32_t soff = 0) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);  // LDS offset: low half of the generic address
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0)
+                 : "memory");
+}
+
+// s_waitcnt with vmcnt(n) only (expcnt / lgkmcnt left free), n < 64
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+    asm volatile("" ::: "memory");  // the builtin is not a memory operation: keep loads after it
+}
+// the same plus lgkmcnt(0): this wave's LDS reads have returned
+template <int N>
+__device__ __forceinline__ void wait_vm_lds() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+    asm volatile("" ::: "memory");
+}
+
+// lgkmcnt(0) only: this wave's LDS reads have returned
+__device__ __forceinline__ void wait_lds() {
+    __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+    asm volatile("" ::: "memory");
+}
+
+// s_barrier without __syncthreads' fence (which would wait for every outstanding
+// load); the empty asm keeps LDS accesses on their side of it for the compiler
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 }  // namespace q4

@@ -34,7 +34,7 @@ namespace {
 template <int MT, int GPW, bool XLDS>
 __global__ __launch_bounds__(1024) void decode_kernel(
     const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x,
-    void* __restrict__ y, int m_rows, int n_rows, int k, int gpairs, int waves, int out_f32) {
+    void* __restrict__ y, int m_rows, int n_rows, int k, int gpairs, int waves, int out_mode, int n_out) {
     constexpr int R = MT < 4 ? MT : 4;
     extern __shared__ uint4 xs_lds[];  // XLDS: x[M][K] as bf16, 16 B per entry
     const int rb = blockIdx.x;
@@ -150,16 +150,18 @@ __global__ __launch_bounds__(1024) void decode_kernel(
         for (int w = 0; w < waves; ++w) v += red[w][t];
         const int r = t >> 6;
         const int l = t & 63;
-        const int mrow = 4 * (l >> 4) + r;
-        const int n = rb * 16 + (l & 15);
-        if (mrow < m_rows && n < n_rows) {
-            const long o = (long)mrow * n_rows + n;
-            if (out_f32)
-                static_cast<float*>(y)[o] = v;
-            else
-                static_cast<uint16_t*>(y)[o] = f32_to_bf16(v);
-        }
+        store_out(y, out_mode, 4 * (l >> 4) + r, m_rows, rb, l & 15, n_rows, n_out, v);
     }
+}
+
+// A chunk's scale/bias words (4 pairs x 16 columns x 8 bytes, contiguous) arrive with
+// one 8-byte load per lane: lane (col, kq) holds pair kq of column col.  Pair i of a
+// lane's own column is fetched from lane 16 i + col through the LDS crossbar.  (Four
+// loads of 8 bytes, each address shared by 4 lanes, cost the memory pipeline about
+// 13% of the lm_head's time; permutes do not touch it.)
+__device__ __forceinline__ uint32_t scale_word(uint2 sv, int pair, int gi, int col) {
+    const int src = (16 * pair + col) * 4;
+    return (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)(gi ? sv.y : sv.x));
 }
 
 // Persistent streaming variant for M <= 4 (x staged in LDS).  Each workgroup walks
@@ -177,7 +179,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(
 template <int MT, int GPW>
 __global__ __launch_bounds__(512) void decode_stream_kernel(
     const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x,
-    void* __restrict__ y, int m_rows, int n_rows, int k, int gpairs, int nblocks, int waves, int out_f32) {
+    void* __restrict__ y, int m_rows, int n_rows, int k, int gpairs, int nblocks, int waves, int out_mode, int n_out) {
     constexpr int R = MT < 4 ? MT : 4;
     constexpr int kPad = GPW * 128;  // zero columns after each x row
     extern __shared__ uint4 lds[];
@@ -197,22 +199,26 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
     const int groups = k >> 6;
     float* negx = reinterpret_cast<float*>(lds + m_rows * row16);  // [2 * (gpairs + GPW)][16]
 
+    static_assert(GPW == 4, "one 8-byte load per lane covers a chunk's scale words");
     uint4 wa[GPW], wb[GPW];
-    uint2 sa[GPW], sbv2[GPW];
-    auto issue = [&](uint4* wv, uint2* sv, int c) {
-        const int rb = (int)blockIdx.x + (c / passes) * (int)gridDim.x;
+    uint2 sa, sbv2;  // scale words of a chunk: lane (col, kq) holds pair kq, column col
+    // Chunks past the workgroup's last are issued too, against an empty range (zeros,
+    // no memory traffic): every loop iteration then issues the same loads, which keeps
+    // the compiler's wait counts exact (a conditional issue makes it wait for both
+    // buffers before using either, draining the prefetch).
+    auto issue = [&](uint4* wv, uint2& sv, int c) {
+        const bool live = c < chunks;
+        const int rb = live ? (int)blockIdx.x + (c / passes) * (int)gridDim.x : 0;
         const int pass = c % passes;
         const int gpb = gp0 + pass * GPW;
         const int left = cnt - pass * GPW;
-        const int n_in = left < GPW ? left : GPW;
+        const int n_in = !live ? 0 : left < GPW ? left : GPW;
         const long first = (long)rb * gpairs + gpb;
         const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * 64, (uint32_t)n_in * 1024u);
         const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * 16, (uint32_t)n_in * 128u);
 #pragma unroll
-        for (int i = 0; i < GPW; ++i) {
-            wv[i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * 1024));
-            sv[i] = buffer_load8<kNonTemporal>(srs, (uint32_t)(col * 8 + i * 128));
-        }
+        for (int i = 0; i < GPW; ++i) wv[i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * 1024));
+        sv = buffer_load8<kNonTemporal>(srs, (uint32_t)(lane * 8));  // the chunk's 512 contiguous bytes
     };
 
     // x -> LDS (loads issued before any weight load), zero padding after each row,
@@ -223,17 +229,15 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
         const int rowc = k >> 3;
         const int nthr = waves * 64;
         const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)k * 2u);
-        for (int c0 = 0; c0 < xchunks; c0 += 4 * nthr) {
-            uint4 tmp[4];
+        uint4 tmp[4];
+        auto load_x = [&](int c0) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = c0 + u * nthr + (int)threadIdx.x;
                 tmp[u] = buffer_load16(xrs, c < xchunks ? (uint32_t)c * 16u : kOutOfRange);
             }
-            if (c0 == 0) {  // both weight buffers requested before anything waits
-                if (chunks > 0) issue(wa, sa, 0);
-                if (chunks > 1) issue(wb, sbv2, 1);
-            }
+        };
+        auto store_x = [&](int c0) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = c0 + u * nthr + (int)threadIdx.x;
@@ -249,6 +253,16 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
                 sum += __shfl_xor(sum, 4);
                 if (c < xchunks && (lane & 7) == 0) negx[(cr >> 3) * 16 + row] = -sum;
             }
+        };
+        // first batch of x, then both weight buffers, then the batch is stored: in
+        // straight-line code, so waiting for x leaves the weight loads in flight
+        load_x(0);
+        issue(wa, sa, 0);
+        issue(wb, sbv2, 1);
+        store_x(0);
+        for (int c0 = 4 * nthr; c0 < xchunks; c0 += 4 * nthr) {  // rows past 2048 elements per thread
+            load_x(c0);
+            store_x(c0);
         }
         for (int c = threadIdx.x; c < m_rows * (kPad >> 3); c += nthr)
             lds[(c / (kPad >> 3)) * row16 + rowc + (c % (kPad >> 3))] = make_uint4(0, 0, 0, 0);
@@ -261,17 +275,19 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
     f32x4 acc = zero;
     int parity = 0;
-    auto compute = [&](const uint4* wv, const uint2* sv, int c) {
+    auto compute = [&](const uint4* wv, const uint2 sv, int c) {
         const int pass = c % passes;
         const int gpb = gp0 + pass * GPW;
         const uint4* xp = lds + arow * row16 + kq + gpb * 16;  // x operand, pair 0
         const float* np = negx + gpb * 32 + 4 * kq;              // -X table, pair 0
+        // operands are read per product (not gathered for the whole chunk first): this
+        // keeps the kernel within 128 VGPRs, so two 8-wave workgroups fit on a CU
 #pragma unroll
         for (int i = 0; i < GPW; ++i) {
 #pragma unroll
             for (int gi = 0; gi < 2; ++gi) {
-                const bf16x8 x0 = __builtin_bit_cast(bf16x8, xp[i * 16 + gi * 8]);
-                const bf16x8 x1 = __builtin_bit_cast(bf16x8, xp[i * 16 + gi * 8 + 4]);
+                const bf16x8 xo0 = __builtin_bit_cast(bf16x8, xp[i * 16 + gi * 8]);
+                const bf16x8 xo1 = __builtin_bit_cast(bf16x8, xp[i * 16 + gi * 8 + 4]);
                 f32x4 xn;
                 if constexpr (R == 1) {
                     xn = zero;
@@ -279,11 +295,11 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
                 } else {
                     xn = *reinterpret_cast<const f32x4*>(np + i * 32 + gi * 16);
                 }
+                const uint32_t sbw = scale_word(sv, i, gi, col);
                 const bf16x8 b0 = expand_word(gi ? wv[i].z : wv[i].x);
                 const bf16x8 b1 = expand_word(gi ? wv[i].w : wv[i].y);
-                f32x4 p = mfma16x16x32(x0, b0, xn);
-                p = mfma16x16x32(x1, b1, p);  // sum(x*q)/16
-                const uint32_t sbw = gi ? sv[i].y : sv[i].x;
+                f32x4 p = mfma16x16x32(xo0, b0, xn);
+                p = mfma16x16x32(xo1, b1, p);  // sum(x*q)/16
                 const float s16 = bf16_lo(sbw) * 16.0f;
                 const float bi = bf16_hi(sbw);
 #pragma unroll
@@ -303,15 +319,7 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
                 for (int w = 0; w < waves; ++w) v += red[parity][w][t];
                 const int r = t >> 6;
                 const int l = t & 63;
-                const int mrow = 4 * (l >> 4) + r;
-                const int n = rb * 16 + (l & 15);
-                if (mrow < m_rows && n < n_rows) {
-                    const long o = (long)mrow * n_rows + n;
-                    if (out_f32)
-                        static_cast<float*>(y)[o] = v;
-                    else
-                        static_cast<uint16_t*>(y)[o] = f32_to_bf16(v);
-                }
+                store_out(y, out_mode, 4 * (l >> 4) + r, m_rows, rb, l & 15, n_rows, n_out, v);
             }
             acc = zero;
             parity ^= 1;
@@ -319,14 +327,182 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
     };
 
     // two chunks in flight: compute one buffer, then refill it two chunks ahead
-    for (int c = 0; c < chunks; c += 2) {
+    int c = 0;
+    for (; c + 1 < chunks; c += 2) {
         compute(wa, sa, c);
-        if (c + 2 < chunks) issue(wa, sa, c + 2);
-        if (c + 1 < chunks) {
-            compute(wb, sbv2, c + 1);
-            if (c + 3 < chunks) issue(wb, sbv2, c + 3);
+        issue(wa, sa, c + 2);
+        compute(wb, sbv2, c + 1);
+        issue(wb, sbv2, c + 3);
+    }
+    if (c < chunks) compute(wa, sa, c);
+}
+
+// Row-block-per-wave variant for M <= 4 when N has many row blocks (gate|up, the
+// lm_head).  Every wave owns whole 16-row blocks (wave w of the grid takes blocks w,
+// w + total waves, ...), so there is no cross-wave reduction and no barrier after x
+// is staged, and each wave keeps NBUF chunks of GPW tiles in flight across block
+// boundaries.  x is staged in LDS once per workgroup, with the table of -X_g per
+// (group, row) that seeds the MFMAs as in decode_stream_kernel.  (At M = 1 a VALU
+// path with v_dot2_f32_bf16 was measured too: it issues as many cycles per chunk as
+// the 16x16x32 MFMAs it replaces and was slower on the lm_head, so the matrix cores
+// stay.)
+template <int MT, int GPW, int NBUF>
+__global__ __launch_bounds__(256) void decode_rows_kernel(
+    const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x,
+    void* __restrict__ y, int m_rows, int n_rows, int k, int gpairs, int nblocks, int out_mode, int n_out) {
+    static_assert(GPW == 4, "one 8-byte load per lane covers a chunk's scale words");
+    constexpr int R = MT < 4 ? MT : 4;
+    constexpr int kPad = GPW * 128;  // zero columns after each x row
+    extern __shared__ uint4 lds[];
+    const int waves = (int)(blockDim.x >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15;
+    const int kq = lane >> 4;
+    const int gwave = (int)blockIdx.x * waves + wave;
+    const int nwaves = (int)gridDim.x * waves;
+    const int passes = (gpairs + GPW - 1) / GPW;
+    const int my_blocks = gwave < nblocks ? (nblocks - gwave + nwaves - 1) / nwaves : 0;
+    const int chunks = my_blocks * passes;
+    const int arow = col < m_rows ? col : m_rows - 1;  // any valid row for A rows >= M
+    const int row16 = (k + kPad) >> 3;                 // x row stride in 16-byte units
+    const int groups = k >> 6;
+    // -X_g table [2 * (gpairs + GPW)][16]
+    float* xtab = reinterpret_cast<float*>(lds + m_rows * row16);
+
+    uint4 w[NBUF][GPW];
+    uint2 sv[NBUF];  // scale words of a chunk: lane (col, kq) holds pair kq, column col
+    // chunk c: block (c / passes), pairs [GPW * (c % passes), ...).  Chunks past the
+    // wave's last read an empty range (zeros, no traffic): every loop iteration issues
+    // the same loads, which keeps the compiler's wait counts exact.
+    auto issue = [&](int b, int c) {
+        const bool live = c < chunks;
+        const int rb = live ? gwave + (c / passes) * nwaves : 0;
+        const int gpb = (c % passes) * GPW;
+        const int left = gpairs - gpb;
+        const int n_in = !live ? 0 : left < GPW ? left : GPW;
+        const long first = (long)rb * gpairs + gpb;
+        const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * 64, (uint32_t)n_in * 1024u);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * 16, (uint32_t)n_in * 128u);
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) w[b][i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * 1024));
+        sv[b] = buffer_load8<kNonTemporal>(srs, (uint32_t)(lane * 8));  // the chunk's 512 contiguous bytes
+    };
+
+    // x -> LDS with zero padding after each row, and -X_g into the table; the first
+    // batch of x is requested before the weights
+    {
+        const int xchunks = (m_rows * k) >> 3;
+        const int rowc = k >> 3;
+        const int nthr = waves * 64;
+        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)k * 2u);
+        uint4 tmp[4];
+        auto load_x = [&](int c0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = c0 + u * nthr + (int)threadIdx.x;
+                tmp[u] = buffer_load16(xrs, c < xchunks ? (uint32_t)c * 16u : kOutOfRange);
+            }
+        };
+        // each thread sums its eight values; eight consecutive lanes hold one group
+        // (K/8 is a multiple of 8)
+        auto store_x = [&](int c0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = c0 + u * nthr + (int)threadIdx.x;
+                const int row = c / rowc;
+                const int cr = c - row * rowc;
+                if (c < xchunks) lds[row * row16 + cr] = tmp[u];
+                const uint32_t w4[4] = {tmp[u].x, tmp[u].y, tmp[u].z, tmp[u].w};
+                float sum = 0.f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sum += bf16_lo(w4[j]) + bf16_hi(w4[j]);
+                sum += __shfl_xor(sum, 1);
+                sum += __shfl_xor(sum, 2);
+                sum += __shfl_xor(sum, 4);
+                if (c < xchunks && (lane & 7) == 0) xtab[(cr >> 3) * 16 + row] = -sum;
+            }
+        };
+        load_x(0);
+#pragma unroll
+        for (int b = 0; b < NBUF; ++b) issue(b, b);
+        store_x(0);
+        for (int c0 = 4 * nthr; c0 < xchunks; c0 += 4 * nthr) {
+            load_x(c0);
+            store_x(c0);
+        }
+        for (int c = threadIdx.x; c < m_rows * (kPad >> 3); c += nthr)
+            lds[(c / (kPad >> 3)) * row16 + rowc + (c % (kPad >> 3))] = make_uint4(0, 0, 0, 0);
+        // table entries of groups past K are read with zero weight slots: keep them finite
+        const int tab_used = groups * 16, tab_all = 2 * (gpairs + GPW) * 16;
+        for (int t = tab_used + (int)threadIdx.x; t < tab_all; t += nthr) xtab[t] = 0.f;
+    }
+    __syncthreads();
+
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc = zero;
+    auto compute = [&](int b, int c) {
+        const int pass = c % passes;
+        const int gpb = pass * GPW;
+        const uint4* xp = lds + arow * row16 + kq + gpb * 16;  // x operand, pair 0
+        // every LDS operand of the chunk first (x, table, scale words), so their latency
+        // is paid once per chunk rather than before each product
+        bf16x8 xo[GPW][2][2];
+        f32x4 xn[GPW][2];
+        uint32_t sbw[GPW][2];
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+#pragma unroll
+            for (int gi = 0; gi < 2; ++gi) {
+                xo[i][gi][0] = __builtin_bit_cast(bf16x8, xp[i * 16 + gi * 8]);
+                xo[i][gi][1] = __builtin_bit_cast(bf16x8, xp[i * 16 + gi * 8 + 4]);
+                if constexpr (R == 1) {
+                    xn[i][gi] = zero;
+                    xn[i][gi][0] = xtab[(gpb + i) * 32 + gi * 16 + 4 * kq];
+                } else {
+                    xn[i][gi] = *reinterpret_cast<const f32x4*>(xtab + (gpb + i) * 32 + gi * 16 + 4 * kq);
+                }
+                sbw[i][gi] = scale_word(sv[b], i, gi, col);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the gather ahead of the math
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+#pragma unroll
+            for (int gi = 0; gi < 2; ++gi) {
+                const bf16x8 b0 = expand_word(gi ? w[b][i].z : w[b][i].x);
+                const bf16x8 b1 = expand_word(gi ? w[b][i].w : w[b][i].y);
+                const float s16 = bf16_lo(sbw[i][gi]) * 16.0f;
+                const float bi = bf16_hi(sbw[i][gi]);
+                f32x4 p = mfma16x16x32(xo[i][gi][0], b0, xn[i][gi]);
+                p = mfma16x16x32(xo[i][gi][1], b1, p);  // sum(x*q)/16
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    acc[r] = __builtin_fmaf(s16, p[r], acc[r]);
+                    acc[r] = __builtin_fmaf(-bi, xn[i][gi][r], acc[r]);
+                }
+            }
+        }
+        if (pass == passes - 1) {  // block done
+            const int rb = gwave + (c / passes) * nwaves;
+            // lane holds rows 4*kq + r of column col
+#pragma unroll
+            for (int r = 0; r < R; ++r) store_out(y, out_mode, 4 * kq + r, m_rows, rb, col, n_rows, n_out, acc[r]);
+            acc = zero;
+        }
+    };
+
+    int c = 0;
+    for (; c + NBUF <= chunks; c += NBUF) {
+#pragma unroll
+        for (int b = 0; b < NBUF; ++b) {
+            compute(b, c + b);
+            issue(b, c + b + NBUF);
         }
     }
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b)
+        if (c + b < chunks) compute(b, c + b);
 }
 
 // Split of K's group pairs over the waves of a workgroup: an exact GPW x waves
@@ -345,16 +521,31 @@ inline Split choose_split(int gpairs, int mt) {
 }
 
 constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950 LDS per CU (and per workgroup)
+// row-block-per-wave kernel: from this many 16-row blocks, 4 waves per workgroup,
+// at most this many workgroups per CU
+constexpr int kRowsMinBlocks = 512;
+constexpr int kRowsWaves = 4;
+constexpr int kRowsPerCu = 2;
 
 
 template <int MT>
 hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
-                     bool out_f32, const Layout& l, hipStream_t stream) {
-    const int f32 = out_f32 ? 1 : 0;
+                     int out_mode, int n_out, const Layout& l, hipStream_t stream) {
     constexpr int GPW = 4;
     constexpr int R = MT < 4 ? MT : 4;
     const size_t static_lds = 2 * 8 * R * 64 * sizeof(float);
     const size_t lds_bytes = (size_t)m * (l.k + GPW * 128) * 2 + (size_t)(l.gp + GPW) * 2 * 16 * 4;
+    if constexpr (MT <= 4) {
+        if (l.nb >= kRowsMinBlocks && lds_bytes <= kLdsPerCu) {
+            // many row blocks: one wave per block, no cross-wave reduction
+            int grid = (l.nb + kRowsWaves - 1) / kRowsWaves;
+            const int cap = device_cus() * kRowsPerCu;
+            if (grid > cap) grid = cap;
+            hipLaunchKernelGGL((decode_rows_kernel<MT, GPW, 3>), dim3(grid), dim3(64 * kRowsWaves), lds_bytes, stream,
+                               tiles, sb, x, y, m, l.n, l.k, l.gp, l.nb, out_mode, n_out);
+            return hipGetLastError();
+        }
+    }
     if (lds_bytes + static_lds <= kLdsPerCu) {
         // persistent streaming kernel: 4 pairs per chunk, up to 8 waves per workgroup
         int waves = (l.gp + GPW - 1) / GPW;
@@ -367,15 +558,15 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, voi
         const int per_wg = (l.nb + capacity - 1) / capacity;
         const int grid = (l.nb + per_wg - 1) / per_wg;
         hipLaunchKernelGGL((decode_stream_kernel<MT, GPW>), dim3(grid), dim3(64 * waves), lds_bytes, stream, tiles,
-                           sb, x, y, m, l.n, l.k, l.gp, l.nb, waves, f32);
+                           sb, x, y, m, l.n, l.k, l.gp, l.nb, waves, out_mode, n_out);
         return hipGetLastError();
     }
     const Split sp = choose_split(l.gp, MT);
     const dim3 grid(l.nb), block(64 * sp.waves);
     if (sp.gpw == 6)
-        hipLaunchKernelGGL((decode_kernel<MT, 6, false>), grid, block, 0, stream, tiles, sb, x, y, m, l.n, l.k, l.gp, sp.waves, f32);
+        hipLaunchKernelGGL((decode_kernel<MT, 6, false>), grid, block, 0, stream, tiles, sb, x, y, m, l.n, l.k, l.gp, sp.waves, out_mode, n_out);
     else
-        hipLaunchKernelGGL((decode_kernel<MT, 4, false>), grid, block, 0, stream, tiles, sb, x, y, m, l.n, l.k, l.gp, sp.waves, f32);
+        hipLaunchKernelGGL((decode_kernel<MT, 4, false>), grid, block, 0, stream, tiles, sb, x, y, m, l.n, l.k, l.gp, sp.waves, out_mode, n_out);
     return hipGetLastError();
 }
 
@@ -394,21 +585,22 @@ int device_cus() {
 }
 
 hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
-                         bool out_f32, const Layout& l, hipStream_t stream) {
-    const size_t ysz = out_f32 ? 4 : 2;
+                         int out_mode, int n_out, const Layout& l, hipStream_t stream) {
+    const size_t ysz = (out_mode == kOutF32 || out_mode == kOutGegluF32) ? 4 : 2;
+    const size_t ycols = out_mode >= kOutGegluBf16 ? (size_t)n_out : (size_t)l.n;
     for (int m0 = 0; m0 < m; m0 += 16) {
         const int mc = (m - m0) < 16 ? (m - m0) : 16;
         const uint16_t* xs = x + (size_t)m0 * l.k;
-        void* ys = static_cast<char*>(y) + (size_t)m0 * l.n * ysz;
+        void* ys = static_cast<char*>(y) + (size_t)m0 * ycols * ysz;
         hipError_t e;
         if (mc == 1)
-            e = launch_mt<1>(tiles, sb, xs, ys, mc, out_f32, l, stream);
+            e = launch_mt<1>(tiles, sb, xs, ys, mc, out_mode, n_out, l, stream);
         else if (mc == 2)
-            e = launch_mt<2>(tiles, sb, xs, ys, mc, out_f32, l, stream);
+            e = launch_mt<2>(tiles, sb, xs, ys, mc, out_mode, n_out, l, stream);
         else if (mc <= 4)
-            e = launch_mt<4>(tiles, sb, xs, ys, mc, out_f32, l, stream);
+            e = launch_mt<4>(tiles, sb, xs, ys, mc, out_mode, n_out, l, stream);
         else
-            e = launch_mt<16>(tiles, sb, xs, ys, mc, out_f32, l, stream);
+            e = launch_mt<16>(tiles, sb, xs, ys, mc, out_mode, n_out, l, stream);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

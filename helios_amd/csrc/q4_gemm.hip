@@ -35,24 +35,6 @@ constexpr int kXChunks = kBM * 8;     // 16-byte chunks of one x group tile (256
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// 16-byte-per-lane DMA into LDS: lane i's 16 bytes land at lds + 16 i, read from
-// voff + soff.  Only voff is checked against the buffer's size (a resource of size
-// 0 reads zeros for any offset); callers keep voff + soff inside the buffer for
-// in-range lanes and put the rest at kOutOfRange.  Issued as
-// inline asm, so the compiler does not track it: it would otherwise insert waits for
-// all outstanding DMAs before LDS reads it cannot tell apart from them (it keeps at
-// most eight DMA records), undoing the prefetch.  Ordering is this kernel's own: every
-// DMA'd slot is read only after an explicit vmcnt wait and a barrier.  M0 (the LDS
-// address) is an operand, so the compiler knows it is written.  The compiler's hazard
-// checks cannot see into the asm, so it opens with the wait states the load may need:
-// 5 after a VALU write of an SGPR it reads (under register pressure the compiler
-// reloads resource and offset SGPRs from VGPR lanes with v_readlane right before it),
-// which also covers the 1 an M0 write needs.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, const void* lds, uint32_t voff, uint32_t soff = 0) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);  // LDS offset: low half of the generic address
-    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0)
-                 : "memory");
-}
 
 // ---------------------------------------------------------------------------
 // X_g = sum of x over each 64-wide group, as the augmented-K MFMA A operand:
@@ -138,25 +120,13 @@ __shared__ uint4 g_wp1[kWPair + kSPair];
 // scale/bias words as uint2 [row block][pair][column] (8 KiB)
 __shared__ uint4 g_xab[16 * 64 + kRB * 4 * 16 / 2];
 
-// s_waitcnt with vmcnt(n) only (expcnt / lgkmcnt left free), n < 64
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
-// the same plus lgkmcnt(0): this wave's LDS reads have returned
-template <int N>
-__device__ __forceinline__ void wait_vm_lds() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
-}
 
-template <bool F32OUT>
+template <int OUT>
 __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ tiles, const uint2* __restrict__ sb,
                                                    const uint16_t* __restrict__ x, const uint4* __restrict__ xaug,
                                                    void* __restrict__ y, int m_rows, int n_rows, int k, int groups,
                                                    int gpairs, int mtiles, int ntiles, int octets, uint32_t tile_bytes,
-                                                   uint32_t sb_bytes, int g_split, long split_stride) {
+                                                   uint32_t sb_bytes, int g_split, long split_stride, int n_out) {
     int mt, nt;
     tile_of((int)blockIdx.x, (int)gridDim.x, mtiles, ntiles, mt, nt);
     // split of K: groups [g_begin, g_end), whole octets; with several splits each
@@ -340,7 +310,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
                 default: wait_vm_lds<0>(); break;  // (not reached) safe fallback
             }
         }
-        __builtin_amdgcn_s_barrier();
+        lds_barrier();
         if ((g & 7) == 0 && g > g_begin) bias();
         if (issues_xa(g)) dma_xa(g >> 3);
         const bool pair = (g & 1) == 0;
@@ -386,11 +356,11 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     {
         const int o = (g_end - 1) >> 3;
         wait_vm<0>();
-        __builtin_amdgcn_s_barrier();
+        lds_barrier();
         if (o > (g_begin >> 3) && 8 * o + 1 >= g_end) {
             dma_xa(o);
             wait_vm<0>();
-            __builtin_amdgcn_s_barrier();
+            lds_barrier();
         }
         bias();
     }
@@ -400,16 +370,16 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     for (int i = 0; i < kMT; ++i) {
 #pragma unroll
         for (int j = 0; j < kNT; ++j) {
-            const int n = (rbw + wn * kNT + j) * 16 + col;
+            const int rb = rbw + wn * kNT + j;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int m = mt * kBM + wm * kWM + 16 * i + 4 * kq + e;
-                if (m < m_rows && n < n_rows) {
-                    const long o = (long)m * n_rows + n;
-                    if (F32OUT)
-                        static_cast<float*>(y)[(long)blockIdx.y * split_stride + o] = acc[i][j][e];
-                    else
-                        static_cast<uint16_t*>(y)[o] = f32_to_bf16(acc[i][j][e]);
+                if constexpr (OUT == kOutF32) {  // fp32 output, or this split's partial plane
+                    const int n = rb * 16 + col;
+                    if (m < m_rows && n < n_rows)
+                        static_cast<float*>(y)[(long)blockIdx.y * split_stride + (long)m * n_rows + n] = acc[i][j][e];
+                } else {
+                    store_out(y, OUT, m, m_rows, rb, col, n_rows, n_out, acc[i][j][e]);
                 }
             }
         }
@@ -465,6 +435,27 @@ __global__ void split_reduce_kernel(const float* __restrict__ part, void* __rest
     }
 }
 
+// h = GeGLU of the summed gate|up partial planes, in split order (deterministic).  One
+// thread per output h[m, hn]: gate and up are columns 16*(hn/8) + hn%8 and that + 8.
+template <int OUT>
+__global__ void split_geglu_kernel(const float* __restrict__ part, void* __restrict__ h, int m_rows, int n_rows,
+                                   int n_out, long elems, int splits) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)m_rows * n_out) return;
+    const int m = (int)(i / n_out);
+    const int hn = (int)(i - (long)m * n_out);
+    const long o = (long)m * n_rows + (hn >> 3) * 16 + (hn & 7);
+    float g = part[o], u = part[o + 8];
+    for (int s = 1; s < splits; ++s) {
+        g += part[(long)s * elems + o];
+        u += part[(long)s * elems + o + 8];
+    }
+    if (OUT == kOutGegluF32)
+        static_cast<float*>(h)[i] = geglu_f32(g, u);
+    else
+        static_cast<uint16_t*>(h)[i] = f32_to_bf16(geglu_bf16(g, u));
+}
+
 }  // namespace
 
 // Split of K over workgroups when the output tiles alone leave CUs idle: the count
@@ -502,8 +493,8 @@ size_t gemm_workspace_bytes(int m, const Layout& l) {
     return p.xaug_bytes + p.part_bytes;
 }
 
-hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, bool out_f32,
-                       const Layout& l, void* workspace, hipStream_t stream) {
+hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, int out_mode,
+                       int n_out, const Layout& l, void* workspace, hipStream_t stream) {
     const GemmPlan plan = plan_gemm(m, l);
     const int octets = (l.g + 7) / 8;
     const int mtiles = (m + kBM - 1) / kBM;
@@ -525,13 +516,23 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     const uint32_t tb = (uint32_t)l.tile_bytes(), sbb = (uint32_t)l.sb_bytes();
     const long elems = (long)m * l.n;
     if (plan.splits > 1) {
-        hipLaunchKernelGGL((gemm_kernel<true>), grid, block, 0, stream, tiles, sb, x, xaug, (void*)part, m, l.n, l.k, l.g,
-                           l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, elems);
+        hipLaunchKernelGGL((gemm_kernel<kOutF32>), grid, block, 0, stream, tiles, sb, x, xaug, (void*)part, m, l.n, l.k,
+                           l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, elems, n_out);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const int rblock = 256;
+        if (out_mode >= kOutGegluBf16) {
+            const unsigned rgrid = (unsigned)(((long)m * n_out + rblock - 1) / rblock);
+            if (out_mode == kOutGegluF32)
+                hipLaunchKernelGGL((split_geglu_kernel<kOutGegluF32>), dim3(rgrid), dim3(rblock), 0, stream, part, y, m,
+                                   l.n, n_out, elems, plan.splits);
+            else
+                hipLaunchKernelGGL((split_geglu_kernel<kOutGegluBf16>), dim3(rgrid), dim3(rblock), 0, stream, part, y, m,
+                                   l.n, n_out, elems, plan.splits);
+            return hipGetLastError();
+        }
         const unsigned rgrid = (unsigned)(((elems + 3) / 4 + rblock - 1) / rblock);
-        if (out_f32)
+        if (out_mode == kOutF32)
             hipLaunchKernelGGL((split_reduce_kernel<true>), dim3(rgrid), dim3(rblock), 0, stream, part, y, elems,
                                plan.splits);
         else
@@ -539,12 +540,16 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
                                plan.splits);
         return hipGetLastError();
     }
-    if (out_f32)
-        hipLaunchKernelGGL((gemm_kernel<true>), grid, block, 0, stream, tiles, sb, x, xaug, y, m, l.n, l.k, l.g, l.gp,
-                           mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L);
-    else
-        hipLaunchKernelGGL((gemm_kernel<false>), grid, block, 0, stream, tiles, sb, x, xaug, y, m, l.n, l.k, l.g, l.gp,
-                           mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L);
+#define Q4_GEMM_LAUNCH(MODE)                                                                                     \
+    hipLaunchKernelGGL((gemm_kernel<MODE>), grid, block, 0, stream, tiles, sb, x, xaug, y, m, l.n, l.k, l.g, l.gp, \
+                       mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L, n_out)
+    switch (out_mode) {
+        case kOutF32: Q4_GEMM_LAUNCH(kOutF32); break;
+        case kOutGegluBf16: Q4_GEMM_LAUNCH(kOutGegluBf16); break;
+        case kOutGegluF32: Q4_GEMM_LAUNCH(kOutGegluF32); break;
+        default: Q4_GEMM_LAUNCH(kOutBf16); break;
+    }
+#undef Q4_GEMM_LAUNCH
     return hipGetLastError();
 }
 

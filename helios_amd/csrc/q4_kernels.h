@@ -27,17 +27,26 @@ inline Layout make_layout(int n, int k) {
     return l;
 }
 
-// MLX layout (device) -> tiled layout (device).
-hipError_t launch_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b, uint4* tiles,
-                         uint2* sb, const Layout& l, hipStream_t stream);
+// A gate|up pair of F rows each is tiled as one projection of pair_layout(F, K):
+// block j holds gate rows 8j..8j+7 then up rows 8j..8j+7 (its N is 16 * ceil(F / 8)).
+inline Layout pair_layout(int f, int k) { return make_layout(16 * ((f + 7) / 8), k); }
 
-// Tiled layout -> fp32 W[N,K] row-major, w = fma(s, q, b).
-hipError_t launch_dequantize(const uint4* tiles, const uint2* sb, float* out, const Layout& l,
+// MLX layout (device) -> tiled layout (device).  pair_rows = 0: one projection
+// (w, s, b); pair_rows = F: the gate (w, s, b) and up (w_up, s_up, b_up) pair.
+hipError_t launch_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint32_t* w_up,
+                         const uint16_t* s_up, const uint16_t* b_up, uint4* tiles, uint2* sb, const Layout& l,
+                         int pair_rows, hipStream_t stream);
+
+// Tiled layout -> fp32 W[N,K] row-major, w = fma(s, q, b); a pair gives [2, F, K].
+hipError_t launch_dequantize(const uint4* tiles, const uint2* sb, float* out, const Layout& l, int pair_rows,
                              hipStream_t stream);
+
+// Output modes (q4_common.h OutMode): 0 bf16 y, 1 fp32 y, 2 bf16 GeGLU h, 3 fp32 GeGLU h.
+// n_out is F for the GeGLU modes (h is [M, F]) and unused otherwise.
 
 // Decode path, M <= 16 rows per launch (the launcher walks larger M in 16-row slabs).
 hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
-                         bool out_f32, const Layout& l, hipStream_t stream);
+                         int out_mode, int n_out, const Layout& l, hipStream_t stream);
 
 // Prefill path: fp32-exact factored GEMM on the matrix cores.  `workspace` holds the
 // group sums of x and, when K is split over workgroups, the fp32 partial sums
@@ -55,8 +64,8 @@ size_t gemm_workspace_bytes(int m, const Layout& l);
 
 // Compute units of the current device (cached per device).
 int device_cus();
-hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, bool out_f32,
-                       const Layout& l, void* workspace, hipStream_t stream);
+hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, int out_mode,
+                       int n_out, const Layout& l, void* workspace, hipStream_t stream);
 
 // Rows at or above which forward uses the GEMM path.
 constexpr int kGemmMinRows = 32;

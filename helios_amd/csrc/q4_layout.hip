@@ -1,5 +1,6 @@
-// Weight-layout kernels: MLX affine layout -> tiled MFMA layout, and the bit-exact
-// fp32 dequantize of the tiled layout (the check that the tiles hold every bit).
+// Weight-layout kernels: MLX affine layout -> tiled MFMA layout (one projection, or a
+// gate|up pair interleaved 8 rows at a time), and the bit-exact fp32 dequantize of
+// the tiled layout (the check that the tiles hold every bit).
 #include "q4_common.h"
 #include "q4_kernels.h"
 
@@ -18,17 +19,43 @@ __device__ __forceinline__ uint32_t tile_word(uint32_t u) {
     return (t << 3) | (t >> 29);
 }
 
-__global__ void repack_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
-                              const uint16_t* __restrict__ b, uint4* __restrict__ tiles,
-                              uint2* __restrict__ sb, int n_rows, int k, int groups, int gpairs,
-                              long total) {
+// Source row of tiled row 16*rb + c: row 16*rb + c of the projection, or for a
+// gate|up pair (pair_rows = F > 0) row 8*rb + c%8 of gate (c < 8) or of up (c >= 8).
+struct SourceRow {
+    const uint32_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+    int row;
+    bool valid;
+};
+
+__device__ __forceinline__ SourceRow source_row(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                                                const uint32_t* w2, const uint16_t* s2, const uint16_t* b2,
+                                                long rb, int c, int n_rows, int pair_rows) {
+    if (pair_rows > 0) {
+        const int row = (int)(rb * 8 + (c & 7));
+        return c < 8 ? SourceRow{w, s, b, row, row < pair_rows} : SourceRow{w2, s2, b2, row, row < pair_rows};
+    }
+    const int row = (int)(rb * 16 + c);
+    return SourceRow{w, s, b, row, row < n_rows};
+}
+
+__global__ void repack_kernel(const uint32_t* __restrict__ w_a, const uint16_t* __restrict__ s_a,
+                              const uint16_t* __restrict__ b_a, const uint32_t* __restrict__ w_b,
+                              const uint16_t* __restrict__ s_b, const uint16_t* __restrict__ b_b,
+                              uint4* __restrict__ tiles, uint2* __restrict__ sb, int n_rows, int pair_rows, int k,
+                              int groups, int gpairs, long total) {
     const long tid = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (tid >= total) return;
     const int lane = (int)(tid & 63);
     const long t = tid >> 6;
     const int gp = (int)(t % gpairs);
     const long rb = t / gpairs;
-    const int row = (int)(rb * 16 + (lane & 15));
+    const SourceRow src = source_row(w_a, s_a, b_a, w_b, s_b, b_b, rb, lane & 15, n_rows, pair_rows);
+    const uint32_t* w = src.w;
+    const uint16_t* s = src.s;
+    const uint16_t* b = src.b;
+    const int row = src.row;
     const int kq = lane >> 4;
     const int words_per_row = k / 8;
     uint32_t out[4];
@@ -38,7 +65,7 @@ __global__ void repack_kernel(const uint32_t* __restrict__ w, const uint16_t* __
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             uint32_t u = 0;
-            if (row < n_rows && g < groups) u = w[(long)row * words_per_row + 8 * g + 4 * h + kq];
+            if (src.valid && g < groups) u = w[(long)row * words_per_row + 8 * g + 4 * h + kq];
             out[2 * gi + h] = tile_word(u);
         }
     }
@@ -49,7 +76,7 @@ __global__ void repack_kernel(const uint32_t* __restrict__ w, const uint16_t* __
         for (int gi = 0; gi < 2; ++gi) {
             const int g = 2 * gp + gi;
             v[gi] = 0;
-            if (row < n_rows && g < groups) {
+            if (src.valid && g < groups) {
                 const long idx = (long)row * groups + g;
                 v[gi] = (uint32_t)s[idx] | ((uint32_t)b[idx] << 16);
             }
@@ -58,8 +85,10 @@ __global__ void repack_kernel(const uint32_t* __restrict__ w, const uint16_t* __
     }
 }
 
+// out row of tiled row 16*rb + c: the same row, or for a gate|up pair gate row r at
+// out row r and up row r at out row F + r (out is [2, F, K])
 __global__ void dequantize_kernel(const uint4* __restrict__ tiles, const uint2* __restrict__ sb,
-                                  float* __restrict__ out, int n_rows, int k, int groups, int gpairs,
+                                  float* __restrict__ out, int n_rows, int pair_rows, int k, int groups, int gpairs,
                                   long total) {
     const long tid = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (tid >= total) return;
@@ -67,9 +96,17 @@ __global__ void dequantize_kernel(const uint4* __restrict__ tiles, const uint2* 
     const long t = tid >> 6;
     const int gp = (int)(t % gpairs);
     const long rb = t / gpairs;
-    const int row = (int)(rb * 16 + (lane & 15));
+    const int c = lane & 15;
     const int kq = lane >> 4;
-    if (row >= n_rows) return;
+    int row;
+    if (pair_rows > 0) {
+        const int r = (int)(rb * 8 + (c & 7));
+        if (r >= pair_rows) return;
+        row = c < 8 ? r : pair_rows + r;
+    } else {
+        row = (int)(rb * 16 + c);
+        if (row >= n_rows) return;
+    }
     const uint4 wv = tiles[tid];
     const uint2 sv = sb[t * 16 + (lane & 15)];
     const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
@@ -95,23 +132,24 @@ __global__ void dequantize_kernel(const uint4* __restrict__ tiles, const uint2* 
 
 }  // namespace
 
-hipError_t launch_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b, uint4* tiles,
-                         uint2* sb, const Layout& l, hipStream_t stream) {
+hipError_t launch_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint32_t* w_up,
+                         const uint16_t* s_up, const uint16_t* b_up, uint4* tiles, uint2* sb, const Layout& l,
+                         int pair_rows, hipStream_t stream) {
     const long total = (long)l.nb * l.gp * 64;
     const int block = 256;
     const long grid = (total + block - 1) / block;
-    hipLaunchKernelGGL(repack_kernel, dim3((unsigned)grid), dim3(block), 0, stream, w, s, b, tiles, sb,
-                       l.n, l.k, l.g, l.gp, total);
+    hipLaunchKernelGGL(repack_kernel, dim3((unsigned)grid), dim3(block), 0, stream, w, s, b, w_up, s_up, b_up, tiles,
+                       sb, l.n, pair_rows, l.k, l.g, l.gp, total);
     return hipGetLastError();
 }
 
-hipError_t launch_dequantize(const uint4* tiles, const uint2* sb, float* out, const Layout& l,
+hipError_t launch_dequantize(const uint4* tiles, const uint2* sb, float* out, const Layout& l, int pair_rows,
                              hipStream_t stream) {
     const long total = (long)l.nb * l.gp * 64;
     const int block = 256;
     const long grid = (total + block - 1) / block;
     hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)grid), dim3(block), 0, stream, tiles, sb, out,
-                       l.n, l.k, l.g, l.gp, total);
+                       l.n, pair_rows, l.k, l.g, l.gp, total);
     return hipGetLastError();
 }
 

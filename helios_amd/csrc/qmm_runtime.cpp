@@ -90,8 +90,9 @@ struct DeviceGuard {
 
 struct Gemma4QLinear {
     uint64_t magic = 0;
-    Gemma4QLinearDesc desc{};
+    Gemma4QLinearDesc desc{};  // out_features is F for a gate|up pair
     q4::Layout layout;
+    int pair_rows = 0;  // F for a gate|up pair (tiled as q4::pair_layout), else 0
     int device = 0;
     uint4* tiles = nullptr;
     uint2* sb = nullptr;
@@ -99,7 +100,7 @@ struct Gemma4QLinear {
 
 namespace {
 
-Gemma4Status check_desc(const Gemma4QLinearDesc* desc, const char* fn) {
+Gemma4Status check_desc(const Gemma4QLinearDesc* desc, bool pair, const char* fn) {
     if (desc == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, std::string(fn) + " requires a non-null desc");
     if (desc->out_features == 0 || desc->in_features == 0)
         return fail(GEMMA4_ERR_INVALID_ARGUMENT, std::string(fn) + ": out_features and in_features must be > 0");
@@ -109,9 +110,10 @@ Gemma4Status check_desc(const Gemma4QLinearDesc* desc, const char* fn) {
                         std::to_string(desc->bits) + " group_size=" + std::to_string(desc->group_size) + ")");
     if (desc->in_features % 64 != 0)
         return fail(GEMMA4_ERR_INVALID_ARGUMENT, std::string(fn) + ": in_features must be a multiple of 64");
-    if (desc->out_features > (1u << 30) || desc->in_features > (1u << 24))
+    if (desc->out_features > (1u << 29) || desc->in_features > (1u << 24))
         return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, std::string(fn) + ": shape exceeds the supported range");
-    const q4::Layout l = q4::make_layout((int)desc->out_features, (int)desc->in_features);
+    const q4::Layout l = pair ? q4::pair_layout((int)desc->out_features, (int)desc->in_features)
+                              : q4::make_layout((int)desc->out_features, (int)desc->in_features);
     if (l.tile_bytes() > q4::kMaxBufferBytes || l.sb_bytes() > q4::kMaxBufferBytes)
         return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
                     std::string(fn) + ": weights exceed 2 GiB per projection (split it along out_features)");
@@ -128,13 +130,23 @@ void release(Gemma4QLinear* h) {
 
 bool valid_handle(const Gemma4QLinear* h) { return h != nullptr && h->magic == kQLinearMagic; }
 
-// Allocates the tiled buffers and repacks from MLX-layout device arrays.
-Gemma4Status build_handle(const Gemma4QLinearDesc* desc, const uint32_t* w_dev, const uint16_t* s_dev,
-                          const uint16_t* b_dev, hipStream_t stream, Gemma4QLinear** out) {
+// One weight triple in MLX layout (device pointers).
+struct Triple {
+    const uint32_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+};
+
+// Allocates the tiled buffers and repacks from MLX-layout device arrays: one
+// projection (up == nullptr) or a gate|up pair.
+Gemma4Status build_handle(const Gemma4QLinearDesc* desc, const Triple& main, const Triple* up, hipStream_t stream,
+                          Gemma4QLinear** out) {
     Gemma4QLinear* h = new (std::nothrow) Gemma4QLinear();
     if (h == nullptr) return fail(GEMMA4_ERR_MEMORY_GUARD, "gemma4_qlinear: host allocation failed");
     h->desc = *desc;
-    h->layout = q4::make_layout((int)desc->out_features, (int)desc->in_features);
+    h->pair_rows = up ? (int)desc->out_features : 0;
+    h->layout = up ? q4::pair_layout((int)desc->out_features, (int)desc->in_features)
+                   : q4::make_layout((int)desc->out_features, (int)desc->in_features);
     hipError_t e = hipGetDevice(&h->device);
     if (e != hipSuccess) {
         delete h;
@@ -148,7 +160,8 @@ Gemma4Status build_handle(const Gemma4QLinearDesc* desc, const uint32_t* w_dev, 
         return fail(GEMMA4_ERR_MEMORY_GUARD, std::string("gemma4_qlinear: device allocation failed: ") +
                                                  hipGetErrorString(e));
     }
-    e = q4::launch_repack(w_dev, s_dev, b_dev, h->tiles, h->sb, h->layout, stream);
+    e = q4::launch_repack(main.w, main.s, main.b, up ? up->w : nullptr, up ? up->s : nullptr, up ? up->b : nullptr,
+                          h->tiles, h->sb, h->layout, h->pair_rows, stream);
     if (e != hipSuccess) {
         release(h);
         delete h;
@@ -156,6 +169,104 @@ Gemma4Status build_handle(const Gemma4QLinearDesc* desc, const uint32_t* w_dev, 
     }
     h->magic = kQLinearMagic;
     *out = h;
+    return ok();
+}
+
+// Host triples -> one staging allocation -> build_handle on the null stream.
+Gemma4Status create_from_host(const Gemma4QLinearDesc* desc, const uint32_t* const* w, const uint16_t* const* s,
+                              const uint16_t* const* b, int parts, const char* fn, Gemma4QLinear** out) {
+    const size_t n = desc->out_features, k = desc->in_features;
+    const size_t wbytes = n * k / 2, sbytes = n * (k / 64) * 2, part = wbytes + 2 * sbytes;
+    void* staging = nullptr;
+    hipError_t e = hipMalloc(&staging, part * parts);
+    if (e != hipSuccess)
+        return fail(GEMMA4_ERR_MEMORY_GUARD, std::string(fn) + ": staging allocation failed: " + hipGetErrorString(e));
+    Triple t[2];
+    for (int i = 0; i < parts && e == hipSuccess; ++i) {
+        char* base = static_cast<char*>(staging) + part * i;
+        e = hipMemcpy(base, w[i], wbytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(base + wbytes, s[i], sbytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(base + wbytes + sbytes, b[i], sbytes, hipMemcpyHostToDevice);
+        t[i] = Triple{reinterpret_cast<const uint32_t*>(base), reinterpret_cast<const uint16_t*>(base + wbytes),
+                      reinterpret_cast<const uint16_t*>(base + wbytes + sbytes)};
+    }
+    if (e != hipSuccess) {
+        (void)hipFree(staging);
+        return hip_fail((std::string(fn) + ": upload").c_str(), e);
+    }
+    Gemma4Status st = build_handle(desc, t[0], parts == 2 ? &t[1] : nullptr, nullptr, out);
+    e = hipStreamSynchronize(nullptr);
+    (void)hipFree(staging);
+    if (st == GEMMA4_OK && e != hipSuccess) {
+        gemma4_qlinear_free(*out);
+        *out = nullptr;
+        return hip_fail((std::string(fn) + ": repack").c_str(), e);
+    }
+    return st;
+}
+
+Gemma4Status create_from_device(const Gemma4QLinearDesc* desc, const Triple& main, const Triple* up, void* stream,
+                                const char* fn, Gemma4QLinear** out) {
+    hipStream_t st_h = static_cast<hipStream_t>(stream);
+    Gemma4Status st = build_handle(desc, main, up, st_h, out);
+    if (st != GEMMA4_OK) return st;
+    const hipError_t e = hipStreamSynchronize(st_h);
+    if (e != hipSuccess) {
+        gemma4_qlinear_free(*out);
+        *out = nullptr;
+        return hip_fail((std::string(fn) + ": repack").c_str(), e);
+    }
+    return ok();
+}
+
+// Checks and dispatch shared by the plain and the GeGLU forward.
+Gemma4Status run_forward(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev, uint32_t rows,
+                         void* y_dev, Gemma4QmmDtype y_dtype, bool geglu, const char* fn) {
+    const std::string name(fn);
+    if (!valid_handle(linear)) return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " received an invalid handle");
+    if (geglu && linear->pair_rows == 0)
+        return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": the handle is one projection, not a gate|up pair "
+                                                        "(create it with gemma4_qgeglu_create)");
+    if (!geglu && linear->pair_rows != 0)
+        return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": the handle is a gate|up pair (use gemma4_qgeglu_forward)");
+    if (y_dtype != GEMMA4_QMM_BF16 && y_dtype != GEMMA4_QMM_F32)
+        return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": the output dtype must be BF16 or F32");
+    if (rows == 0) return ok();
+    if (x_dev == nullptr || y_dev == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " requires non-null x and y");
+    if ((reinterpret_cast<uintptr_t>(x_dev) & 15u) != 0)
+        return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": x must be 16-byte aligned");
+    const uintptr_t yalign = y_dtype == GEMMA4_QMM_F32 ? 3u : 1u;
+    if ((reinterpret_cast<uintptr_t>(y_dev) & yalign) != 0)
+        return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": the output is misaligned for its dtype");
+    if (rows > (1u << 24)) return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, name + ": rows exceeds 2^24");
+    if ((size_t)rows * linear->layout.k * 2 > q4::kMaxBufferBytes)
+        return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, name + ": x exceeds 2 GiB (split the rows into several calls)");
+    DeviceGuard guard;
+    hipError_t e = guard.enter(linear->device);
+    if (e != hipSuccess) return hip_fail((name + ": hipSetDevice").c_str(), e);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool f32 = y_dtype == GEMMA4_QMM_F32;
+    const int mode = geglu ? (f32 ? q4::kOutGegluF32 : q4::kOutGegluBf16) : (f32 ? q4::kOutF32 : q4::kOutBf16);
+    const int n_out = linear->pair_rows;
+    if ((int)rows < q4::kGemmMinRows) {
+        e = q4::launch_decode(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, mode, n_out, linear->layout, st);
+        if (e != hipSuccess) return hip_fail((name + ": decode launch").c_str(), e);
+        return ok();
+    }
+    // group sums of x (and split-K partial sums) live in a stream-ordered scratch
+    // allocation for this call
+    const size_t ws_bytes = q4::gemm_workspace_bytes((int)rows, linear->layout);
+    hipMemPool_t pool = nullptr;
+    e = scratch_pool(linear->device, &pool);
+    if (e != hipSuccess) return hip_fail((name + ": scratch pool").c_str(), e);
+    void* ws = nullptr;
+    e = hipMallocFromPoolAsync(&ws, ws_bytes, pool, st);
+    if (e != hipSuccess)
+        return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
+    e = q4::launch_gemm(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, mode, n_out, linear->layout, ws, st);
+    const hipError_t ef = hipFreeAsync(ws, st);
+    if (e != hipSuccess) return hip_fail((name + ": gemm launch").c_str(), e);
+    if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);
     return ok();
 }
 
@@ -183,36 +294,11 @@ Gemma4Status gemma4_qlinear_create(const Gemma4QLinearDesc* desc, const uint32_t
     try {
         if (out == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_create requires a non-null out pointer");
         *out = nullptr;
-        Gemma4Status st = check_desc(desc, "gemma4_qlinear_create");
+        Gemma4Status st = check_desc(desc, false, "gemma4_qlinear_create");
         if (st != GEMMA4_OK) return st;
         if (weight == nullptr || scales == nullptr || biases == nullptr)
             return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_create requires non-null weight, scales and biases");
-        const size_t n = desc->out_features, k = desc->in_features;
-        const size_t wbytes = n * k / 2, sbytes = n * (k / 64) * 2;
-        void* staging = nullptr;
-        hipError_t e = hipMalloc(&staging, wbytes + 2 * sbytes);
-        if (e != hipSuccess)
-            return fail(GEMMA4_ERR_MEMORY_GUARD, std::string("gemma4_qlinear_create: staging allocation failed: ") +
-                                                     hipGetErrorString(e));
-        char* base = static_cast<char*>(staging);
-        e = hipMemcpy(base, weight, wbytes, hipMemcpyHostToDevice);
-        if (e == hipSuccess) e = hipMemcpy(base + wbytes, scales, sbytes, hipMemcpyHostToDevice);
-        if (e == hipSuccess) e = hipMemcpy(base + wbytes + sbytes, biases, sbytes, hipMemcpyHostToDevice);
-        if (e != hipSuccess) {
-            (void)hipFree(staging);
-            return hip_fail("gemma4_qlinear_create: upload", e);
-        }
-        st = build_handle(desc, reinterpret_cast<const uint32_t*>(base),
-                          reinterpret_cast<const uint16_t*>(base + wbytes),
-                          reinterpret_cast<const uint16_t*>(base + wbytes + sbytes), nullptr, out);
-        e = hipStreamSynchronize(nullptr);
-        (void)hipFree(staging);
-        if (st == GEMMA4_OK && e != hipSuccess) {
-            gemma4_qlinear_free(*out);
-            *out = nullptr;
-            return hip_fail("gemma4_qlinear_create: repack", e);
-        }
-        return st;
+        return create_from_host(desc, &weight, &scales, &biases, 1, "gemma4_qlinear_create", out);
     } catch (...) {
         return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_create: unexpected native exception");
     }
@@ -225,23 +311,57 @@ Gemma4Status gemma4_qlinear_create_device(const Gemma4QLinearDesc* desc, const u
         if (out == nullptr)
             return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_create_device requires a non-null out pointer");
         *out = nullptr;
-        Gemma4Status st = check_desc(desc, "gemma4_qlinear_create_device");
+        Gemma4Status st = check_desc(desc, false, "gemma4_qlinear_create_device");
         if (st != GEMMA4_OK) return st;
         if (weight_dev == nullptr || scales_dev == nullptr || biases_dev == nullptr)
             return fail(GEMMA4_ERR_INVALID_ARGUMENT,
                         "gemma4_qlinear_create_device requires non-null weight, scales and biases");
-        hipStream_t st_h = static_cast<hipStream_t>(stream);
-        st = build_handle(desc, weight_dev, scales_dev, biases_dev, st_h, out);
-        if (st != GEMMA4_OK) return st;
-        const hipError_t e = hipStreamSynchronize(st_h);
-        if (e != hipSuccess) {
-            gemma4_qlinear_free(*out);
-            *out = nullptr;
-            return hip_fail("gemma4_qlinear_create_device: repack", e);
-        }
-        return ok();
+        return create_from_device(desc, Triple{weight_dev, scales_dev, biases_dev}, nullptr, stream,
+                                  "gemma4_qlinear_create_device", out);
     } catch (...) {
         return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_create_device: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qgeglu_create(const Gemma4QLinearDesc* desc, const uint32_t* gate_weight,
+                                  const uint16_t* gate_scales, const uint16_t* gate_biases, const uint32_t* up_weight,
+                                  const uint16_t* up_scales, const uint16_t* up_biases, Gemma4QLinear** out) {
+    try {
+        if (out == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qgeglu_create requires a non-null out pointer");
+        *out = nullptr;
+        Gemma4Status st = check_desc(desc, true, "gemma4_qgeglu_create");
+        if (st != GEMMA4_OK) return st;
+        if (!gate_weight || !gate_scales || !gate_biases || !up_weight || !up_scales || !up_biases)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT,
+                        "gemma4_qgeglu_create requires non-null weight, scales and biases for gate and up");
+        const uint32_t* w[2] = {gate_weight, up_weight};
+        const uint16_t* s[2] = {gate_scales, up_scales};
+        const uint16_t* b[2] = {gate_biases, up_biases};
+        return create_from_host(desc, w, s, b, 2, "gemma4_qgeglu_create", out);
+    } catch (...) {
+        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qgeglu_create: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qgeglu_create_device(const Gemma4QLinearDesc* desc, const uint32_t* gate_weight_dev,
+                                         const uint16_t* gate_scales_dev, const uint16_t* gate_biases_dev,
+                                         const uint32_t* up_weight_dev, const uint16_t* up_scales_dev,
+                                         const uint16_t* up_biases_dev, void* stream, Gemma4QLinear** out) {
+    try {
+        if (out == nullptr)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qgeglu_create_device requires a non-null out pointer");
+        *out = nullptr;
+        Gemma4Status st = check_desc(desc, true, "gemma4_qgeglu_create_device");
+        if (st != GEMMA4_OK) return st;
+        if (!gate_weight_dev || !gate_scales_dev || !gate_biases_dev || !up_weight_dev || !up_scales_dev ||
+            !up_biases_dev)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT,
+                        "gemma4_qgeglu_create_device requires non-null weight, scales and biases for gate and up");
+        const Triple up{up_weight_dev, up_scales_dev, up_biases_dev};
+        return create_from_device(desc, Triple{gate_weight_dev, gate_scales_dev, gate_biases_dev}, &up, stream,
+                                  "gemma4_qgeglu_create_device", out);
+    } catch (...) {
+        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qgeglu_create_device: unexpected native exception");
     }
 }
 
@@ -265,55 +385,25 @@ Gemma4Status gemma4_qlinear_info(const Gemma4QLinear* linear, Gemma4QLinearInfo*
     out->group_size = linear->desc.group_size;
     out->device_bytes = linear->layout.tile_bytes() + linear->layout.sb_bytes();
     out->device = linear->device;
+    out->flags = linear->pair_rows ? GEMMA4_QLINEAR_GEGLU_PAIR : 0u;
     return ok();
 }
 
 Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
                                     uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype) {
     try {
-        if (!valid_handle(linear))
-            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_forward received an invalid handle");
-        if (y_dtype != GEMMA4_QMM_BF16 && y_dtype != GEMMA4_QMM_F32)
-            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_forward: y_dtype must be BF16 or F32");
-        if (rows == 0) return ok();
-        if (x_dev == nullptr || y_dev == nullptr)
-            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_forward requires non-null x and y");
-        if ((reinterpret_cast<uintptr_t>(x_dev) & 15u) != 0)
-            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_forward: x must be 16-byte aligned");
-        const uintptr_t yalign = y_dtype == GEMMA4_QMM_F32 ? 3u : 1u;
-        if ((reinterpret_cast<uintptr_t>(y_dev) & yalign) != 0)
-            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_forward: y is misaligned for its dtype");
-        if (rows > (1u << 24)) return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, "gemma4_qlinear_forward: rows exceeds 2^24");
-        if ((size_t)rows * linear->layout.k * 2 > q4::kMaxBufferBytes)
-            return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
-                        "gemma4_qlinear_forward: x exceeds 2 GiB (split the rows into several calls)");
-        DeviceGuard guard;
-        hipError_t e = guard.enter(linear->device);
-        if (e != hipSuccess) return hip_fail("gemma4_qlinear_forward: hipSetDevice", e);
-        hipStream_t st = static_cast<hipStream_t>(stream);
-        const bool f32 = y_dtype == GEMMA4_QMM_F32;
-        if ((int)rows < q4::kGemmMinRows) {
-            e = q4::launch_decode(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, f32, linear->layout, st);
-            if (e != hipSuccess) return hip_fail("gemma4_qlinear_forward: decode launch", e);
-            return ok();
-        }
-        // group sums of x live in a stream-ordered scratch allocation for this call
-        const size_t ws_bytes = q4::gemm_workspace_bytes((int)rows, linear->layout);
-        hipMemPool_t pool = nullptr;
-        e = scratch_pool(linear->device, &pool);
-        if (e != hipSuccess) return hip_fail("gemma4_qlinear_forward: scratch pool", e);
-        void* ws = nullptr;
-        e = hipMallocFromPoolAsync(&ws, ws_bytes, pool, st);
-        if (e != hipSuccess)
-            return fail(GEMMA4_ERR_MEMORY_GUARD, std::string("gemma4_qlinear_forward: workspace allocation failed: ") +
-                                                     hipGetErrorString(e));
-        e = q4::launch_gemm(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, f32, linear->layout, ws, st);
-        const hipError_t ef = hipFreeAsync(ws, st);
-        if (e != hipSuccess) return hip_fail("gemma4_qlinear_forward: gemm launch", e);
-        if (ef != hipSuccess) return hip_fail("gemma4_qlinear_forward: workspace release", ef);
-        return ok();
+        return run_forward(linear, stream, x_dev, rows, y_dev, y_dtype, false, "gemma4_qlinear_forward");
     } catch (...) {
         return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qgeglu_forward(const Gemma4QLinear* pair, void* stream, const uint16_t* x_dev, uint32_t rows,
+                                   void* h_dev, Gemma4QmmDtype h_dtype) {
+    try {
+        return run_forward(pair, stream, x_dev, rows, h_dev, h_dtype, true, "gemma4_qgeglu_forward");
+    } catch (...) {
+        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qgeglu_forward: unexpected native exception");
     }
 }
 
@@ -327,7 +417,8 @@ Gemma4Status gemma4_qlinear_dequantize(const Gemma4QLinear* linear, void* stream
         DeviceGuard guard;
         hipError_t e = guard.enter(linear->device);
         if (e != hipSuccess) return hip_fail("gemma4_qlinear_dequantize: hipSetDevice", e);
-        e = q4::launch_dequantize(linear->tiles, linear->sb, w_dev, linear->layout, static_cast<hipStream_t>(stream));
+        e = q4::launch_dequantize(linear->tiles, linear->sb, w_dev, linear->layout, linear->pair_rows,
+                                  static_cast<hipStream_t>(stream));
         if (e != hipSuccess) return hip_fail("gemma4_qlinear_dequantize: launch", e);
         return ok();
     } catch (...) {

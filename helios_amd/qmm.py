@@ -8,7 +8,10 @@ the same operations with the same argument meaning on device tensors:
 
 * :func:`quantized_matmul` / :func:`dequantize` — one-shot, MLX-style signatures;
 * :class:`QuantizedLinear` — the resident-weight form the call sites actually
-  need (weights loaded once, ``forward`` per step), one C-ABI handle each.
+  need (weights loaded once, ``forward`` per step), one C-ABI handle each;
+* :class:`QuantizedGeGLU` — gate and up as one resident pair whose ``forward``
+  returns ``geglu(x . Wg^T, x . Wu^T)``, the MLP front half of
+  ``native_model.cc:934-949`` with ``geglu`` (``:378-386``) fused in.
 
 Errors surface as :class:`Gemma4Error` carrying the C status and the native
 last-error text, as the reference's Rust wrapper does with ``check()``
@@ -59,7 +62,7 @@ class _Info(ctypes.Structure):
     _fields_ = [("out_features", ctypes.c_uint32), ("in_features", ctypes.c_uint32),
                 ("bits", ctypes.c_uint32), ("group_size", ctypes.c_uint32),
                 ("device_bytes", ctypes.c_uint64), ("device", ctypes.c_int32),
-                ("reserved", ctypes.c_uint32)]
+                ("flags", ctypes.c_uint32)]
 
 
 class _Version(ctypes.Structure):
@@ -69,12 +72,14 @@ class _Version(ctypes.Structure):
 
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
+GEGLU_PAIR = 1  # Gemma4QLinearInfo.flags
 
 _lib = None
 
 
 def load_library(path: str | None = None):
-    """Loads libgemma4_qmm.so (built by ``python -m helios_amd.build``)."""
+    """Loads libgemma4_qmm.so (built by ``python -m helios_amd.build``), or the build
+    at `path`, and makes it the library the classes and functions here call."""
     global _lib
     if _lib is not None and path is None:
         return _lib
@@ -93,13 +98,15 @@ def load_library(path: str | None = None):
         "gemma4_qlinear_info": [vp, ctypes.POINTER(_Info)],
         "gemma4_qlinear_forward": [vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int],
         "gemma4_qlinear_dequantize": [vp, vp, vp],
+        "gemma4_qgeglu_create": [ctypes.POINTER(_Desc), vp, vp, vp, vp, vp, vp, ctypes.POINTER(vp)],
+        "gemma4_qgeglu_create_device": [ctypes.POINTER(_Desc), vp, vp, vp, vp, vp, vp, vp, ctypes.POINTER(vp)],
+        "gemma4_qgeglu_forward": [vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = st
-    if path == LIB_PATH:
-        _lib = lib
+    _lib = lib
     return lib
 
 
@@ -146,7 +153,80 @@ def _check_spec(group_size: int, bits: int, mode: str, transpose: bool = True) -
                           f"only bits=4 group_size=64 is supported (got bits={bits} group_size={group_size})")
 
 
-class QuantizedLinear:
+def _host_triple(weight, scales, biases, n: int, k: int, group_size: int):
+    w = np.ascontiguousarray(weight, dtype=np.uint32)
+    s = np.ascontiguousarray(scales, dtype=np.uint16)
+    b = np.ascontiguousarray(biases, dtype=np.uint16)
+    if w.shape != (n, k // 8) or s.shape != (n, k // group_size) or b.shape != s.shape:
+        raise Gemma4Error(Status.INVALID_ARGUMENT, f"weight must be [{n}, {k // 8}] and scales/biases [{n}, {k // group_size}]")
+    return w, s, b
+
+
+def _device_triple(weight, scales, biases, n: int, k: int, group_size: int):
+    import torch
+
+    w = weight.contiguous()
+    s = scales.contiguous()
+    b = biases.contiguous()
+    if w.dtype not in (torch.int32, torch.uint32) or s.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise Gemma4Error(Status.INVALID_ARGUMENT, "weight must be int32/uint32 and scales/biases bfloat16")
+    if tuple(w.shape) != (n, k // 8) or tuple(s.shape) != (n, k // group_size) or tuple(b.shape) != tuple(s.shape):
+        raise Gemma4Error(Status.INVALID_ARGUMENT, f"weight must be [{n}, {k // 8}] and scales/biases [{n}, {k // group_size}]")
+    if not (w.is_cuda and s.is_cuda and b.is_cuda):
+        raise Gemma4Error(Status.INVALID_ARGUMENT, "device tensors must be on a CUDA (HIP) device")
+    return w, s, b
+
+
+def _host_ptrs(t):
+    return [a.ctypes.data_as(ctypes.c_void_p) for a in t]
+
+
+def _run_forward(fn, handle, lib, x, in_features: int, out_features: int, out=None, out_dtype=None, stream=None):
+    import torch
+
+    if out_dtype is None:
+        out_dtype = out.dtype if out is not None else torch.bfloat16
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise Gemma4Error(Status.INVALID_ARGUMENT, "out_dtype must be bfloat16 or float32")
+    if x.dtype != torch.bfloat16:
+        raise Gemma4Error(Status.INVALID_ARGUMENT, "x must be bfloat16")
+    if x.shape[-1] != in_features:
+        raise Gemma4Error(Status.INVALID_ARGUMENT, f"x last dim {x.shape[-1]} != in_features {in_features}")
+    lead = tuple(x.shape[:-1])
+    x2 = x.reshape(-1, in_features).contiguous()
+    rows = x2.shape[0]
+    if out is None:
+        out = torch.empty(lead + (out_features,), dtype=out_dtype, device=x.device)
+    elif out.dtype != out_dtype or tuple(out.shape) != lead + (out_features,) or not out.is_contiguous():
+        raise Gemma4Error(Status.INVALID_ARGUMENT, "out has the wrong dtype, shape or layout")
+    code = DTYPE_F32 if out_dtype == torch.float32 else DTYPE_BF16
+    check(fn(handle, _stream_ptr(stream), _dev_ptr(x2), rows, _dev_ptr(out), code), lib)
+    return out
+
+
+class _Handle:
+    """Owner of one ``Gemma4QLinear`` handle (freed by ``close`` or on collection)."""
+
+    _handle = None
+
+    def info(self) -> dict:
+        info = _Info()
+        check(self._lib.gemma4_qlinear_info(self._handle, ctypes.byref(info)), self._lib)
+        return {f: getattr(info, f) for f, _ in _Info._fields_}
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None) is not None and self._handle.value:
+            check(self._lib.gemma4_qlinear_free(self._handle), self._lib)
+            self._handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class QuantizedLinear(_Handle):
     """One projection's weight triple resident on the GPU (a ``Gemma4QLinear`` handle).
 
     ``weight`` uint32/int32 [N, K/8], ``scales``/``biases`` bf16 [N, K/64] in MLX
@@ -161,65 +241,25 @@ class QuantizedLinear:
         k = int(weight.shape[1]) * 32 // bits
         desc = _Desc(n, k, bits, group_size)
         if isinstance(weight, np.ndarray):
-            w = np.ascontiguousarray(weight, dtype=np.uint32)
-            s = np.ascontiguousarray(scales, dtype=np.uint16)
-            b = np.ascontiguousarray(biases, dtype=np.uint16)
-            if s.shape != (n, k // group_size) or b.shape != s.shape:
-                raise Gemma4Error(Status.INVALID_ARGUMENT, f"scales/biases must be [{n}, {k // group_size}]")
-            status = self._lib.gemma4_qlinear_create(ctypes.byref(desc), w.ctypes.data_as(ctypes.c_void_p),
-                                                     s.ctypes.data_as(ctypes.c_void_p),
-                                                     b.ctypes.data_as(ctypes.c_void_p),
-                                                     ctypes.byref(self._handle))
+            t = _host_triple(weight, scales, biases, n, k, group_size)
+            status = self._lib.gemma4_qlinear_create(ctypes.byref(desc), *_host_ptrs(t), ctypes.byref(self._handle))
         else:
             import torch
 
-            w = weight.contiguous()
-            s = scales.contiguous()
-            b = biases.contiguous()
-            if w.dtype not in (torch.int32, torch.uint32) or s.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
-                raise Gemma4Error(Status.INVALID_ARGUMENT, "weight must be int32/uint32 and scales/biases bfloat16")
-            if tuple(s.shape) != (n, k // group_size) or tuple(b.shape) != tuple(s.shape):
-                raise Gemma4Error(Status.INVALID_ARGUMENT, f"scales/biases must be [{n}, {k // group_size}]")
-            if not (w.is_cuda and s.is_cuda and b.is_cuda):
-                raise Gemma4Error(Status.INVALID_ARGUMENT, "device tensors must be on a CUDA (HIP) device")
-            with torch.cuda.device(w.device):
-                status = self._lib.gemma4_qlinear_create_device(
-                    ctypes.byref(desc), _dev_ptr(w), _dev_ptr(s), _dev_ptr(b), _stream_ptr(stream),
-                    ctypes.byref(self._handle))
+            t = _device_triple(weight, scales, biases, n, k, group_size)
+            with torch.cuda.device(t[0].device):
+                status = self._lib.gemma4_qlinear_create_device(ctypes.byref(desc), *map(_dev_ptr, t),
+                                                                _stream_ptr(stream), ctypes.byref(self._handle))
         check(status, self._lib)
         self.out_features = n
         self.in_features = k
         self.group_size = group_size
         self.bits = bits
 
-    def info(self) -> dict:
-        info = _Info()
-        check(self._lib.gemma4_qlinear_info(self._handle, ctypes.byref(info)), self._lib)
-        return {f: getattr(info, f) for f, _ in _Info._fields_ if f != "reserved"}
-
     def forward(self, x, out=None, out_dtype=None, stream=None):
         """y = x . W^T for x bf16 [..., K] on the device; returns [..., N]."""
-        import torch
-
-        if out_dtype is None:
-            out_dtype = out.dtype if out is not None else torch.bfloat16
-        if out_dtype not in (torch.bfloat16, torch.float32):
-            raise Gemma4Error(Status.INVALID_ARGUMENT, "out_dtype must be bfloat16 or float32")
-        if x.dtype != torch.bfloat16:
-            raise Gemma4Error(Status.INVALID_ARGUMENT, "x must be bfloat16")
-        if x.shape[-1] != self.in_features:
-            raise Gemma4Error(Status.INVALID_ARGUMENT, f"x last dim {x.shape[-1]} != in_features {self.in_features}")
-        lead = tuple(x.shape[:-1])
-        x2 = x.reshape(-1, self.in_features).contiguous()
-        rows = x2.shape[0]
-        if out is None:
-            out = torch.empty(lead + (self.out_features,), dtype=out_dtype, device=x.device)
-        elif out.dtype != out_dtype or tuple(out.shape) != lead + (self.out_features,) or not out.is_contiguous():
-            raise Gemma4Error(Status.INVALID_ARGUMENT, "out has the wrong dtype, shape or layout")
-        code = DTYPE_F32 if out_dtype == torch.float32 else DTYPE_BF16
-        check(self._lib.gemma4_qlinear_forward(self._handle, _stream_ptr(stream), _dev_ptr(x2), rows,
-                                               _dev_ptr(out), code), self._lib)
-        return out
+        return _run_forward(self._lib.gemma4_qlinear_forward, self._handle, self._lib, x, self.in_features,
+                            self.out_features, out, out_dtype, stream)
 
     __call__ = forward
 
@@ -236,16 +276,62 @@ class QuantizedLinear:
         check(self._lib.gemma4_qlinear_dequantize(self._handle, _stream_ptr(stream), _dev_ptr(out)), self._lib)
         return out
 
-    def close(self) -> None:
-        if getattr(self, "_handle", None) is not None and self._handle.value:
-            check(self._lib.gemma4_qlinear_free(self._handle), self._lib)
-            self._handle = ctypes.c_void_p()
 
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
+class QuantizedGeGLU(_Handle):
+    """Gate and up projections resident as one pair: ``forward(x)`` returns
+    ``h = geglu(x . Wg^T, x . Wu^T)`` [..., F], the reference's two quantized_linear
+    calls and ``geglu`` (``native_model.cc:934-949``, ``:378-386``) in one kernel.
+    In bf16 the qmm outputs and each GeGLU op round to bf16 as the reference's bf16
+    array ops do; in fp32 (the float32 override) everything stays fp32.  Triples as
+    for :class:`QuantizedLinear`; both must have the same shape."""
+
+    def __init__(self, gate, up, group_size: int = 64, bits: int = 4, stream=None):
+        _check_spec(group_size, bits, "affine")
+        self._lib = load_library()
+        self._handle = ctypes.c_void_p()
+        n = int(gate[0].shape[0])
+        k = int(gate[0].shape[1]) * 32 // bits
+        desc = _Desc(n, k, bits, group_size)
+        if isinstance(gate[0], np.ndarray):
+            tg = _host_triple(*gate, n, k, group_size)
+            tu = _host_triple(*up, n, k, group_size)
+            status = self._lib.gemma4_qgeglu_create(ctypes.byref(desc), *_host_ptrs(tg), *_host_ptrs(tu),
+                                                    ctypes.byref(self._handle))
+        else:
+            import torch
+
+            tg = _device_triple(*gate, n, k, group_size)
+            tu = _device_triple(*up, n, k, group_size)
+            with torch.cuda.device(tg[0].device):
+                status = self._lib.gemma4_qgeglu_create_device(ctypes.byref(desc), *map(_dev_ptr, tg),
+                                                               *map(_dev_ptr, tu), _stream_ptr(stream),
+                                                               ctypes.byref(self._handle))
+        check(status, self._lib)
+        self.out_features = n
+        self.in_features = k
+        self.group_size = group_size
+        self.bits = bits
+
+    def forward(self, x, out=None, out_dtype=None, stream=None):
+        """h = geglu(x . Wg^T, x . Wu^T) for x bf16 [..., K] on the device; returns [..., F]."""
+        return _run_forward(self._lib.gemma4_qgeglu_forward, self._handle, self._lib, x, self.in_features,
+                            self.out_features, out, out_dtype, stream)
+
+    __call__ = forward
+
+    def forward_raw(self, x_ptr: int, rows: int, h_ptr: int, f32: bool = False, stream_ptr: int = 0) -> None:
+        """Direct C-ABI call on raw device pointers (benchmark loops)."""
+        check(self._lib.gemma4_qgeglu_forward(self._handle, ctypes.c_void_p(stream_ptr), ctypes.c_void_p(x_ptr),
+                                              rows, ctypes.c_void_p(h_ptr), DTYPE_F32 if f32 else DTYPE_BF16),
+              self._lib)
+
+    def dequantize(self, stream=None):
+        """fp32 [2, F, K]: the gate rows, then the up rows (bit-exact)."""
+        import torch
+
+        out = torch.empty((2, self.out_features, self.in_features), dtype=torch.float32, device="cuda")
+        check(self._lib.gemma4_qlinear_dequantize(self._handle, _stream_ptr(stream), _dev_ptr(out)), self._lib)
+        return out
 
 
 def quantized_matmul(x, w, scales, biases, transpose: bool = True, group_size: int = 64, bits: int = 4,

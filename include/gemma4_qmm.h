@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define GEMMA4_QMM_ABI_VERSION 1u
+#define GEMMA4_QMM_ABI_VERSION 2u
 
 /* Same codes as the reference status enum (gemma4_mlx.h:12-21); defined here only
  * when that header has not been included first. */
@@ -95,8 +95,10 @@ typedef struct Gemma4QLinearInfo {
     uint32_t group_size;
     uint64_t device_bytes; /* resident bytes of the tiled weight triple */
     int32_t device;        /* HIP device ordinal that holds it */
-    uint32_t reserved;
+    uint32_t flags;        /* GEMMA4_QLINEAR_GEGLU_PAIR for a gate|up pair */
 } Gemma4QLinearInfo;
+
+#define GEMMA4_QLINEAR_GEGLU_PAIR 1u
 
 /* Replaces gemma4_runtime_version (runtime.cc:805-814) for this library. */
 Gemma4Status gemma4_qmm_runtime_version(Gemma4QmmVersionInfo* out);
@@ -134,8 +136,37 @@ Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, c
 
 /* Writes the fp32 dequantized weight W[N,K] = s*q + b (row-major) to w_dev —
  * mlx::core::dequantize (native_model.cc:364-376) with a float32 result.  Bit-exact:
- * the product s*q is exact in fp32, so the value is unique. */
+ * the product s*q is exact in fp32, so the value is unique.  For a gate|up pair the
+ * output is [2, F, K]: the gate rows, then the up rows. */
 Gemma4Status gemma4_qlinear_dequantize(const Gemma4QLinear* linear, void* stream, float* w_dev);
+
+/* ---- Fused gate|up projection with the GeGLU epilogue ----
+ * Replaces the reference's MLP front half, two quantized_linear calls on the same
+ * input followed by geglu (native_model.cc:934-949 prefill, :1318-1321 decode, and
+ * geglu itself at native_model.cc:378-386):
+ *     h[M,F] = geglu(x . Wg^T, x . Wu^T),  geglu(g, u) = 0.5*g*(1+tanh(c1*(g+c2*g^3)))*u
+ * in one pass over both weight matrices, without writing gate and up to memory.
+ * With h_dtype BF16 the qmm outputs and every GeGLU op are rounded to bf16 as the
+ * reference's bf16 array ops are (constants bf16(0.7978845608), bf16(0.044715));
+ * with F32 everything stays fp32 (the GEMMA4D_NATIVE_FORCE_FLOAT32 path).  The pair
+ * is one Gemma4QLinear handle (freed with gemma4_qlinear_free; info reports
+ * out_features = F and flags = GEMMA4_QLINEAR_GEGLU_PAIR); desc describes one of
+ * the two projections (out_features = F, the same K, bits and group size for both). */
+Gemma4Status gemma4_qgeglu_create(const Gemma4QLinearDesc* desc, const uint32_t* gate_weight,
+                                  const uint16_t* gate_scales, const uint16_t* gate_biases, const uint32_t* up_weight,
+                                  const uint16_t* up_scales, const uint16_t* up_biases, Gemma4QLinear** out);
+
+/* Same, from device memory in MLX layout (as gemma4_qlinear_create_device). */
+Gemma4Status gemma4_qgeglu_create_device(const Gemma4QLinearDesc* desc, const uint32_t* gate_weight_dev,
+                                         const uint16_t* gate_scales_dev, const uint16_t* gate_biases_dev,
+                                         const uint32_t* up_weight_dev, const uint16_t* up_scales_dev,
+                                         const uint16_t* up_biases_dev, void* stream, Gemma4QLinear** out);
+
+/* h[M,F] = geglu(x . Wg^T, x . Wu^T) on a handle from gemma4_qgeglu_create*.  x as for
+ * gemma4_qlinear_forward; h is [rows, F] of h_dtype in device memory.  A plain
+ * projection handle is rejected here, and a pair is rejected by gemma4_qlinear_forward. */
+Gemma4Status gemma4_qgeglu_forward(const Gemma4QLinear* pair, void* stream, const uint16_t* x_dev, uint32_t rows,
+                                   void* h_dev, Gemma4QmmDtype h_dtype);
 
 #ifdef __cplusplus
 }

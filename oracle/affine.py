@@ -196,13 +196,35 @@ def make_activations(m: int, k: int, seed: int, outliers: bool = False) -> np.nd
     return f32_to_bf16_bits(x)
 
 
-def gelu_tanh_times(gate_bits, up_bits) -> np.ndarray:
-    """GeGLU as native_model.cc:378-386: 0.5*g*(1+tanh(0.79788456*(g+0.044715*g^3)))*up.
+# GeGLU constants of native_model.cc:379-380 (model_scalar makes them bf16 in the bf16
+# model dtype, native_model.cc:342-347)
+GEGLU_C_TANH = 0.7978845608028654
+GEGLU_C_CUBIC = 0.044715
 
-    Evaluated in fp32 on the bf16 inputs, rounded once to bf16 (the harness feeds
-    identical bf16 bytes to the GPU and the oracle, so only determinism matters)."""
-    g = bf16_bits_to_f32(gate_bits).astype(np.float32)
-    u = bf16_bits_to_f32(up_bits).astype(np.float32)
-    inner = np.float32(0.7978845608028654) * (g + np.float32(0.044715) * g * g * g)
-    gelu = np.float32(0.5) * g * (np.float32(1) + np.tanh(inner))
-    return f32_to_bf16_bits((gelu * u).astype(np.float32))
+
+def geglu_ops(gate, up, bf16: bool) -> np.ndarray:
+    """GeGLU of native_model.cc:378-386 evaluated op by op as the reference's array
+    ops do: gelu = (0.5 * g) * (1 + tanh(c1 * (g + c2 * g**3))), h = gelu * up.
+
+    Each op is one float32 operation.  With ``bf16`` (the model dtype) the inputs,
+    the constants and every intermediate are bf16, so each op's result is rounded to
+    bf16; otherwise (the float32 override, native_model.cc:330-347) all stay float32.
+    ``g**3`` is ``g*g*g`` (exact in float32 for bf16 g).  Returns float32 values
+    (bf16-representable when ``bf16``)."""
+    f32 = np.float32
+    g = np.asarray(gate, dtype=np.float32)
+    u = np.asarray(up, dtype=np.float32)
+    r = round_to_bf16 if bf16 else (lambda v: np.asarray(v, dtype=np.float32))
+    c_tanh, c_cubic = r(f32(GEGLU_C_TANH)), r(f32(GEGLU_C_CUBIC))
+    g, u = r(g), r(u)
+    g3 = r(g * g * g)
+    a = r(g + r(c_cubic * g3))
+    t = r(np.tanh(r(c_tanh * a)))
+    gelu = r(r(f32(0.5) * g) * r(f32(1.0) + t))
+    return r(gelu * u)
+
+
+def gelu_tanh_times(gate_bits, up_bits) -> np.ndarray:
+    """bf16 GeGLU of bf16 gate/up bit patterns (``geglu_ops`` in the bf16 model
+    dtype), as bf16 bits: the down_proj input of the prefill chain."""
+    return f32_to_bf16_bits(geglu_ops(bf16_bits_to_f32(gate_bits), bf16_bits_to_f32(up_bits), bf16=True))

@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_runtime_version(lib):
     v = qmm.runtime_version()
-    assert v["abi_version"] == 1 and v["backend_name"] == "gemma4_qmm"
+    assert v["abi_version"] == 2 and v["backend_name"] == "gemma4_qmm"
     assert qmm.last_error() == ""
 
 
@@ -82,6 +82,28 @@ def test_null_and_invalid_arguments_set_last_error(lib):
     assert lib.gemma4_qmm_get_last_error(None, 0) == qmm.Status.INVALID_ARGUMENT
 
 
+def test_geglu_pair_argument_checks(lib):
+    out = ctypes.c_void_p()
+    assert lib.gemma4_qgeglu_create(None, None, None, None, None, None, None, ctypes.byref(out)) == \
+        qmm.Status.INVALID_ARGUMENT
+    assert "non-null desc" in qmm.last_error()
+    desc = qmm._Desc(15360, 3840, 4, 64)
+    assert lib.gemma4_qgeglu_create(ctypes.byref(desc), None, None, None, None, None, None, None) == \
+        qmm.Status.INVALID_ARGUMENT
+    assert "out pointer" in qmm.last_error()
+    assert lib.gemma4_qgeglu_create(ctypes.byref(desc), None, None, None, None, None, None, ctypes.byref(out)) == \
+        qmm.Status.INVALID_ARGUMENT
+    assert "gate and up" in qmm.last_error()
+    desc = qmm._Desc(64, 64, 8, 64)
+    assert lib.gemma4_qgeglu_create_device(ctypes.byref(desc), None, None, None, None, None, None, None,
+                                           ctypes.byref(out)) == qmm.Status.UNSUPPORTED_CONFIG
+    assert out.value is None
+    bogus = ctypes.create_string_buffer(64)
+    assert lib.gemma4_qgeglu_forward(ctypes.cast(bogus, ctypes.c_void_p), None, None, 1, None, 0) == \
+        qmm.Status.INVALID_ARGUMENT
+    assert "invalid handle" in qmm.last_error()
+
+
 def test_last_error_is_thread_local(lib):
     out = ctypes.c_void_p()
     assert lib.gemma4_qlinear_create(None, None, None, None, ctypes.byref(out)) != 0
@@ -101,6 +123,7 @@ def test_struct_layouts_match_header():
     assert ctypes.sizeof(qmm._Desc) == 16
     assert ctypes.sizeof(qmm._Info) == 32
     assert qmm._Info.device_bytes.offset == 16 and qmm._Info.device.offset == 24
+    assert qmm._Info.flags.offset == 28
     assert ctypes.sizeof(qmm._Version) == 24
 
 

@@ -1,4 +1,4 @@
-"""Checks on the compiled gfx950 code of the GEMM (CPU only: hipcc cross-compiles).
+"""Checks on the compiled gfx950 code (CPU only: hipcc cross-compiles).
 
 The GEMM issues its LDS DMAs (`buffer_load_dwordx4 ... lds`) from inline asm, which
 the compiler's hazard recognizer cannot see into.  A VALU write of an SGPR (for
@@ -43,7 +43,7 @@ def gemm_asm():
 
 def test_lds_dma_sgpr_hazards_covered(gemm_asm):
     kernels = list(_kernels(gemm_asm))
-    assert len(kernels) == 2  # bf16 and fp32 outputs
+    assert len(kernels) == 4  # bf16 / fp32 outputs, bf16 / fp32 GeGLU pairs
     for name, lines in kernels:
         dmas = 0
         for i, line in enumerate(lines):
@@ -72,3 +72,21 @@ def test_no_spills_and_lds_budget(gemm_asm):
         assert vals and max(vals) == 0, (field, vals)
     lds = [int(v) for v in re.findall(r"\.group_segment_fixed_size:\s+(\d+)", gemm_asm)]
     assert max(lds) <= 160 * 1024
+
+
+def _kernel_meta(asm: str):
+    """(name, vgpr_count, spill bytes) of every kernel in the metadata block."""
+    for m in re.finditer(r"- \.agpr_count:.*?\.name:\s+(\S+).*?\.private_segment_fixed_size:\s+(\d+).*?"
+                         r"\.vgpr_count:\s+(\d+)", asm, re.S):
+        yield m.group(1), int(m.group(3)), int(m.group(2))
+
+
+def test_decode_register_budgets():
+    asm = hbuild.device_asm("q4_decode.hip")
+    meta = list(_kernel_meta(asm))
+    assert any("decode_stream_kernel" in n for n, _, _ in meta)
+    for name, vgprs, private in meta:
+        assert private == 0, f"{name} spills to scratch"
+        if "decode_stream_kernel" in name:
+            # two 8-wave workgroups per CU (the launcher's occupancy assumption)
+            assert vgprs <= 128, f"{name}: {vgprs} VGPRs"

@@ -7,17 +7,19 @@ projections q, k, v, o, gate, up, down of the Gemma-style 12B layer (hidden 3840
 16 q heads x 256, 8 KV heads x 256, FFN 15360), all 4-bit group-64 affine, at
 batch M=1.  They run as the model's data dependencies allow: q|k|v as one fused
 projection (weights concatenated along N at load, all read the same x), then o,
-then gate|up fused, then down.  Weights are synthetic (N(0, 0.02) rounded to bf16,
+then gate and up as one pair with the GeGLU epilogue (gemma4_qgeglu_forward, whose
+output h feeds down), then down.  Weights are synthetic (N(0, 0.02) rounded to bf16,
 then quantized), activations N(0, 1) in bf16.  `value` is algorithmic bytes per
-step (packed W + bf16 scales/biases + bf16 x + bf16 y, see algo_bytes) / measured
-step time, with the weights already resident in HBM, timed over graph replays of
+step (packed W + bf16 scales/biases + bf16 x + bf16 y of the seven projections,
+see algo_bytes) / measured step time, with the weights already resident in HBM, timed over graph replays of
 the step.  The loop rotates over enough distinct weight copies (>= 512 MiB) that
 the 256 MiB Infinity Cache cannot serve them.
 
-Also reported: the dominant kernel's roofline (the fused gate|up GEMV, timed per
-launch from graph replays of back-to-back launches), every projection at M = 1, 4,
-8, the lm_head at M = 1, 8, 16, the prefill GEMM at M=2048, and the CPU baseline
-(the oracle's fp32 loop on the host cores, on a bounded sample of the same work).
+Also reported: the dominant kernel's roofline (the gate|up GeGLU pair at M=1, timed
+per launch from graph replays of back-to-back launches), every projection at M = 1,
+4, 8, the lm_head at M = 1, 8, 16, the prefill GEMM at M = 512 and 2048 (the seven
+projections and the GeGLU pair), and the CPU baseline (the oracle's fp32 loop on the
+host cores, on a bounded sample of the same work).
 
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--quick]
     python bench.py --roofline-only   # the dominant kernel and a 1 GiB copy only (for rocprofv3)
@@ -56,14 +58,16 @@ LAYER = [
     ("up_proj", 15360, 3840),
     ("down_proj", 3840, 15360),
 ]
-# launches of one decode step: projections sharing x are fused along N
+# launches of one decode step: projections sharing x are fused along N; gate and up
+# form the GeGLU pair (output h [M, 15360])
 STEP = [("qkv_proj", ("q_proj", "k_proj", "v_proj")), ("o_proj", ("o_proj",)),
-        ("gate_up_proj", ("gate_proj", "up_proj")), ("down_proj", ("down_proj",))]
+        ("gate_up_geglu", ("gate_proj", "up_proj")), ("down_proj", ("down_proj",))]
+PAIR = "gate_up_geglu"
 SEED_BASE = 20260630
 ROTATE_BYTES = 512 << 20
 COPY_BYTES = 1 << 30
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_decode_m1_traffic.json")
-# the kernel that runs the fused gate|up projection at M = 1 (30720 rows: one wave per
+# the kernel that runs the gate|up GeGLU pair at M = 1 (2 x 15360 rows: one wave per
 # 16-row block)
 DOM_KERNEL = "decode_rows_kernel"
 
@@ -71,6 +75,11 @@ DOM_KERNEL = "decode_rows_kernel"
 def algo_bytes(m: int, n: int, k: int, y_bytes: int = 2) -> int:
     """Packed W + bf16 scales and biases + bf16 x + y."""
     return n * k // 2 + 4 * n * (k // 64) + 2 * m * k + y_bytes * m * n
+
+
+def pair_algo_bytes(m: int, f: int, k: int) -> int:
+    """The GeGLU pair: both packed weights with scales and biases + bf16 x + bf16 h."""
+    return 2 * f * k // 2 + 2 * 4 * f * (k // 64) + 2 * m * k + 2 * m * f
 
 
 def algo_flops(m: int, n: int, k: int) -> int:
@@ -127,12 +136,11 @@ def graph_ms(torch, fn, replays: int, warmup: int) -> float:
     return ms
 
 
-def kernel_us(torch, Q, triple, m: int, k: int, n: int, xdev, reps_per_graph: int = 40) -> float:
-    """Average duration of one forward launch: back-to-back launches over rotated
-    weight copies, captured in a graph and replayed."""
-    wbytes = n * k // 2 + 4 * n * (k // 64)
+def kernel_us(torch, make, m: int, k: int, n: int, xdev, wbytes: int, reps_per_graph: int = 40) -> float:
+    """Average duration of one forward launch (of make(), output [m, n]): back-to-back
+    launches over rotated weight copies, captured in a graph and replayed."""
     copies = max(2, -(-ROTATE_BYTES // wbytes))
-    lins = [Q.QuantizedLinear(*triple) for _ in range(copies)]
+    lins = [make() for _ in range(copies)]
     y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
     launches = max(copies, (reps_per_graph // copies) * copies)
 
@@ -354,34 +362,47 @@ def main() -> int:
     torch.cuda.set_device(0)
     log("quantizing one decoder layer")
     host = quantized_layer()
-    fused = {name: fused_triple(host, parts) for name, parts in STEP}
-    fused_nk = {name: (sum(dict((l[0], l[1]) for l in LAYER)[p] for p in parts), dict((l[0], l[2]) for l in LAYER)[parts[0]])
-                for name, parts in STEP}
+    dims = {name: (n, k) for name, n, k in LAYER}
+    fused = {name: fused_triple(host, parts) for name, parts in STEP if name != PAIR}
+    # N of each launch's output and its K
+    step_nk = {name: (sum(dims[p][0] for p in parts) if name != PAIR else dims[parts[0]][0], dims[parts[0]][1])
+               for name, parts in STEP}
+    wbytes_of = {name: sum(dims[p][0] * dims[p][1] // 2 + 4 * dims[p][0] * (dims[p][1] // 64) for p in parts)
+                 for name, parts in STEP}
+
+    def maker(name):
+        if name == PAIR:
+            return lambda: Q.QuantizedGeGLU(host["gate_proj"], host["up_proj"])
+        return lambda: Q.QuantizedLinear(*fused[name])
+
     xs = {k: torch.from_numpy(A.make_activations(16, k, seed=SEED_BASE + k).view(np.int16)).view(torch.bfloat16).cuda()
           for k in {k for _, _, k in LAYER}}
-    n_gu, k_gu = fused_nk["gate_up_proj"]
-    gu_bytes = algo_bytes(1, n_gu, k_gu)
-    gu_kernel = f"{DOM_KERNEL}<1,4,3> gate|up fused N={n_gu} K={k_gu} M=1"
+    f_gu, k_gu = step_nk[PAIR]
+    gu_bytes = pair_algo_bytes(1, f_gu, k_gu)
+    gu_kernel = f"{DOM_KERNEL}<1,4,3> gate|up GeGLU pair F={f_gu} K={k_gu} M=1"
+
+    def pair_us(m):
+        return kernel_us(torch, maker(PAIR), m, k_gu, f_gu, xs[k_gu], wbytes_of[PAIR])
 
     if args.roofline_only:
-        us_gu = kernel_us(torch, Q, fused["gate_up_proj"], 1, k_gu, n_gu, xs[k_gu])
+        us_gu = pair_us(1)
         cgbs = copy_gbs(torch)
         print(json.dumps({"kernel": gu_kernel, "algo_bytes_per_launch": gu_bytes, "avg_launch_us": round(us_gu, 3),
                           "achieved_GBps": round(gu_bytes / (us_gu * 1e-6) / 1e9, 1),
                           "copy_bytes": COPY_BYTES, "copy_GBps": round(cgbs, 1)}), flush=True)
         return 0
 
-    layer_w_bytes = sum(n * k // 2 + 4 * n * (k // 64) for _, n, k in LAYER)
+    layer_w_bytes = sum(wbytes_of.values())
     copies = max(2, -(-ROTATE_BYTES // layer_w_bytes))
     log(f"uploading {copies} copies of the layer ({copies * layer_w_bytes / 2**20:.0f} MiB)")
-    layers = [{name: Q.QuantizedLinear(*fused[name]) for name, _ in STEP} for _ in range(copies)]
-    ys = {name: torch.empty((16, n), dtype=torch.bfloat16, device="cuda") for name, (n, _) in fused_nk.items()}
+    layers = [{name: maker(name)() for name, _ in STEP} for _ in range(copies)]
+    ys = {name: torch.empty((16, n), dtype=torch.bfloat16, device="cuda") for name, (n, _) in step_nk.items()}
 
     def step_fn(m):
         def fn():
             for c in range(copies):
                 for name, _ in STEP:
-                    n, k = fused_nk[name]
+                    n, k = step_nk[name]
                     layers[c][name].forward(xs[k][:m], out=ys[name][:m])
         return fn
 
@@ -400,8 +421,8 @@ def main() -> int:
             lin.close()
     del layers
 
-    # --- dominant kernel: fused gate|up GEMV at M=1 ---
-    us_gu = kernel_us(torch, Q, fused["gate_up_proj"], 1, k_gu, n_gu, xs[k_gu])
+    # --- dominant kernel: the gate|up GeGLU pair at M=1 ---
+    us_gu = pair_us(1)
     gu_gbs = gu_bytes / (us_gu * 1e-6) / 1e9
     traffic, traffic_rec = recorded_traffic(gu_kernel, gu_bytes)
     roofline = {
@@ -423,14 +444,15 @@ def main() -> int:
     if not args.quick:
         for m in (1, 4, 8):
             for name, n, k in LAYER:
-                us = kernel_us(torch, Q, host[name], m, k, n, xs[k])
+                us = kernel_us(torch, lambda: Q.QuantizedLinear(*host[name]), m, k, n, xs[k],
+                               n * k // 2 + 4 * n * (k // 64))
                 per_proj[f"{name}_m{m}"] = {"us": round(us, 2), "GBps": round(algo_bytes(m, n, k) / (us * 1e-6) / 1e9, 1)}
-            for name, _ in STEP:
-                if len(dict(STEP)[name]) > 1:
-                    n, k = fused_nk[name]
-                    us = kernel_us(torch, Q, fused[name], m, k, n, xs[k])
-                    per_proj[f"{name}_m{m}"] = {"us": round(us, 2),
-                                                "GBps": round(algo_bytes(m, n, k) / (us * 1e-6) / 1e9, 1)}
+            n, k = step_nk["qkv_proj"]
+            us = kernel_us(torch, maker("qkv_proj"), m, k, n, xs[k], wbytes_of["qkv_proj"])
+            per_proj[f"qkv_proj_m{m}"] = {"us": round(us, 2), "GBps": round(algo_bytes(m, n, k) / (us * 1e-6) / 1e9, 1)}
+            us = pair_us(m)
+            per_proj[f"{PAIR}_m{m}"] = {"us": round(us, 2),
+                                        "GBps": round(pair_algo_bytes(m, f_gu, k_gu) / (us * 1e-6) / 1e9, 1)}
         try:
             from oracle import c_oracle as C
 
@@ -441,7 +463,8 @@ def main() -> int:
             del lm_w
             lm = {}
             for m in (1, 8, 16):
-                us = kernel_us(torch, Q, lm_triple, m, HIDDEN, 262144, xs[HIDDEN], reps_per_graph=4)
+                us = kernel_us(torch, lambda: Q.QuantizedLinear(*lm_triple), m, HIDDEN, 262144, xs[HIDDEN],
+                               262144 * HIDDEN // 2 + 4 * 262144 * (HIDDEN // 64), reps_per_graph=4)
                 lm[f"m{m}"] = {"us": round(us, 1), "GBps": round(algo_bytes(m, 262144, HIDDEN) / (us * 1e-6) / 1e9, 1)}
             del lm_triple
         except Exception as e:  # memory or build problems should not hide the headline
@@ -465,6 +488,15 @@ def main() -> int:
                 gemm[f"{name}_m{m}"] = {"us": round(ms * 1e3, 1), "TFLOPS": round(tflops, 1),
                                         "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
                 del ym
+            if not args.quick:  # the GeGLU pair: gate and up in one GEMM, h = geglu(gate, up)
+                hm = torch.empty((m, f_gu), dtype=torch.bfloat16, device="cuda")
+                pair = Q.QuantizedGeGLU(host["gate_proj"], host["up_proj"])
+                ms = graph_ms(torch, lambda: pair.forward(xk[k_gu], out=hm), replays=10, warmup=2)
+                pair.close()
+                tflops = algo_flops(m, 2 * f_gu, k_gu) / (ms * 1e-3) / 1e12
+                gemm[f"{PAIR}_m{m}"] = {"us": round(ms * 1e3, 1), "TFLOPS": round(tflops, 1),
+                                        "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
+                del hm
             del xk
         head = gemm["gate_proj_m2048"]
         gemm["headline"] = {"shape": "gate_proj M=2048 N=15360 K=3840", **head}
@@ -496,7 +528,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": "one Gemma-style 12B decoder layer's 7 projections (q,k,v,o,gate,up,down) at decode M=1, "
-                        "4-bit group-64 affine, hidden 3840, FFN 15360; launched as qkv, o, gate_up, down",
+                        "4-bit group-64 affine, hidden 3840, FFN 15360; launched as qkv, o, gate|up GeGLU pair, down",
             "global_batch": 1,
             "parallelism": "none (1 GPU)",
             "weight_copies_rotated": copies,

@@ -140,16 +140,28 @@ __device__ __forceinline__ float round_bf16(float v) { return (float)(__bf16)v; 
 // contracts by default, also across the header's __fmul_rn / __fadd_rn, which are
 // plain operators).  g^3 is g*g*g: exact in fp32 for a bf16 g (at most 24
 // significant bits), and within an ulp of the reference's pow(g, 3) for an fp32 g.
-__device__ __forceinline__ float geglu_bf16(float gate, float up) {
+// gelu of a bf16 g in the bf16 op sequence: a function of g's 16 bits only, so the
+// GEMM epilogue reads it from a 65536-entry table built by this same code.
+__device__ __forceinline__ float gelu_bf16(float g) {
 #pragma clang fp contract(off)
     const float c_tanh = 0.796875f;           // bf16(0.7978845608028654)
     const float c_cubic = 0.044677734375f;    // bf16(0.044715)
-    const float g = round_bf16(gate), u = round_bf16(up);
     const float g3 = round_bf16(g * g * g);
     const float a = round_bf16(g + round_bf16(c_cubic * g3));
     const float t = round_bf16(tanhf(round_bf16(c_tanh * a)));
-    const float gelu = round_bf16(round_bf16(0.5f * g) * round_bf16(1.0f + t));
-    return round_bf16(gelu * u);
+    return round_bf16(round_bf16(0.5f * g) * round_bf16(1.0f + t));
+}
+
+__device__ __forceinline__ float geglu_bf16(float gate, float up) {
+#pragma clang fp contract(off)
+    return round_bf16(gelu_bf16(round_bf16(gate)) * round_bf16(up));
+}
+
+// The same from the table of gelu_bf16 over all bf16 bit patterns.
+__device__ __forceinline__ float geglu_bf16_table(const uint16_t* __restrict__ table, float gate, float up) {
+#pragma clang fp contract(off)
+    const float gelu = __uint_as_float((uint32_t)table[f32_to_bf16(gate)] << 16);
+    return round_bf16(gelu * round_bf16(up));
 }
 
 __device__ __forceinline__ float geglu_f32(float g, float u) {
@@ -194,6 +206,22 @@ __device__ __forceinline__ void store_out(void* y, int mode, int m, int m_rows, 
         }
     }
 }
+
+// GeGLU of two accumulators of one column, rows m0 (v0) and m1 (v1), with every lane
+// doing useful work: lanes col < 8 hold gate, lanes col >= 8 up.  After one exchange
+// lane col < 8 has (gate, up) of row m0 for h column 8*rb + col, and lane col >= 8
+// has (gate, up) of row m1 for h column 8*rb + col - 8 (geglu2_row / geglu2_col give
+// the lane's output coordinates).  All lanes of the wave call it together.  In bf16
+// gelu comes from `table` (gelu_bf16 of every bf16 pattern).
+__device__ __forceinline__ float geglu2(int mode, int col, float v0, float v1, const uint16_t* __restrict__ table) {
+    const bool lo = col < 8;
+    const float other = row_swap8(lo ? v1 : v0);  // lo: up of row m0; hi: gate of row m1
+    const float g = lo ? v0 : other;
+    const float u = lo ? other : v1;
+    return mode == kOutGegluF32 ? geglu_f32(g, u) : geglu_bf16_table(table, g, u);
+}
+__device__ __forceinline__ int geglu2_row(int col, int m0, int m1) { return col < 8 ? m0 : m1; }
+__device__ __forceinline__ int geglu2_col(int col, int rb) { return rb * 8 + (col & 7); }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

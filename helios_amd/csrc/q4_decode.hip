@@ -521,9 +521,12 @@ inline Split choose_split(int gpairs, int mt) {
 }
 
 constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950 LDS per CU (and per workgroup)
-// row-block-per-wave kernel: from this many 16-row blocks, 4 waves per workgroup,
-// at most this many workgroups per CU
-constexpr int kRowsMinBlocks = 512;
+// row-block-per-wave kernel: M = 1 with this many 16-row blocks, 4 waves per
+// workgroup, at most this many workgroups per CU.  Measured against the streaming
+// kernel: ~0.4 us ahead for gate (960 blocks) and gate|up (1920); behind for the
+// qkv-sized 512 blocks, for the lm_head's 16384 and for every M > 1.
+constexpr int kRowsMinBlocks = 768;
+constexpr int kRowsMaxBlocks = 4096;
 constexpr int kRowsWaves = 4;
 constexpr int kRowsPerCu = 2;
 
@@ -535,8 +538,8 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, voi
     constexpr int R = MT < 4 ? MT : 4;
     const size_t static_lds = 2 * 8 * R * 64 * sizeof(float);
     const size_t lds_bytes = (size_t)m * (l.k + GPW * 128) * 2 + (size_t)(l.gp + GPW) * 2 * 16 * 4;
-    if constexpr (MT <= 4) {
-        if (l.nb >= kRowsMinBlocks && lds_bytes <= kLdsPerCu) {
+    if constexpr (MT == 1) {
+        if (l.nb >= kRowsMinBlocks && l.nb <= kRowsMaxBlocks && lds_bytes <= kLdsPerCu) {
             // many row blocks: one wave per block, no cross-wave reduction
             int grid = (l.nb + kRowsWaves - 1) / kRowsWaves;
             const int cap = device_cus() * kRowsPerCu;

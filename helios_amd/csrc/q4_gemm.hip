@@ -126,7 +126,8 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
                                                    const uint16_t* __restrict__ x, const uint4* __restrict__ xaug,
                                                    void* __restrict__ y, int m_rows, int n_rows, int k, int groups,
                                                    int gpairs, int mtiles, int ntiles, int octets, uint32_t tile_bytes,
-                                                   uint32_t sb_bytes, int g_split, long split_stride, int n_out) {
+                                                   uint32_t sb_bytes, int g_split, long split_stride, int n_out,
+                                                   const uint16_t* __restrict__ gelu_table) {
     int mt, nt;
     tile_of((int)blockIdx.x, (int)gridDim.x, mtiles, ntiles, mt, nt);
     // split of K: groups [g_begin, g_end), whole octets; with several splits each
@@ -365,21 +366,62 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         bias();
     }
 
-    // store: lane holds rows 4*kq + e of column col of each 16x16 tile
+    // store: lane holds rows 4*kq + e of column col of each 16x16 tile.  The GeGLU
+    // store takes its lane coordinates afresh (mbcnt), so nothing lane-dependent of
+    // its own stays live across the main loop (which runs at the 256-VGPR limit).
+    const int slane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
 #pragma unroll
     for (int i = 0; i < kMT; ++i) {
 #pragma unroll
         for (int j = 0; j < kNT; ++j) {
             const int rb = rbw + wn * kNT + j;
+            if constexpr (OUT == kOutGegluBf16) {  // rows e and e + 1 share one GeGLU pass
+                // all values first, stores after the loop: with no store between them
+                // the table reads are issued together rather than waited for one by one
+                acc[i][j][0] = geglu2(OUT, slane & 15, acc[i][j][0], acc[i][j][1], gelu_table);
+                acc[i][j][2] = geglu2(OUT, slane & 15, acc[i][j][2], acc[i][j][3], gelu_table);
+                continue;
+            }
+            if constexpr (OUT == kOutGegluF32) {  // no memory reads: value and store together
+                const int c = slane & 15;
+                const int m = mt * kBM + wm * kWM + 16 * i + 4 * (slane >> 4);
+                const int hn = geglu2_col(c, rb);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int m = mt * kBM + wm * kWM + 16 * i + 4 * kq + e;
-                if constexpr (OUT == kOutF32) {  // fp32 output, or this split's partial plane
-                    const int n = rb * 16 + col;
-                    if (m < m_rows && n < n_rows)
-                        static_cast<float*>(y)[(long)blockIdx.y * split_stride + (long)m * n_rows + n] = acc[i][j][e];
-                } else {
-                    store_out(y, OUT, m, m_rows, rb, col, n_rows, n_out, acc[i][j][e]);
+                for (int e = 0; e < 4; e += 2) {
+                    const float h = geglu2(OUT, c, acc[i][j][e], acc[i][j][e + 1], gelu_table);
+                    const int mr = geglu2_row(c, m + e, m + e + 1);
+                    if (mr < m_rows && hn < n_out) static_cast<float*>(y)[(long)mr * n_out + hn] = h;
+                }
+                continue;
+            }
+            const int m = mt * kBM + wm * kWM + 16 * i + 4 * kq;
+            {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (OUT == kOutF32) {  // fp32 output, or this split's partial plane
+                        const int n = rb * 16 + col;
+                        if (m + e < m_rows && n < n_rows)
+                            static_cast<float*>(y)[(long)blockIdx.y * split_stride + (long)(m + e) * n_rows + n] =
+                                acc[i][j][e];
+                    } else {
+                        store_out(y, OUT, m + e, m_rows, rb, col, n_rows, n_out, acc[i][j][e]);
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (OUT == kOutGegluBf16) {
+        const int c = slane & 15;
+#pragma unroll
+        for (int i = 0; i < kMT; ++i) {
+#pragma unroll
+            for (int j = 0; j < kNT; ++j) {
+                const int m = mt * kBM + wm * kWM + 16 * i + 4 * (slane >> 4);
+                const int hn = geglu2_col(c, rbw + wn * kNT + j);
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    const int mr = geglu2_row(c, m + e, m + e + 1);
+                    if (mr < m_rows && hn < n_out) static_cast<uint16_t*>(y)[(long)mr * n_out + hn] = f32_to_bf16(acc[i][j][e]);
                 }
             }
         }
@@ -433,6 +475,12 @@ __global__ void split_reduce_kernel(const float* __restrict__ part, void* __rest
                 static_cast<uint16_t*>(y)[j] = f32_to_bf16(v);
         }
     }
+}
+
+// gelu_bf16 of every bf16 bit pattern (the table the bf16 GeGLU epilogue reads)
+__global__ void gelu_table_kernel(uint16_t* __restrict__ table) {
+    const int b = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (b < 65536) table[b] = f32_to_bf16(gelu_bf16(__uint_as_float((uint32_t)b << 16)));
 }
 
 // h = GeGLU of the summed gate|up partial planes, in split order (deterministic).  One
@@ -493,8 +541,14 @@ size_t gemm_workspace_bytes(int m, const Layout& l) {
     return p.xaug_bytes + p.part_bytes;
 }
 
+hipError_t launch_gelu_table(uint16_t* table, hipStream_t stream) {
+    hipLaunchKernelGGL(gelu_table_kernel, dim3(256), dim3(256), 0, stream, table);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, int out_mode,
-                       int n_out, const Layout& l, void* workspace, hipStream_t stream) {
+                       int n_out, const Layout& l, void* workspace, const uint16_t* gelu_table,
+                       hipStream_t stream) {
     const GemmPlan plan = plan_gemm(m, l);
     const int octets = (l.g + 7) / 8;
     const int mtiles = (m + kBM - 1) / kBM;
@@ -517,7 +571,7 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     const long elems = (long)m * l.n;
     if (plan.splits > 1) {
         hipLaunchKernelGGL((gemm_kernel<kOutF32>), grid, block, 0, stream, tiles, sb, x, xaug, (void*)part, m, l.n, l.k,
-                           l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, elems, n_out);
+                           l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, elems, n_out, gelu_table);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const int rblock = 256;
@@ -542,7 +596,7 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     }
 #define Q4_GEMM_LAUNCH(MODE)                                                                                     \
     hipLaunchKernelGGL((gemm_kernel<MODE>), grid, block, 0, stream, tiles, sb, x, xaug, y, m, l.n, l.k, l.g, l.gp, \
-                       mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L, n_out)
+                       mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L, n_out, gelu_table)
     switch (out_mode) {
         case kOutF32: Q4_GEMM_LAUNCH(kOutF32); break;
         case kOutGegluBf16: Q4_GEMM_LAUNCH(kOutGegluBf16); break;

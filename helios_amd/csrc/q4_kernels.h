@@ -64,8 +64,14 @@ size_t gemm_workspace_bytes(int m, const Layout& l);
 
 // Compute units of the current device (cached per device).
 int device_cus();
+// gelu_table: 65536 bf16 values from launch_gelu_table, read by the bf16 GeGLU
+// epilogue (out_mode 2); may be null for the other modes.
 hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, int out_mode,
-                       int n_out, const Layout& l, void* workspace, hipStream_t stream);
+                       int n_out, const Layout& l, void* workspace, const uint16_t* gelu_table,
+                       hipStream_t stream);
+
+// Fills table[65536] with gelu of every bf16 bit pattern, in the bf16 op sequence.
+hipError_t launch_gelu_table(uint16_t* table, hipStream_t stream);
 
 // Rows at or above which forward uses the GEMM path.
 constexpr int kGemmMinRows = 32;

@@ -68,6 +68,31 @@ hipError_t scratch_pool(int device, hipMemPool_t* out) {
     return hipSuccess;
 }
 
+// The bf16 GeGLU epilogue's table of gelu over all bf16 patterns (128 KiB), built
+// once per device when its first gate|up pair is created (create synchronizes, so
+// every later forward, on any stream, sees it complete).  Kept until the process ends.
+std::mutex g_table_mu;
+uint16_t* g_gelu_tables[64] = {};
+
+hipError_t gelu_table(int device, const uint16_t** out) {
+    if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_table_mu);
+    if (g_gelu_tables[device] == nullptr) {
+        uint16_t* t = nullptr;
+        hipError_t e = hipMalloc(&t, 65536 * sizeof(uint16_t));
+        if (e != hipSuccess) return e;
+        e = q4::launch_gelu_table(t, nullptr);
+        if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+        if (e != hipSuccess) {
+            (void)hipFree(t);
+            return e;
+        }
+        g_gelu_tables[device] = t;
+    }
+    *out = g_gelu_tables[device];
+    return hipSuccess;
+}
+
 // Restores the caller's current device on scope exit.
 struct DeviceGuard {
     int saved = -1;
@@ -93,6 +118,7 @@ struct Gemma4QLinear {
     Gemma4QLinearDesc desc{};  // out_features is F for a gate|up pair
     q4::Layout layout;
     int pair_rows = 0;  // F for a gate|up pair (tiled as q4::pair_layout), else 0
+    const uint16_t* gelu_table = nullptr;  // the device's gelu table (pairs only)
     int device = 0;
     uint4* tiles = nullptr;
     uint2* sb = nullptr;
@@ -151,6 +177,13 @@ Gemma4Status build_handle(const Gemma4QLinearDesc* desc, const Triple& main, con
     if (e != hipSuccess) {
         delete h;
         return hip_fail("hipGetDevice", e);
+    }
+    if (up != nullptr) {
+        e = gelu_table(h->device, &h->gelu_table);
+        if (e != hipSuccess) {
+            delete h;
+            return hip_fail("gemma4_qgeglu: gelu table", e);
+        }
     }
     e = hipMalloc(&h->tiles, h->layout.tile_bytes());
     if (e == hipSuccess) e = hipMalloc(&h->sb, h->layout.sb_bytes());
@@ -263,7 +296,8 @@ Gemma4Status run_forward(const Gemma4QLinear* linear, void* stream, const uint16
     e = hipMallocFromPoolAsync(&ws, ws_bytes, pool, st);
     if (e != hipSuccess)
         return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
-    e = q4::launch_gemm(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, mode, n_out, linear->layout, ws, st);
+    e = q4::launch_gemm(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, mode, n_out, linear->layout, ws,
+                        linear->gelu_table, st);
     const hipError_t ef = hipFreeAsync(ws, st);
     if (e != hipSuccess) return hip_fail((name + ": gemm launch").c_str(), e);
     if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);

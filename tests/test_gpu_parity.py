@@ -201,12 +201,14 @@ def test_forward_rejects_misaligned_x(gpu_lib):
 
 
 @pytest.mark.parametrize("m", [1, 3, 4])
-def test_forward_many_row_blocks_per_workgroup(gpu_lib, m):
-    """Tall, narrow weights: far more 16-row blocks than resident workgroups, so the
-    persistent decode path walks many row blocks per workgroup."""
+@pytest.mark.parametrize("n,k", [(131072 + 48, 128), (32768 + 40, 256)])
+def test_forward_many_row_blocks_per_workgroup(gpu_lib, m, n, k):
+    """Tall, narrow weights: more 16-row blocks than resident waves, so the persistent
+    decode kernels walk several row blocks per workgroup (8195 blocks: the streaming
+    kernel) or per wave (2051 blocks at M = 1: the row-block-per-wave kernel), with a
+    ragged last block."""
     import torch
 
-    n, k = 131072 + 48, 128
     wq, s, b = random_triple(n, k, seed=41 + m)
     x = A.make_activations(m, k, seed=42 + m, outliers=True)
     lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))

@@ -124,10 +124,22 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_
 // 8j..8j+7 in columns 0..7 and the same up rows in columns 8..15, so each output
 // h[m, 8j + c] = geglu(gate, up) combines columns c and c + 8 of one block.
 enum OutMode : int {
-    kOutBf16 = 0,       // y bf16 [M, N]
-    kOutF32 = 1,        // y fp32 [M, N] (also the split-K partial planes)
-    kOutGegluBf16 = 2,  // h bf16 [M, F], the bf16 model dtype's GeGLU
-    kOutGegluF32 = 3,   // h fp32 [M, F], the float32 override's GeGLU
+    kOutBf16 = 0,        // y bf16 [M, N]
+    kOutF32 = 1,         // y fp32 [M, N] (also the split-K partial planes)
+    kOutGegluBf16 = 2,   // h bf16 [M, F], the bf16 model dtype's GeGLU
+    kOutGegluF32 = 3,    // h fp32 [M, F], the float32 override's GeGLU
+    kOutGreedyBf16 = 4,  // lm_head: softcap in bf16 ops, optional logits, best (value, index) per block
+    kOutGreedyF32 = 5,   // the same in fp32
+};
+
+// Where and how a decode kernel writes its outputs.
+struct OutParams {
+    void* y;                   // y [M, N], h [M, F], or the greedy modes' logits [M, N] (may be null)
+    unsigned long long* part;  // greedy modes: best key of each (row, 16-row block), [M][nb]
+    int mode;
+    int n_out;                 // GeGLU modes: F
+    int nb;                    // greedy modes: row blocks (the stride of part)
+    float cap;                 // greedy modes: the softcap (0: none)
 };
 
 __device__ __forceinline__ float round_bf16(float v) { return (float)(__bf16)v; }
@@ -180,11 +192,68 @@ __device__ __forceinline__ float row_swap8(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
 }
 
+// The lm_head's final-logit softcap, tanh(logits / cap) * cap (native_model.cc:1794),
+// op by op: bf16 rounding after the qmm output and after every op in the bf16 model
+// dtype (cap is then bf16), all fp32 under the float32 override.  Division is IEEE
+// (correctly rounded).  cap = 0 leaves the (rounded) logits as they are.
+__device__ __forceinline__ float softcap_bf16(float v, float cap) {
+#pragma clang fp contract(off)
+    const float l = round_bf16(v);
+    if (cap == 0.0f) return l;
+    const float c = round_bf16(cap);
+    return round_bf16(round_bf16(tanhf(round_bf16(l / c))) * c);
+}
+__device__ __forceinline__ float softcap_f32(float v, float cap) {
+#pragma clang fp contract(off)
+    return cap == 0.0f ? v : tanhf(v / cap) * cap;
+}
+
+// Greedy key of (value, index): unsigned order = value order, and on equal values the
+// lower index is larger (argmax returns the first maximum).  0 is below every key.
+__device__ __forceinline__ unsigned long long greedy_key(float v, int n) {
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)o << 32) | (0xFFFFFFFFu - (uint32_t)n);
+}
+__device__ __forceinline__ float greedy_value(unsigned long long key) {
+    const uint32_t o = (uint32_t)(key >> 32);
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+__device__ __forceinline__ int greedy_index(unsigned long long key) {
+    return (int)(0xFFFFFFFFu - (uint32_t)key);
+}
+
 // Writes accumulator v of output row m, column 16*rb + col.  All lanes of the wave
-// call it together (the GeGLU modes read the partner column from lane col ^ 8);
-// n_rows bounds a plain projection's N, n_out a pair's F.
-__device__ __forceinline__ void store_out(void* y, int mode, int m, int m_rows, int rb, int col, int n_rows,
-                                          int n_out, float v) {
+// call it together (the GeGLU modes read the partner column from lane col ^ 8, the
+// greedy modes reduce over the block's 16 columns); n_rows bounds the projection's N.
+// Kernels never launched in the greedy modes compile that branch out (kGreedy).
+template <bool kGreedy = true>
+__device__ __forceinline__ void store_out(const OutParams& op, int m, int m_rows, int rb, int col, int n_rows,
+                                          float v) {
+    void* y = op.y;
+    const int mode = op.mode;
+    const int n_out = op.n_out;
+    if (kGreedy && mode >= kOutGreedyBf16) {
+        const int n = rb * 16 + col;
+        const bool bf = mode == kOutGreedyBf16;
+        const float c = bf ? softcap_bf16(v, op.cap) : softcap_f32(v, op.cap);
+        const bool valid = m < m_rows && n < n_rows;
+        if (valid && y != nullptr) {
+            const long o = (long)m * n_rows + n;
+            if (bf)
+                static_cast<uint16_t*>(y)[o] = f32_to_bf16(c);
+            else
+                static_cast<float*>(y)[o] = c;
+        }
+        unsigned long long key = n < n_rows ? greedy_key(c, n) : 0ull;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) {  // max over the 16 columns of this row
+            const unsigned long long o = __shfl_xor(key, d);
+            key = o > key ? o : key;
+        }
+        if (col == 0 && m < m_rows) op.part[(long)m * op.nb + rb] = key;
+        return;
+    }
     if (mode < kOutGegluBf16) {
         const int n = rb * 16 + col;
         if (m < m_rows && n < n_rows) {

@@ -34,7 +34,7 @@ namespace {
 template <int MT, int GPW, bool XLDS>
 __global__ __launch_bounds__(1024) void decode_kernel(
     const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x,
-    void* __restrict__ y, int m_rows, int n_rows, int k, int gpairs, int waves, int out_mode, int n_out) {
+    OutParams op, int m_rows, int n_rows, int k, int gpairs, int waves) {
     constexpr int R = MT < 4 ? MT : 4;
     extern __shared__ uint4 xs_lds[];  // XLDS: x[M][K] as bf16, 16 B per entry
     const int rb = blockIdx.x;
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(
         for (int w = 0; w < waves; ++w) v += red[w][t];
         const int r = t >> 6;
         const int l = t & 63;
-        store_out(y, out_mode, 4 * (l >> 4) + r, m_rows, rb, l & 15, n_rows, n_out, v);
+        store_out(op, 4 * (l >> 4) + r, m_rows, rb, l & 15, n_rows, v);
     }
 }
 
@@ -179,7 +179,7 @@ __device__ __forceinline__ uint32_t scale_word(uint2 sv, int pair, int gi, int c
 template <int MT, int GPW>
 __global__ __launch_bounds__(512) void decode_stream_kernel(
     const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x,
-    void* __restrict__ y, int m_rows, int n_rows, int k, int gpairs, int nblocks, int waves, int out_mode, int n_out) {
+    OutParams op, int m_rows, int n_rows, int k, int gpairs, int nblocks, int waves) {
     constexpr int R = MT < 4 ? MT : 4;
     constexpr int kPad = GPW * 128;  // zero columns after each x row
     extern __shared__ uint4 lds[];
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
                 for (int w = 0; w < waves; ++w) v += red[parity][w][t];
                 const int r = t >> 6;
                 const int l = t & 63;
-                store_out(y, out_mode, 4 * (l >> 4) + r, m_rows, rb, l & 15, n_rows, n_out, v);
+                store_out(op, 4 * (l >> 4) + r, m_rows, rb, l & 15, n_rows, v);
             }
             acc = zero;
             parity ^= 1;
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
 template <int MT, int GPW, int NBUF>
 __global__ __launch_bounds__(256) void decode_rows_kernel(
     const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x,
-    void* __restrict__ y, int m_rows, int n_rows, int k, int gpairs, int nblocks, int out_mode, int n_out) {
+    OutParams op, int m_rows, int n_rows, int k, int gpairs, int nblocks) {
     static_assert(GPW == 4, "one 8-byte load per lane covers a chunk's scale words");
     constexpr int R = MT < 4 ? MT : 4;
     constexpr int kPad = GPW * 128;  // zero columns after each x row
@@ -487,7 +487,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(
             const int rb = gwave + (c / passes) * nwaves;
             // lane holds rows 4*kq + r of column col
 #pragma unroll
-            for (int r = 0; r < R; ++r) store_out(y, out_mode, 4 * kq + r, m_rows, rb, col, n_rows, n_out, acc[r]);
+            for (int r = 0; r < R; ++r) store_out<false>(op, 4 * kq + r, m_rows, rb, col, n_rows, acc[r]);
             acc = zero;
         }
     };
@@ -532,20 +532,20 @@ constexpr int kRowsPerCu = 2;
 
 
 template <int MT>
-hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
-                     int out_mode, int n_out, const Layout& l, hipStream_t stream) {
+hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, const OutParams& op, int m,
+                     const Layout& l, hipStream_t stream) {
     constexpr int GPW = 4;
     constexpr int R = MT < 4 ? MT : 4;
     const size_t static_lds = 2 * 8 * R * 64 * sizeof(float);
     const size_t lds_bytes = (size_t)m * (l.k + GPW * 128) * 2 + (size_t)(l.gp + GPW) * 2 * 16 * 4;
     if constexpr (MT == 1) {
-        if (l.nb >= kRowsMinBlocks && l.nb <= kRowsMaxBlocks && lds_bytes <= kLdsPerCu) {
+        if (l.nb >= kRowsMinBlocks && l.nb <= kRowsMaxBlocks && lds_bytes <= kLdsPerCu && op.mode < kOutGreedyBf16) {
             // many row blocks: one wave per block, no cross-wave reduction
             int grid = (l.nb + kRowsWaves - 1) / kRowsWaves;
             const int cap = device_cus() * kRowsPerCu;
             if (grid > cap) grid = cap;
             hipLaunchKernelGGL((decode_rows_kernel<MT, GPW, 3>), dim3(grid), dim3(64 * kRowsWaves), lds_bytes, stream,
-                               tiles, sb, x, y, m, l.n, l.k, l.gp, l.nb, out_mode, n_out);
+                               tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb);
             return hipGetLastError();
         }
     }
@@ -561,15 +561,15 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, voi
         const int per_wg = (l.nb + capacity - 1) / capacity;
         const int grid = (l.nb + per_wg - 1) / per_wg;
         hipLaunchKernelGGL((decode_stream_kernel<MT, GPW>), dim3(grid), dim3(64 * waves), lds_bytes, stream, tiles,
-                           sb, x, y, m, l.n, l.k, l.gp, l.nb, waves, out_mode, n_out);
+                           sb, x, op, m, l.n, l.k, l.gp, l.nb, waves);
         return hipGetLastError();
     }
     const Split sp = choose_split(l.gp, MT);
     const dim3 grid(l.nb), block(64 * sp.waves);
     if (sp.gpw == 6)
-        hipLaunchKernelGGL((decode_kernel<MT, 6, false>), grid, block, 0, stream, tiles, sb, x, y, m, l.n, l.k, l.gp, sp.waves, out_mode, n_out);
+        hipLaunchKernelGGL((decode_kernel<MT, 6, false>), grid, block, 0, stream, tiles, sb, x, op, m, l.n, l.k, l.gp, sp.waves);
     else
-        hipLaunchKernelGGL((decode_kernel<MT, 4, false>), grid, block, 0, stream, tiles, sb, x, y, m, l.n, l.k, l.gp, sp.waves, out_mode, n_out);
+        hipLaunchKernelGGL((decode_kernel<MT, 4, false>), grid, block, 0, stream, tiles, sb, x, op, m, l.n, l.k, l.gp, sp.waves);
     return hipGetLastError();
 }
 
@@ -587,26 +587,60 @@ int device_cus() {
     return cus[dev];
 }
 
-hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
-                         int out_mode, int n_out, const Layout& l, hipStream_t stream) {
-    const size_t ysz = (out_mode == kOutF32 || out_mode == kOutGegluF32) ? 4 : 2;
-    const size_t ycols = out_mode >= kOutGegluBf16 ? (size_t)n_out : (size_t)l.n;
+hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, const OutParams& op, int m,
+                         const Layout& l, hipStream_t stream) {
+    const bool f32 = op.mode == kOutF32 || op.mode == kOutGegluF32 || op.mode == kOutGreedyF32;
+    const size_t ysz = f32 ? 4 : 2;
+    const size_t ycols = (op.mode == kOutGegluBf16 || op.mode == kOutGegluF32) ? (size_t)op.n_out : (size_t)l.n;
     for (int m0 = 0; m0 < m; m0 += 16) {
         const int mc = (m - m0) < 16 ? (m - m0) : 16;
         const uint16_t* xs = x + (size_t)m0 * l.k;
-        void* ys = static_cast<char*>(y) + (size_t)m0 * ycols * ysz;
+        OutParams slab = op;
+        if (op.y != nullptr) slab.y = static_cast<char*>(op.y) + (size_t)m0 * ycols * ysz;
+        if (op.part != nullptr) slab.part = op.part + (size_t)m0 * op.nb;
         hipError_t e;
         if (mc == 1)
-            e = launch_mt<1>(tiles, sb, xs, ys, mc, out_mode, n_out, l, stream);
+            e = launch_mt<1>(tiles, sb, xs, slab, mc, l, stream);
         else if (mc == 2)
-            e = launch_mt<2>(tiles, sb, xs, ys, mc, out_mode, n_out, l, stream);
+            e = launch_mt<2>(tiles, sb, xs, slab, mc, l, stream);
         else if (mc <= 4)
-            e = launch_mt<4>(tiles, sb, xs, ys, mc, out_mode, n_out, l, stream);
+            e = launch_mt<4>(tiles, sb, xs, slab, mc, l, stream);
         else
-            e = launch_mt<16>(tiles, sb, xs, ys, mc, out_mode, n_out, l, stream);
+            e = launch_mt<16>(tiles, sb, xs, slab, mc, l, stream);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+// argmax over the blocks' best keys: one workgroup per row (deterministic: the max of
+// keys does not depend on order)
+__global__ __launch_bounds__(256) void greedy_reduce_kernel(const unsigned long long* __restrict__ part, int nb,
+                                                            int32_t* __restrict__ token, float* __restrict__ value) {
+    const int m = (int)blockIdx.x;
+    unsigned long long best = 0;
+    for (int i = (int)threadIdx.x; i < nb; i += (int)blockDim.x) {
+        const unsigned long long k = part[(long)m * nb + i];
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const unsigned long long o = __shfl_xor(best, d);
+        best = o > best ? o : best;
+    }
+    __shared__ unsigned long long wbest[4];
+    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) best = wbest[w] > best ? wbest[w] : best;
+        token[m] = greedy_index(best);
+        if (value != nullptr) value[m] = greedy_value(best);
+    }
+}
+
+hipError_t launch_greedy_reduce(const unsigned long long* part, int nb, int m, int32_t* token, float* value,
+                                hipStream_t stream) {
+    hipLaunchKernelGGL(greedy_reduce_kernel, dim3(m), dim3(256), 0, stream, part, nb, token, value);
+    return hipGetLastError();
 }
 
 }  // namespace q4

@@ -404,7 +404,8 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
                             static_cast<float*>(y)[(long)blockIdx.y * split_stride + (long)(m + e) * n_rows + n] =
                                 acc[i][j][e];
                     } else {
-                        store_out(y, OUT, m + e, m_rows, rb, col, n_rows, n_out, acc[i][j][e]);
+                        const OutParams op{y, nullptr, OUT, n_out, 0, 0.0f};
+                        store_out<false>(op, m + e, m_rows, rb, col, n_rows, acc[i][j][e]);
                     }
                 }
             }

@@ -41,12 +41,19 @@ hipError_t launch_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b
 hipError_t launch_dequantize(const uint4* tiles, const uint2* sb, float* out, const Layout& l, int pair_rows,
                              hipStream_t stream);
 
-// Output modes (q4_common.h OutMode): 0 bf16 y, 1 fp32 y, 2 bf16 GeGLU h, 3 fp32 GeGLU h.
-// n_out is F for the GeGLU modes (h is [M, F]) and unused otherwise.
+// Output modes (q4_common.h OutMode): 0 bf16 y, 1 fp32 y, 2 bf16 GeGLU h, 3 fp32 GeGLU h,
+// 4 / 5 the greedy lm_head (softcap, optional logits, per-block best keys).  n_out is
+// F for the GeGLU modes (h is [M, F]) and unused otherwise.
+struct OutParams;
 
 // Decode path, M <= 16 rows per launch (the launcher walks larger M in 16-row slabs).
-hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m,
-                         int out_mode, int n_out, const Layout& l, hipStream_t stream);
+hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, const OutParams& op, int m,
+                         const Layout& l, hipStream_t stream);
+
+// token[m] (and value[m] when not null) = argmax over the keys part[m][0..nb) left by
+// the greedy modes, for m < rows.
+hipError_t launch_greedy_reduce(const unsigned long long* part, int nb, int rows, int32_t* token, float* value,
+                                hipStream_t stream);
 
 // Prefill path: fp32-exact factored GEMM on the matrix cores.  `workspace` holds the
 // group sums of x and, when K is split over workgroups, the fp32 partial sums

@@ -19,6 +19,7 @@
 namespace {
 
 constexpr uint64_t kQLinearMagic = 0x47454d3451344c4eULL;  // "GEM4Q4LN"
+constexpr int kGreedyMaxRows = 16;  // rows per greedy-head call (decode and verify blocks)
 thread_local char g_last_error[512] = "";
 
 Gemma4Status fail(Gemma4Status status, const std::string& message) {
@@ -282,7 +283,8 @@ Gemma4Status run_forward(const Gemma4QLinear* linear, void* stream, const uint16
     const int mode = geglu ? (f32 ? q4::kOutGegluF32 : q4::kOutGegluBf16) : (f32 ? q4::kOutF32 : q4::kOutBf16);
     const int n_out = linear->pair_rows;
     if ((int)rows < q4::kGemmMinRows) {
-        e = q4::launch_decode(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, mode, n_out, linear->layout, st);
+        const q4::OutParams op{y_dev, nullptr, mode, n_out, 0, 0.0f};
+        e = q4::launch_decode(linear->tiles, linear->sb, x_dev, op, (int)rows, linear->layout, st);
         if (e != hipSuccess) return hip_fail((name + ": decode launch").c_str(), e);
         return ok();
     }
@@ -438,6 +440,58 @@ Gemma4Status gemma4_qgeglu_forward(const Gemma4QLinear* pair, void* stream, cons
         return run_forward(pair, stream, x_dev, rows, h_dev, h_dtype, true, "gemma4_qgeglu_forward");
     } catch (...) {
         return fail(GEMMA4_ERR_RUNTIME, "gemma4_qgeglu_forward: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qlinear_forward_greedy(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
+                                           uint32_t rows, float softcap, void* logits_dev, Gemma4QmmDtype dtype,
+                                           int32_t* token_dev, float* value_dev) {
+    try {
+        const std::string name("gemma4_qlinear_forward_greedy");
+        if (!valid_handle(linear)) return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " received an invalid handle");
+        if (linear->pair_rows != 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": the handle is a gate|up pair, not a projection");
+        if (dtype != GEMMA4_QMM_BF16 && dtype != GEMMA4_QMM_F32)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": dtype must be BF16 or F32");
+        if (!(softcap >= 0.0f) || softcap > 3.0e38f)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": softcap must be finite and >= 0 (0: none)");
+        if (rows == 0) return ok();
+        if (rows > (uint32_t)kGreedyMaxRows)
+            return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
+                        name + ": at most " + std::to_string(kGreedyMaxRows) +
+                            " rows per call (the verify block cap, gemma4_mlx.h:77-79)");
+        if (x_dev == nullptr || token_dev == nullptr)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " requires non-null x and token outputs");
+        if ((reinterpret_cast<uintptr_t>(x_dev) & 15u) != 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": x must be 16-byte aligned");
+        const uintptr_t lalign = dtype == GEMMA4_QMM_F32 ? 3u : 1u;
+        if ((reinterpret_cast<uintptr_t>(logits_dev) & lalign) != 0 || (reinterpret_cast<uintptr_t>(token_dev) & 3u) != 0 ||
+            (reinterpret_cast<uintptr_t>(value_dev) & 3u) != 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": an output is misaligned for its type");
+        DeviceGuard guard;
+        hipError_t e = guard.enter(linear->device);
+        if (e != hipSuccess) return hip_fail((name + ": hipSetDevice").c_str(), e);
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        hipMemPool_t pool = nullptr;
+        e = scratch_pool(linear->device, &pool);
+        if (e != hipSuccess) return hip_fail((name + ": scratch pool").c_str(), e);
+        const int nb = linear->layout.nb;
+        void* part = nullptr;
+        e = hipMallocFromPoolAsync(&part, (size_t)rows * nb * sizeof(unsigned long long), pool, st);
+        if (e != hipSuccess)
+            return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
+        const int mode = dtype == GEMMA4_QMM_F32 ? q4::kOutGreedyF32 : q4::kOutGreedyBf16;
+        const q4::OutParams op{logits_dev, static_cast<unsigned long long*>(part), mode, 0, nb, softcap};
+        e = q4::launch_decode(linear->tiles, linear->sb, x_dev, op, (int)rows, linear->layout, st);
+        if (e == hipSuccess)
+            e = q4::launch_greedy_reduce(static_cast<const unsigned long long*>(part), nb, (int)rows, token_dev,
+                                         value_dev, st);
+        const hipError_t ef = hipFreeAsync(part, st);
+        if (e != hipSuccess) return hip_fail((name + ": launch").c_str(), e);
+        if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);
+        return ok();
+    } catch (...) {
+        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward_greedy: unexpected native exception");
     }
 }
 

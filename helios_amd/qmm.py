@@ -101,6 +101,7 @@ def load_library(path: str | None = None):
         "gemma4_qgeglu_create": [ctypes.POINTER(_Desc), vp, vp, vp, vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qgeglu_create_device": [ctypes.POINTER(_Desc), vp, vp, vp, vp, vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qgeglu_forward": [vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int],
+        "gemma4_qlinear_forward_greedy": [vp, vp, vp, ctypes.c_uint32, ctypes.c_float, vp, ctypes.c_int, vp, vp],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -268,6 +269,31 @@ class QuantizedLinear(_Handle):
         check(self._lib.gemma4_qlinear_forward(self._handle, ctypes.c_void_p(stream_ptr), ctypes.c_void_p(x_ptr),
                                                rows, ctypes.c_void_p(y_ptr), DTYPE_F32 if f32 else DTYPE_BF16),
               self._lib)
+
+    def forward_greedy(self, x, softcap: float = 30.0, out_dtype=None, return_logits: bool = False, stream=None):
+        """The greedy lm_head: softcapped logits of x . W^T and their argmax per row.
+
+        Returns (token int32 [rows], value float32 [rows], logits [rows, N] or None):
+        the first maximum of each row's tanh(logits / softcap) * softcap and that
+        maximum (native_model.cc:1782-1795 and the argmax at :3734).  x is bf16
+        [rows, K] with rows <= 16; softcap 0 skips the softcap."""
+        import torch
+
+        out_dtype = out_dtype or torch.bfloat16
+        if out_dtype not in (torch.bfloat16, torch.float32):
+            raise Gemma4Error(Status.INVALID_ARGUMENT, "out_dtype must be bfloat16 or float32")
+        if x.dtype != torch.bfloat16 or x.shape[-1] != self.in_features:
+            raise Gemma4Error(Status.INVALID_ARGUMENT, f"x must be bfloat16 [..., {self.in_features}]")
+        x2 = x.reshape(-1, self.in_features).contiguous()
+        rows = x2.shape[0]
+        token = torch.empty((rows,), dtype=torch.int32, device=x.device)
+        value = torch.empty((rows,), dtype=torch.float32, device=x.device)
+        logits = torch.empty((rows, self.out_features), dtype=out_dtype, device=x.device) if return_logits else None
+        code = DTYPE_F32 if out_dtype == torch.float32 else DTYPE_BF16
+        check(self._lib.gemma4_qlinear_forward_greedy(
+            self._handle, _stream_ptr(stream), _dev_ptr(x2), rows, float(softcap),
+            _dev_ptr(logits) if logits is not None else None, code, _dev_ptr(token), _dev_ptr(value)), self._lib)
+        return token, value, logits
 
     def dequantize(self, stream=None):
         import torch

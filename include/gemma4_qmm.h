@@ -140,6 +140,22 @@ Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, c
  * output is [2, F, K]: the gate rows, then the up rows. */
 Gemma4Status gemma4_qlinear_dequantize(const Gemma4QLinear* linear, void* stream, float* w_dev);
 
+/* Greedy lm_head: the product, the final-logit softcap and argmax in one call —
+ * replaces target_logits_for_hidden (native_model.cc:1782-1795: quantized_matmul, then
+ * tanh(logits / 30) * 30) followed by argmax over the vocabulary (native_model.cc:3734,
+ * :3825, :3934; per row at :4114, :4242) and the max logit (greedy_logit_for_vector_logits).
+ *   token_dev [rows] int32   index of the first maximum of row m's softcapped logits
+ *   value_dev [rows] float   that maximum (optional, NULL to skip)
+ *   logits_dev [rows, N]     the softcapped logits in dtype (optional, NULL to skip)
+ * softcap 0 skips the softcap.  With dtype BF16 the logits and every softcap op are
+ * rounded to bf16 as the reference's bf16 array ops are; F32 keeps fp32.  rows <= 16
+ * (a decode step or a verify block, gemma4_mlx.h:77-79).  Deterministic: ties go to
+ * the lowest index whatever the execution order.  Uses a stream-ordered scratch of
+ * rows * ceil(N/16) * 8 bytes. */
+Gemma4Status gemma4_qlinear_forward_greedy(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
+                                           uint32_t rows, float softcap, void* logits_dev, Gemma4QmmDtype dtype,
+                                           int32_t* token_dev, float* value_dev);
+
 /* ---- Fused gate|up projection with the GeGLU epilogue ----
  * Replaces the reference's MLP front half, two quantized_linear calls on the same
  * input followed by geglu (native_model.cc:934-949 prefill, :1318-1321 decode, and

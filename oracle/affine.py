@@ -228,3 +228,28 @@ def gelu_tanh_times(gate_bits, up_bits) -> np.ndarray:
     """bf16 GeGLU of bf16 gate/up bit patterns (``geglu_ops`` in the bf16 model
     dtype), as bf16 bits: the down_proj input of the prefill chain."""
     return f32_to_bf16_bits(geglu_ops(bf16_bits_to_f32(gate_bits), bf16_bits_to_f32(up_bits), bf16=True))
+
+
+# lm_head final-logit softcap (native_model.cc:1794): tanh(logits / 30) * 30
+LOGIT_SOFTCAP = 30.0
+
+
+def softcap_ops(logits, cap: float = LOGIT_SOFTCAP, bf16: bool = True) -> np.ndarray:
+    """The reference's softcap op by op: model_dtype(tanh(logits / cap) * cap).  With
+    ``bf16`` the logits (the qmm output in the model dtype), the constant and each
+    op's result are bf16-rounded; otherwise all are float32.  ``cap == 0`` returns the
+    (rounded) logits unchanged.  Returns float32."""
+    r = round_to_bf16 if bf16 else (lambda v: np.asarray(v, dtype=np.float32))
+    l = r(np.asarray(logits, dtype=np.float32))
+    if cap == 0:
+        return l
+    c = r(np.float32(cap))
+    return r(r(np.tanh(r(l / c))) * c)
+
+
+def greedy(values) -> tuple:
+    """argmax along the last axis (the first maximum, as mlx::core::argmax and
+    np.argmax return it) and the maximum itself."""
+    v = np.asarray(values, dtype=np.float32)
+    idx = np.argmax(v, axis=-1)
+    return idx.astype(np.int32), np.take_along_axis(v, idx[..., None], axis=-1)[..., 0]

@@ -90,3 +90,6 @@ def test_decode_register_budgets():
         if "decode_stream_kernel" in name:
             # two 8-wave workgroups per CU (the launcher's occupancy assumption)
             assert vgprs <= 128, f"{name}: {vgprs} VGPRs"
+        if "decode_rows_kernel" in name:
+            # two waves per SIMD (two 4-wave workgroups per CU)
+            assert vgprs <= 256, f"{name}: {vgprs} VGPRs"

@@ -41,6 +41,11 @@ hipError_t launch_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b
 hipError_t launch_dequantize(const uint4* tiles, const uint2* sb, float* out, const Layout& l, int pair_rows,
                              hipStream_t stream);
 
+// out[t, :] = dequantized row ids[t] of a projection (fp32, or bf16 rounded once), t <
+// count; ids outside [0, N) give zero rows.  out is 16-byte aligned, [count, K].
+hipError_t launch_embed(const uint4* tiles, const uint2* sb, const int32_t* ids, int count, void* out, bool out_f32,
+                        const Layout& l, hipStream_t stream);
+
 // Output modes (q4_common.h OutMode): 0 bf16 y, 1 fp32 y, 2 bf16 GeGLU h, 3 fp32 GeGLU h,
 // 4 / 5 the greedy lm_head (softcap, optional logits, per-block best keys).  n_out is
 // F for the GeGLU modes (h is [M, F]) and unused otherwise.

@@ -130,7 +130,66 @@ __global__ void dequantize_kernel(const uint4* __restrict__ tiles, const uint2* 
     }
 }
 
+// Row gather of the dequantized weight: out[t, :] = W[ids[t], :] (fp32, or bf16 rounded
+// once).  One thread per (token, group pair, k-quarter): the four words of lane
+// (ids[t] % 16, kq) in tile (ids[t] / 16, gp), 32 values.  ids outside [0, n_rows)
+// give zero rows.
+__global__ void embed_kernel(const uint4* __restrict__ tiles, const uint2* __restrict__ sb,
+                             const int32_t* __restrict__ ids, void* __restrict__ out, int out_f32, int n_rows, int k,
+                             int groups, int gpairs, long total) {
+    const long tid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tid >= total) return;
+    const int kq = (int)(tid & 3);
+    const long r = tid >> 2;
+    const int gp = (int)(r % gpairs);
+    const long t = r / gpairs;
+    const int id = ids[t];
+    const bool valid = id >= 0 && id < n_rows;
+    const long rb = valid ? id >> 4 : 0;
+    const int col = valid ? id & 15 : 0;
+    const long tile = rb * gpairs + gp;
+    const uint4 wv = valid ? tiles[tile * 64 + col + 16 * kq] : make_uint4(0, 0, 0, 0);
+    const uint2 sv = valid ? sb[tile * 16 + col] : make_uint2(0, 0);
+    const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        const int g = 2 * gp + gi;
+        if (g >= groups) continue;
+        const uint32_t sbv = gi ? sv.y : sv.x;
+        const float sc = bf16_lo(sbv);
+        const float bi = bf16_hi(sbv);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(sc, (float)word_nibble(words[2 * gi + h], i), bi);
+            const long o = t * k + 64 * g + 32 * h + 8 * kq;
+            if (out_f32) {
+                float4* dst = reinterpret_cast<float4*>(static_cast<float*>(out) + o);
+                dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+                dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+            } else {
+                uint32_t p[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    p[j] = (uint32_t)f32_to_bf16(v[2 * j]) | ((uint32_t)f32_to_bf16(v[2 * j + 1]) << 16);
+                *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + o) = make_uint4(p[0], p[1], p[2], p[3]);
+            }
+        }
+    }
+}
+
 }  // namespace
+
+hipError_t launch_embed(const uint4* tiles, const uint2* sb, const int32_t* ids, int count, void* out, bool out_f32,
+                        const Layout& l, hipStream_t stream) {
+    const long total = (long)count * l.gp * 4;
+    const int block = 256;
+    const long grid = (total + block - 1) / block;
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)grid), dim3(block), 0, stream, tiles, sb, ids, out, out_f32 ? 1 : 0,
+                       l.n, l.k, l.g, l.gp, total);
+    return hipGetLastError();
+}
 
 hipError_t launch_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint32_t* w_up,
                          const uint16_t* s_up, const uint16_t* b_up, uint4* tiles, uint2* sb, const Layout& l,

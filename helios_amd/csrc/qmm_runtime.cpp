@@ -495,6 +495,33 @@ Gemma4Status gemma4_qlinear_forward_greedy(const Gemma4QLinear* linear, void* st
     }
 }
 
+Gemma4Status gemma4_qlinear_embed(const Gemma4QLinear* linear, void* stream, const int32_t* ids_dev, uint32_t count,
+                                  void* out_dev, Gemma4QmmDtype dtype) {
+    try {
+        const std::string name("gemma4_qlinear_embed");
+        if (!valid_handle(linear)) return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " received an invalid handle");
+        if (linear->pair_rows != 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": the handle is a gate|up pair, not a projection");
+        if (dtype != GEMMA4_QMM_BF16 && dtype != GEMMA4_QMM_F32)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": dtype must be BF16 or F32");
+        if (count == 0) return ok();
+        if (ids_dev == nullptr || out_dev == nullptr)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " requires non-null ids and output");
+        if ((reinterpret_cast<uintptr_t>(out_dev) & 15u) != 0 || (reinterpret_cast<uintptr_t>(ids_dev) & 3u) != 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": ids must be 4-byte and the output 16-byte aligned");
+        if (count > (1u << 24)) return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, name + ": count exceeds 2^24");
+        DeviceGuard guard;
+        hipError_t e = guard.enter(linear->device);
+        if (e != hipSuccess) return hip_fail((name + ": hipSetDevice").c_str(), e);
+        e = q4::launch_embed(linear->tiles, linear->sb, ids_dev, (int)count, out_dev, dtype == GEMMA4_QMM_F32,
+                             linear->layout, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_fail((name + ": launch").c_str(), e);
+        return ok();
+    } catch (...) {
+        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_embed: unexpected native exception");
+    }
+}
+
 Gemma4Status gemma4_qlinear_dequantize(const Gemma4QLinear* linear, void* stream, float* w_dev) {
     try {
         if (!valid_handle(linear))

@@ -102,6 +102,7 @@ def load_library(path: str | None = None):
         "gemma4_qgeglu_create_device": [ctypes.POINTER(_Desc), vp, vp, vp, vp, vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qgeglu_forward": [vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int],
         "gemma4_qlinear_forward_greedy": [vp, vp, vp, ctypes.c_uint32, ctypes.c_float, vp, ctypes.c_int, vp, vp],
+        "gemma4_qlinear_embed": [vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -294,6 +295,22 @@ class QuantizedLinear(_Handle):
             self._handle, _stream_ptr(stream), _dev_ptr(x2), rows, float(softcap),
             _dev_ptr(logits) if logits is not None else None, code, _dev_ptr(token), _dev_ptr(value)), self._lib)
         return token, value, logits
+
+    def embed(self, ids, out_dtype=None, stream=None):
+        """Rows ids of the dequantized weight, [len(ids), K] (the quantized embedding
+        gather, native_model.cc:364-376).  ids: int32 device tensor; rows outside
+        [0, N) come back as zeros.  fp32 is bit-exact; bf16 is it rounded once."""
+        import torch
+
+        out_dtype = out_dtype or torch.bfloat16
+        if out_dtype not in (torch.bfloat16, torch.float32):
+            raise Gemma4Error(Status.INVALID_ARGUMENT, "out_dtype must be bfloat16 or float32")
+        ids = ids.to(torch.int32).contiguous()
+        out = torch.empty((ids.numel(), self.in_features), dtype=out_dtype, device=ids.device)
+        check(self._lib.gemma4_qlinear_embed(self._handle, _stream_ptr(stream), _dev_ptr(ids), ids.numel(),
+                                             _dev_ptr(out), DTYPE_F32 if out_dtype == torch.float32 else DTYPE_BF16),
+              self._lib)
+        return out.reshape(tuple(ids.shape) + (self.in_features,))
 
     def dequantize(self, stream=None):
         import torch

@@ -140,6 +140,15 @@ Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, c
  * output is [2, F, K]: the gate rows, then the up rows. */
 Gemma4Status gemma4_qlinear_dequantize(const Gemma4QLinear* linear, void* stream, float* w_dev);
 
+/* Quantized embedding gather — replaces quantized_embedding (native_model.cc:364-376:
+ * take of the embed_tokens triple's rows, then dequantize; the same tied triple the
+ * lm_head uses).  out[t, :] = s * q + b of row ids[t], for t < count:
+ *   ids_dev int32 [count] on the device; ids outside [0, N) give rows of zeros
+ *   out_dev [count, K] of dtype, 16-byte aligned: F32 is bit-exact (as
+ *   gemma4_qlinear_dequantize); BF16 is that fp32 value rounded once (to nearest even). */
+Gemma4Status gemma4_qlinear_embed(const Gemma4QLinear* linear, void* stream, const int32_t* ids_dev, uint32_t count,
+                                  void* out_dev, Gemma4QmmDtype dtype);
+
 /* Greedy lm_head: the product, the final-logit softcap and argmax in one call —
  * replaces target_logits_for_hidden (native_model.cc:1782-1795: quantized_matmul, then
  * tanh(logits / 30) * 30) followed by argmax over the vocabulary (native_model.cc:3734,

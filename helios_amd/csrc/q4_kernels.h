@@ -41,6 +41,18 @@ hipError_t launch_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b
 hipError_t launch_dequantize(const uint4* tiles, const uint2* sb, float* out, const Layout& l, int pair_rows,
                              hipStream_t stream);
 
+// 8-bit affine weights as two 4-bit planes over K' = 2K (q4_layout.hip): the layout l
+// of such a handle is make_layout(N, 2K) (pair_layout(F, 2K) for a pair); its kernels
+// take x' = [x | x] from launch_duplicate_x (x 16-byte aligned, K a multiple of 64).
+hipError_t launch_repack8(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint32_t* w_up,
+                          const uint16_t* s_up, const uint16_t* b_up, uint4* tiles, uint2* sb, const Layout& l,
+                          int pair_rows, hipStream_t stream);
+hipError_t launch_dequantize8(const uint4* tiles, const uint2* sb, float* out, const Layout& l, int pair_rows,
+                              hipStream_t stream);
+hipError_t launch_embed8(const uint4* tiles, const uint2* sb, const int32_t* ids, int count, void* out, bool out_f32,
+                         const Layout& l, hipStream_t stream);
+hipError_t launch_duplicate_x(const uint16_t* x, uint16_t* xp, int m, int k, hipStream_t stream);
+
 // out[t, :] = dequantized row ids[t] of a projection (fp32, or bf16 rounded once), t <
 // count; ids outside [0, N) give zero rows.  out is 16-byte aligned, [count, K].
 hipError_t launch_embed(const uint4* tiles, const uint2* sb, const int32_t* ids, int count, void* out, bool out_f32,

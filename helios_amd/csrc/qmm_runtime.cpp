@@ -127,20 +127,26 @@ struct Gemma4QLinear {
 
 namespace {
 
+// Tiled layout of a handle: a 4-bit projection over K, an 8-bit one as two 4-bit
+// planes over 2K; a gate|up pair interleaves its two projections 8 rows at a time.
+q4::Layout handle_layout(const Gemma4QLinearDesc& d, bool pair) {
+    const int k = (int)d.in_features * (d.bits == 8 ? 2 : 1);
+    return pair ? q4::pair_layout((int)d.out_features, k) : q4::make_layout((int)d.out_features, k);
+}
+
 Gemma4Status check_desc(const Gemma4QLinearDesc* desc, bool pair, const char* fn) {
     if (desc == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, std::string(fn) + " requires a non-null desc");
     if (desc->out_features == 0 || desc->in_features == 0)
         return fail(GEMMA4_ERR_INVALID_ARGUMENT, std::string(fn) + ": out_features and in_features must be > 0");
-    if (desc->bits != 4 || desc->group_size != 64)
+    if ((desc->bits != 4 && desc->bits != 8) || desc->group_size != 64)
         return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
-                    std::string(fn) + ": only affine bits=4 group_size=64 is supported (got bits=" +
+                    std::string(fn) + ": only affine bits=4 or 8 with group_size=64 is supported (got bits=" +
                         std::to_string(desc->bits) + " group_size=" + std::to_string(desc->group_size) + ")");
     if (desc->in_features % 64 != 0)
         return fail(GEMMA4_ERR_INVALID_ARGUMENT, std::string(fn) + ": in_features must be a multiple of 64");
-    if (desc->out_features > (1u << 29) || desc->in_features > (1u << 24))
+    if (desc->out_features > (1u << 29) || desc->in_features > (1u << 23))
         return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, std::string(fn) + ": shape exceeds the supported range");
-    const q4::Layout l = pair ? q4::pair_layout((int)desc->out_features, (int)desc->in_features)
-                              : q4::make_layout((int)desc->out_features, (int)desc->in_features);
+    const q4::Layout l = handle_layout(*desc, pair);
     if (l.tile_bytes() > q4::kMaxBufferBytes || l.sb_bytes() > q4::kMaxBufferBytes)
         return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
                     std::string(fn) + ": weights exceed 2 GiB per projection (split it along out_features)");
@@ -157,6 +163,32 @@ void release(Gemma4QLinear* h) {
 
 bool valid_handle(const Gemma4QLinear* h) { return h != nullptr && h->magic == kQLinearMagic; }
 
+// The x the kernels read: x itself, or for an 8-bit handle x' = [x | x] (rows x 2K) in
+// a stream-ordered scratch allocation that the caller frees on the same stream.
+Gemma4Status prepare_x(const Gemma4QLinear* h, const uint16_t* x, uint32_t rows, hipStream_t st, const std::string& name,
+                       const uint16_t** xk, void** scratch) {
+    *xk = x;
+    *scratch = nullptr;
+    if (h->desc.bits != 8) return GEMMA4_OK;
+    const size_t k = h->desc.in_features;
+    if ((size_t)rows * 2 * k * 2 > q4::kMaxBufferBytes)
+        return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, name + ": x exceeds 1 GiB for an 8-bit projection (split the rows)");
+    hipMemPool_t pool = nullptr;
+    hipError_t e = scratch_pool(h->device, &pool);
+    if (e != hipSuccess) return hip_fail((name + ": scratch pool").c_str(), e);
+    e = hipMallocFromPoolAsync(scratch, (size_t)rows * 2 * k * 2, pool, st);
+    if (e != hipSuccess)
+        return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": x workspace allocation failed: " + hipGetErrorString(e));
+    e = q4::launch_duplicate_x(x, static_cast<uint16_t*>(*scratch), (int)rows, (int)k, st);
+    if (e != hipSuccess) {
+        (void)hipFreeAsync(*scratch, st);
+        *scratch = nullptr;
+        return hip_fail((name + ": x duplicate").c_str(), e);
+    }
+    *xk = static_cast<const uint16_t*>(*scratch);
+    return GEMMA4_OK;
+}
+
 // One weight triple in MLX layout (device pointers).
 struct Triple {
     const uint32_t* w;
@@ -172,8 +204,7 @@ Gemma4Status build_handle(const Gemma4QLinearDesc* desc, const Triple& main, con
     if (h == nullptr) return fail(GEMMA4_ERR_MEMORY_GUARD, "gemma4_qlinear: host allocation failed");
     h->desc = *desc;
     h->pair_rows = up ? (int)desc->out_features : 0;
-    h->layout = up ? q4::pair_layout((int)desc->out_features, (int)desc->in_features)
-                   : q4::make_layout((int)desc->out_features, (int)desc->in_features);
+    h->layout = handle_layout(*desc, up != nullptr);
     hipError_t e = hipGetDevice(&h->device);
     if (e != hipSuccess) {
         delete h;
@@ -194,8 +225,12 @@ Gemma4Status build_handle(const Gemma4QLinearDesc* desc, const Triple& main, con
         return fail(GEMMA4_ERR_MEMORY_GUARD, std::string("gemma4_qlinear: device allocation failed: ") +
                                                  hipGetErrorString(e));
     }
-    e = q4::launch_repack(main.w, main.s, main.b, up ? up->w : nullptr, up ? up->s : nullptr, up ? up->b : nullptr,
-                          h->tiles, h->sb, h->layout, h->pair_rows, stream);
+    if (desc->bits == 8)
+        e = q4::launch_repack8(main.w, main.s, main.b, up ? up->w : nullptr, up ? up->s : nullptr,
+                               up ? up->b : nullptr, h->tiles, h->sb, h->layout, h->pair_rows, stream);
+    else
+        e = q4::launch_repack(main.w, main.s, main.b, up ? up->w : nullptr, up ? up->s : nullptr,
+                              up ? up->b : nullptr, h->tiles, h->sb, h->layout, h->pair_rows, stream);
     if (e != hipSuccess) {
         release(h);
         delete h;
@@ -210,7 +245,7 @@ Gemma4Status build_handle(const Gemma4QLinearDesc* desc, const Triple& main, con
 Gemma4Status create_from_host(const Gemma4QLinearDesc* desc, const uint32_t* const* w, const uint16_t* const* s,
                               const uint16_t* const* b, int parts, const char* fn, Gemma4QLinear** out) {
     const size_t n = desc->out_features, k = desc->in_features;
-    const size_t wbytes = n * k / 2, sbytes = n * (k / 64) * 2, part = wbytes + 2 * sbytes;
+    const size_t wbytes = n * k * desc->bits / 8, sbytes = n * (k / 64) * 2, part = wbytes + 2 * sbytes;
     void* staging = nullptr;
     hipError_t e = hipMalloc(&staging, part * parts);
     if (e != hipSuccess)
@@ -282,10 +317,15 @@ Gemma4Status run_forward(const Gemma4QLinear* linear, void* stream, const uint16
     const bool f32 = y_dtype == GEMMA4_QMM_F32;
     const int mode = geglu ? (f32 ? q4::kOutGegluF32 : q4::kOutGegluBf16) : (f32 ? q4::kOutF32 : q4::kOutBf16);
     const int n_out = linear->pair_rows;
+    void* xs = nullptr;
+    Gemma4Status pst = prepare_x(linear, x_dev, rows, st, name, &x_dev, &xs);
+    if (pst != GEMMA4_OK) return pst;
     if ((int)rows < q4::kGemmMinRows) {
         const q4::OutParams op{y_dev, nullptr, mode, n_out, 0, 0.0f};
         e = q4::launch_decode(linear->tiles, linear->sb, x_dev, op, (int)rows, linear->layout, st);
+        const hipError_t ex = xs ? hipFreeAsync(xs, st) : hipSuccess;
         if (e != hipSuccess) return hip_fail((name + ": decode launch").c_str(), e);
+        if (ex != hipSuccess) return hip_fail((name + ": x workspace release").c_str(), ex);
         return ok();
     }
     // group sums of x (and split-K partial sums) live in a stream-ordered scratch
@@ -293,16 +333,19 @@ Gemma4Status run_forward(const Gemma4QLinear* linear, void* stream, const uint16
     const size_t ws_bytes = q4::gemm_workspace_bytes((int)rows, linear->layout);
     hipMemPool_t pool = nullptr;
     e = scratch_pool(linear->device, &pool);
-    if (e != hipSuccess) return hip_fail((name + ": scratch pool").c_str(), e);
     void* ws = nullptr;
-    e = hipMallocFromPoolAsync(&ws, ws_bytes, pool, st);
-    if (e != hipSuccess)
+    if (e == hipSuccess) e = hipMallocFromPoolAsync(&ws, ws_bytes, pool, st);
+    if (e != hipSuccess) {
+        if (xs) (void)hipFreeAsync(xs, st);
         return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
+    }
     e = q4::launch_gemm(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, mode, n_out, linear->layout, ws,
                         linear->gelu_table, st);
     const hipError_t ef = hipFreeAsync(ws, st);
+    const hipError_t ex = xs ? hipFreeAsync(xs, st) : hipSuccess;
     if (e != hipSuccess) return hip_fail((name + ": gemm launch").c_str(), e);
     if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);
+    if (ex != hipSuccess) return hip_fail((name + ": x workspace release").c_str(), ex);
     return ok();
 }
 
@@ -482,10 +525,17 @@ Gemma4Status gemma4_qlinear_forward_greedy(const Gemma4QLinear* linear, void* st
             return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
         const int mode = dtype == GEMMA4_QMM_F32 ? q4::kOutGreedyF32 : q4::kOutGreedyBf16;
         const q4::OutParams op{logits_dev, static_cast<unsigned long long*>(part), mode, 0, nb, softcap};
+        void* xs = nullptr;
+        const Gemma4Status pst = prepare_x(linear, x_dev, rows, st, name, &x_dev, &xs);
+        if (pst != GEMMA4_OK) {
+            (void)hipFreeAsync(part, st);
+            return pst;
+        }
         e = q4::launch_decode(linear->tiles, linear->sb, x_dev, op, (int)rows, linear->layout, st);
         if (e == hipSuccess)
             e = q4::launch_greedy_reduce(static_cast<const unsigned long long*>(part), nb, (int)rows, token_dev,
                                          value_dev, st);
+        if (xs) (void)hipFreeAsync(xs, st);
         const hipError_t ef = hipFreeAsync(part, st);
         if (e != hipSuccess) return hip_fail((name + ": launch").c_str(), e);
         if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);
@@ -513,8 +563,12 @@ Gemma4Status gemma4_qlinear_embed(const Gemma4QLinear* linear, void* stream, con
         DeviceGuard guard;
         hipError_t e = guard.enter(linear->device);
         if (e != hipSuccess) return hip_fail((name + ": hipSetDevice").c_str(), e);
-        e = q4::launch_embed(linear->tiles, linear->sb, ids_dev, (int)count, out_dev, dtype == GEMMA4_QMM_F32,
-                             linear->layout, static_cast<hipStream_t>(stream));
+        if (linear->desc.bits == 8)
+            e = q4::launch_embed8(linear->tiles, linear->sb, ids_dev, (int)count, out_dev, dtype == GEMMA4_QMM_F32,
+                                  linear->layout, static_cast<hipStream_t>(stream));
+        else
+            e = q4::launch_embed(linear->tiles, linear->sb, ids_dev, (int)count, out_dev, dtype == GEMMA4_QMM_F32,
+                                 linear->layout, static_cast<hipStream_t>(stream));
         if (e != hipSuccess) return hip_fail((name + ": launch").c_str(), e);
         return ok();
     } catch (...) {
@@ -532,8 +586,12 @@ Gemma4Status gemma4_qlinear_dequantize(const Gemma4QLinear* linear, void* stream
         DeviceGuard guard;
         hipError_t e = guard.enter(linear->device);
         if (e != hipSuccess) return hip_fail("gemma4_qlinear_dequantize: hipSetDevice", e);
-        e = q4::launch_dequantize(linear->tiles, linear->sb, w_dev, linear->layout, linear->pair_rows,
-                                  static_cast<hipStream_t>(stream));
+        if (linear->desc.bits == 8)
+            e = q4::launch_dequantize8(linear->tiles, linear->sb, w_dev, linear->layout, linear->pair_rows,
+                                       static_cast<hipStream_t>(stream));
+        else
+            e = q4::launch_dequantize(linear->tiles, linear->sb, w_dev, linear->layout, linear->pair_rows,
+                                      static_cast<hipStream_t>(stream));
         if (e != hipSuccess) return hip_fail("gemma4_qlinear_dequantize: launch", e);
         return ok();
     } catch (...) {

@@ -150,21 +150,22 @@ def _check_spec(group_size: int, bits: int, mode: str, transpose: bool = True) -
         raise Gemma4Error(Status.UNSUPPORTED_CONFIG, f"mode {mode!r} is not supported (affine only)")
     if not transpose:
         raise Gemma4Error(Status.UNSUPPORTED_CONFIG, "transpose=False is not supported (the call sites use y = x . W^T)")
-    if bits != 4 or group_size != 64:
+    if bits not in (4, 8) or group_size != 64:
         raise Gemma4Error(Status.UNSUPPORTED_CONFIG,
-                          f"only bits=4 group_size=64 is supported (got bits={bits} group_size={group_size})")
+                          f"only bits=4 or 8 with group_size=64 is supported (got bits={bits} group_size={group_size})")
 
 
-def _host_triple(weight, scales, biases, n: int, k: int, group_size: int):
+def _host_triple(weight, scales, biases, n: int, k: int, group_size: int, bits: int):
     w = np.ascontiguousarray(weight, dtype=np.uint32)
     s = np.ascontiguousarray(scales, dtype=np.uint16)
     b = np.ascontiguousarray(biases, dtype=np.uint16)
-    if w.shape != (n, k // 8) or s.shape != (n, k // group_size) or b.shape != s.shape:
-        raise Gemma4Error(Status.INVALID_ARGUMENT, f"weight must be [{n}, {k // 8}] and scales/biases [{n}, {k // group_size}]")
+    wc = k * bits // 32
+    if w.shape != (n, wc) or s.shape != (n, k // group_size) or b.shape != s.shape:
+        raise Gemma4Error(Status.INVALID_ARGUMENT, f"weight must be [{n}, {wc}] and scales/biases [{n}, {k // group_size}]")
     return w, s, b
 
 
-def _device_triple(weight, scales, biases, n: int, k: int, group_size: int):
+def _device_triple(weight, scales, biases, n: int, k: int, group_size: int, bits: int):
     import torch
 
     w = weight.contiguous()
@@ -172,8 +173,9 @@ def _device_triple(weight, scales, biases, n: int, k: int, group_size: int):
     b = biases.contiguous()
     if w.dtype not in (torch.int32, torch.uint32) or s.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
         raise Gemma4Error(Status.INVALID_ARGUMENT, "weight must be int32/uint32 and scales/biases bfloat16")
-    if tuple(w.shape) != (n, k // 8) or tuple(s.shape) != (n, k // group_size) or tuple(b.shape) != tuple(s.shape):
-        raise Gemma4Error(Status.INVALID_ARGUMENT, f"weight must be [{n}, {k // 8}] and scales/biases [{n}, {k // group_size}]")
+    wc = k * bits // 32
+    if tuple(w.shape) != (n, wc) or tuple(s.shape) != (n, k // group_size) or tuple(b.shape) != tuple(s.shape):
+        raise Gemma4Error(Status.INVALID_ARGUMENT, f"weight must be [{n}, {wc}] and scales/biases [{n}, {k // group_size}]")
     if not (w.is_cuda and s.is_cuda and b.is_cuda):
         raise Gemma4Error(Status.INVALID_ARGUMENT, "device tensors must be on a CUDA (HIP) device")
     return w, s, b
@@ -231,9 +233,9 @@ class _Handle:
 class QuantizedLinear(_Handle):
     """One projection's weight triple resident on the GPU (a ``Gemma4QLinear`` handle).
 
-    ``weight`` uint32/int32 [N, K/8], ``scales``/``biases`` bf16 [N, K/64] in MLX
-    layout — torch tensors on the current CUDA device, or numpy arrays on the host
-    (``uint32`` and ``uint16`` bit patterns)."""
+    ``weight`` uint32/int32 [N, K*bits/32], ``scales``/``biases`` bf16 [N, K/64] in
+    MLX layout — torch tensors on the current CUDA device, or numpy arrays on the
+    host (``uint32`` and ``uint16`` bit patterns).  bits is 4 or 8 (group 64)."""
 
     def __init__(self, weight, scales, biases, group_size: int = 64, bits: int = 4, stream=None):
         _check_spec(group_size, bits, "affine")
@@ -243,12 +245,12 @@ class QuantizedLinear(_Handle):
         k = int(weight.shape[1]) * 32 // bits
         desc = _Desc(n, k, bits, group_size)
         if isinstance(weight, np.ndarray):
-            t = _host_triple(weight, scales, biases, n, k, group_size)
+            t = _host_triple(weight, scales, biases, n, k, group_size, bits)
             status = self._lib.gemma4_qlinear_create(ctypes.byref(desc), *_host_ptrs(t), ctypes.byref(self._handle))
         else:
             import torch
 
-            t = _device_triple(weight, scales, biases, n, k, group_size)
+            t = _device_triple(weight, scales, biases, n, k, group_size, bits)
             with torch.cuda.device(t[0].device):
                 status = self._lib.gemma4_qlinear_create_device(ctypes.byref(desc), *map(_dev_ptr, t),
                                                                 _stream_ptr(stream), ctypes.byref(self._handle))
@@ -336,15 +338,15 @@ class QuantizedGeGLU(_Handle):
         k = int(gate[0].shape[1]) * 32 // bits
         desc = _Desc(n, k, bits, group_size)
         if isinstance(gate[0], np.ndarray):
-            tg = _host_triple(*gate, n, k, group_size)
-            tu = _host_triple(*up, n, k, group_size)
+            tg = _host_triple(*gate, n, k, group_size, bits)
+            tu = _host_triple(*up, n, k, group_size, bits)
             status = self._lib.gemma4_qgeglu_create(ctypes.byref(desc), *_host_ptrs(tg), *_host_ptrs(tu),
                                                     ctypes.byref(self._handle))
         else:
             import torch
 
-            tg = _device_triple(*gate, n, k, group_size)
-            tu = _device_triple(*up, n, k, group_size)
+            tg = _device_triple(*gate, n, k, group_size, bits)
+            tu = _device_triple(*up, n, k, group_size, bits)
             with torch.cuda.device(tg[0].device):
                 status = self._lib.gemma4_qgeglu_create_device(ctypes.byref(desc), *map(_dev_ptr, tg),
                                                                *map(_dev_ptr, tu), _stream_ptr(stream),

@@ -31,8 +31,11 @@
  *   w[n,k] = scales[n,k/64] * q[n,k] + biases[n,k/64]
  *   x       bf16   [M, K] row-major, device memory, 16-byte aligned
  *   y       bf16 or fp32 [M, N] row-major, device memory;  y = x . W^T
- * Only bits = 4 with group_size = 64 is accepted (the configuration every
- * projection of the reference's Gemma 4 12B artifact uses, model_manifest.cc:148).
+ * bits = 4 or 8 with group_size = 64 is accepted: the default of the reference's
+ * Gemma 4 12B artifact and the only overrides its loader allows (model_manifest.cc:148).
+ * With bits = 8 the weight is uint32 [N, K/4], code k in byte k%4 of word k/4, lowest
+ * byte first; it is held as two 4-bit planes (q = 16*qh + ql) and runs on the same
+ * kernels over 2K, reading [x | x].
  *
  * Streams are hipStream_t values passed as void* (NULL = the null stream).  All
  * device work is asynchronous on that stream.  A handle is immutable after
@@ -84,7 +87,7 @@ typedef struct Gemma4QmmVersionInfo {
 typedef struct Gemma4QLinearDesc {
     uint32_t out_features; /* N */
     uint32_t in_features;  /* K, a multiple of group_size */
-    uint32_t bits;         /* 4 */
+    uint32_t bits;         /* 4 or 8 */
     uint32_t group_size;   /* 64 */
 } Gemma4QLinearDesc;
 

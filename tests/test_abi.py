@@ -55,10 +55,16 @@ def test_null_and_invalid_arguments_set_last_error(lib):
     assert "non-null desc" in qmm.last_error()
     assert lib.gemma4_qlinear_create(None, None, None, None, None) == qmm.Status.INVALID_ARGUMENT
     assert "out pointer" in qmm.last_error()
-    desc = qmm._Desc(16, 64, 8, 64)
+    desc = qmm._Desc(16, 64, 2, 64)
     assert lib.gemma4_qlinear_create(ctypes.byref(desc), None, None, None, ctypes.byref(out)) == \
         qmm.Status.UNSUPPORTED_CONFIG
-    assert "bits=8" in qmm.last_error()
+    assert "bits=2" in qmm.last_error()
+    desc = qmm._Desc(16, 64, 8, 32)
+    assert lib.gemma4_qlinear_create(ctypes.byref(desc), None, None, None, ctypes.byref(out)) == \
+        qmm.Status.UNSUPPORTED_CONFIG
+    desc = qmm._Desc(16, 64, 8, 64)  # 8-bit is accepted: the next check is the pointers
+    assert lib.gemma4_qlinear_create(ctypes.byref(desc), None, None, None, ctypes.byref(out)) == \
+        qmm.Status.INVALID_ARGUMENT
     desc = qmm._Desc(16, 100, 4, 64)
     assert lib.gemma4_qlinear_create(ctypes.byref(desc), None, None, None, ctypes.byref(out)) == \
         qmm.Status.INVALID_ARGUMENT
@@ -94,7 +100,7 @@ def test_geglu_pair_argument_checks(lib):
     assert lib.gemma4_qgeglu_create(ctypes.byref(desc), None, None, None, None, None, None, ctypes.byref(out)) == \
         qmm.Status.INVALID_ARGUMENT
     assert "gate and up" in qmm.last_error()
-    desc = qmm._Desc(64, 64, 8, 64)
+    desc = qmm._Desc(64, 64, 3, 64)
     assert lib.gemma4_qgeglu_create_device(ctypes.byref(desc), None, None, None, None, None, None, None,
                                            ctypes.byref(out)) == qmm.Status.UNSUPPORTED_CONFIG
     assert out.value is None
@@ -129,7 +135,7 @@ def test_struct_layouts_match_header():
 
 def test_python_mirror_rejects_unsupported_specs():
     with pytest.raises(qmm.Gemma4Error) as e:
-        qmm.quantized_matmul(None, None, None, None, bits=8)
+        qmm.quantized_matmul(None, None, None, None, bits=3)
     assert e.value.status == qmm.Status.UNSUPPORTED_CONFIG
     with pytest.raises(qmm.Gemma4Error):
         qmm.quantized_matmul(None, None, None, None, transpose=False)

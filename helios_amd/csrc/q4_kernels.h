@@ -97,6 +97,12 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
 // Fills table[65536] with gelu of every bf16 bit pattern, in the bf16 op sequence.
 hipError_t launch_gelu_table(uint16_t* table, hipStream_t stream);
 
+// LoRA delta added in place to a projection output y [m, n] (bf16 or fp32) already
+// holding the base product: t [m, rank] is fp32 scratch, a [rank, k] and b [n, rank]
+// fp32 on the device (q4_lora.hip).
+hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float* t, void* y, int m, int n, int k,
+                       int rank, float scale, bool out_f32, hipStream_t stream);
+
 // Rows at or above which forward uses the GEMM path.
 constexpr int kGemmMinRows = 32;
 

@@ -20,6 +20,7 @@ namespace {
 
 constexpr uint64_t kQLinearMagic = 0x47454d3451344c4eULL;  // "GEM4Q4LN"
 constexpr int kGreedyMaxRows = 16;  // rows per greedy-head call (decode and verify blocks)
+constexpr uint64_t kLoraMagic = 0x47454d344c4f5241ULL;  // "GEM4LORA"
 thread_local char g_last_error[512] = "";
 
 Gemma4Status fail(Gemma4Status status, const std::string& message) {
@@ -123,6 +124,15 @@ struct Gemma4QLinear {
     int device = 0;
     uint4* tiles = nullptr;
     uint2* sb = nullptr;
+};
+
+struct Gemma4QLora {
+    uint64_t magic = 0;
+    uint32_t rank = 0, in_features = 0, out_features = 0;
+    float scale = 1.0f;
+    int device = 0;
+    float* a = nullptr;  // [rank, K] fp32
+    float* b = nullptr;  // [N, rank] fp32
 };
 
 namespace {
@@ -542,6 +552,93 @@ Gemma4Status gemma4_qlinear_forward_greedy(const Gemma4QLinear* linear, void* st
         return ok();
     } catch (...) {
         return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward_greedy: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qlora_create(const float* a, const float* b, uint32_t rank, uint32_t in_features,
+                                 uint32_t out_features, float scale, Gemma4QLora** out) {
+    try {
+        const std::string name("gemma4_qlora_create");
+        if (out == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " requires a non-null out pointer");
+        *out = nullptr;
+        if (a == nullptr || b == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " requires non-null A and B");
+        if (rank == 0 || rank > 1024 || in_features == 0 || out_features == 0 || in_features > (1u << 24) ||
+            out_features > (1u << 29))
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": rank must be 1..1024 and the shape non-empty");
+        if (!(scale == scale) || scale > 3.0e38f || scale < -3.0e38f)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": scale must be finite");
+        Gemma4QLora* h = new (std::nothrow) Gemma4QLora();
+        if (h == nullptr) return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": host allocation failed");
+        h->rank = rank;
+        h->in_features = in_features;
+        h->out_features = out_features;
+        h->scale = scale;
+        hipError_t e = hipGetDevice(&h->device);
+        const size_t abytes = (size_t)rank * in_features * 4, bbytes = (size_t)out_features * rank * 4;
+        if (e == hipSuccess) e = hipMalloc(&h->a, abytes);
+        if (e == hipSuccess) e = hipMalloc(&h->b, bbytes);
+        if (e == hipSuccess) e = hipMemcpy(h->a, a, abytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(h->b, b, bbytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            if (h->a) (void)hipFree(h->a);
+            if (h->b) (void)hipFree(h->b);
+            delete h;
+            return fail(GEMMA4_ERR_ADAPTER, name + ": device copy failed: " + hipGetErrorString(e));
+        }
+        h->magic = kLoraMagic;
+        *out = h;
+        return ok();
+    } catch (...) {
+        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlora_create: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qlora_free(Gemma4QLora* lora) {
+    if (lora == nullptr) return ok();
+    if (lora->magic != kLoraMagic) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlora_free received an invalid handle");
+    DeviceGuard guard;
+    (void)guard.enter(lora->device);
+    (void)hipFree(lora->a);
+    (void)hipFree(lora->b);
+    lora->magic = 0;
+    delete lora;
+    return ok();
+}
+
+Gemma4Status gemma4_qlinear_forward_lora(const Gemma4QLinear* linear, const Gemma4QLora* lora, void* stream,
+                                         const uint16_t* x_dev, uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype) {
+    try {
+        const std::string name("gemma4_qlinear_forward_lora");
+        if (lora != nullptr) {
+            if (lora->magic != kLoraMagic)
+                return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " received an invalid adapter handle");
+            if (valid_handle(linear) &&
+                (lora->in_features != linear->desc.in_features || lora->out_features != linear->desc.out_features))
+                return fail(GEMMA4_ERR_ADAPTER, name + ": adapter shape does not match the projection");
+            if (valid_handle(linear) && lora->device != linear->device)
+                return fail(GEMMA4_ERR_ADAPTER, name + ": adapter and projection are on different devices");
+        }
+        Gemma4Status st = run_forward(linear, stream, x_dev, rows, y_dev, y_dtype, false, name.c_str());
+        if (st != GEMMA4_OK || lora == nullptr || rows == 0) return st;
+        DeviceGuard guard;
+        hipError_t e = guard.enter(linear->device);
+        if (e != hipSuccess) return hip_fail((name + ": hipSetDevice").c_str(), e);
+        hipStream_t sh = static_cast<hipStream_t>(stream);
+        hipMemPool_t pool = nullptr;
+        e = scratch_pool(linear->device, &pool);
+        void* t = nullptr;
+        if (e == hipSuccess) e = hipMallocFromPoolAsync(&t, (size_t)rows * lora->rank * 4, pool, sh);
+        if (e != hipSuccess)
+            return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
+        e = q4::launch_lora(x_dev, lora->a, lora->b, static_cast<float*>(t), y_dev, (int)rows,
+                            (int)linear->desc.out_features, (int)linear->desc.in_features, (int)lora->rank, lora->scale,
+                            y_dtype == GEMMA4_QMM_F32, sh);
+        const hipError_t ef = hipFreeAsync(t, sh);
+        if (e != hipSuccess) return hip_fail((name + ": launch").c_str(), e);
+        if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);
+        return ok();
+    } catch (...) {
+        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward_lora: unexpected native exception");
     }
 }
 

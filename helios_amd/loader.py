@@ -14,7 +14,8 @@ packed width, ``K = weight.shape[1] * 32 / bits`` (``native_model.cc:281-287``).
 This module mirrors that: :func:`parse_quantization`, :func:`quantization_for`,
 :class:`Checkpoint` (a safetensors reader that maps the files and executes nothing
 from them), :func:`load_linear` / :func:`load_geglu_pair` (handles on the current
-device) and :func:`write_safetensors` (for fixtures).
+device), :func:`load_lora_adapter` (the LoRA modules of an adapter directory,
+``native_model.cc:3300-3440``) and :func:`write_safetensors` (for fixtures).
 """
 
 from __future__ import annotations
@@ -184,3 +185,83 @@ def write_safetensors(path: str, tensors: dict, metadata: dict | None = None) ->
         f.write(h)
         for raw in blobs:
             f.write(raw)
+
+
+# ---------------------------------------------------------------------------
+# LoRA adapters (native_model.cc:225-288, :3300-3440)
+# ---------------------------------------------------------------------------
+
+def canonical_lora_prefix(prefix: str) -> str:
+    """PEFT names -> the base model's tensor prefixes (native_model.cc:237-248)."""
+    for head in ("base_model.model.model.", "base_model.model.", "model."):
+        if prefix.startswith(head):
+            return "language_model.model." + prefix[len(head):]
+    return prefix
+
+
+def target_module_allowed(prefix: str, target_modules) -> bool:
+    """The leaf name, the whole prefix or a dotted suffix matches (native_model.cc:267-279)."""
+    leaf = prefix.rsplit(".", 1)[-1]
+    for module in target_modules:
+        t = module.strip()
+        if t and (leaf == t or prefix == t or prefix.endswith("." + t)):
+            return True
+    return False
+
+
+def load_lora_adapter(adapter_path: str, rank: int, alpha: float, target_modules, ckpt: Checkpoint,
+                      config: QuantizationConfig) -> dict:
+    """{prefix: LoraAdapter} from <adapter_path>/adapter_model.safetensors, checked
+    against the base checkpoint the way the reference checks them: lora_A [rank, K]
+    and lora_B [N, rank] for a quantized projection that exists, K from its packed
+    width; scale = alpha / rank."""
+    if rank <= 0:
+        raise qmm.Gemma4Error(qmm.Status.ADAPTER, "LoRA rank must be greater than zero")
+    if not (alpha > 0 and np.isfinite(alpha)):
+        raise qmm.Gemma4Error(qmm.Status.ADAPTER, "LoRA alpha must be finite and positive")
+    if not target_modules:
+        raise qmm.Gemma4Error(qmm.Status.ADAPTER, "LoRA target_modules must not be empty")
+    path = os.path.join(adapter_path, "adapter_model.safetensors")
+    if not os.path.exists(path):
+        raise qmm.Gemma4Error(qmm.Status.ADAPTER, f"adapter_model.safetensors not found at {path}")
+    ad = Checkpoint(path)
+    lora_a, lora_b = {}, {}
+    for name in ad.keys():
+        for suffix, dst in ((".lora_A.weight", lora_a), (".lora_B.weight", lora_b)):
+            if name.endswith(suffix):
+                prefix = canonical_lora_prefix(name[: -len(suffix)])
+                if target_module_allowed(prefix, target_modules):
+                    dst[prefix] = name
+    scale = np.float32(alpha) / np.float32(rank)
+    out = {}
+    for prefix, a_name in sorted(lora_a.items()):
+        if prefix not in lora_b:
+            raise qmm.Gemma4Error(qmm.Status.ADAPTER, f"missing lora_B tensor for {prefix}")
+        if prefix + ".weight" not in ckpt.index:
+            raise qmm.Gemma4Error(qmm.Status.ADAPTER, f"adapter target module does not exist in native model: {prefix}")
+        a = _as_float32(ad, a_name)
+        b = _as_float32(ad, lora_b[prefix])
+        spec = quantization_for(config, prefix)
+        w_shape = ckpt.index[prefix + ".weight"][2]
+        k = w_shape[1] * (32 // spec.bits)
+        if a.shape != (rank, k) or b.shape != (w_shape[0], rank):
+            raise qmm.Gemma4Error(qmm.Status.ADAPTER,
+                                  f"LoRA shape mismatch for {prefix}: A={list(a.shape)} B={list(b.shape)} "
+                                  f"expected A=[{rank},{k}] B=[{w_shape[0]},{rank}]")
+        out[prefix] = qmm.LoraAdapter(a, b, float(scale))
+    if not out:
+        raise qmm.Gemma4Error(qmm.Status.ADAPTER, "adapter contains no supported LoRA tensor pairs for requested "
+                                                  "target_modules")
+    return out
+
+
+def _as_float32(ck: Checkpoint, name: str) -> np.ndarray:
+    dt = ck.dtype(name)
+    v = ck.get(name)
+    if dt == "BF16":
+        return (v.astype(np.uint32) << 16).view(np.float32)
+    if dt == "F16":
+        return v.view(np.float16).astype(np.float32)
+    if dt in ("F32", "F64"):
+        return v.astype(np.float32)
+    raise qmm.Gemma4Error(qmm.Status.ADAPTER, f"{name}: unsupported LoRA dtype {dt}")

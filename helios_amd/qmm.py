@@ -103,6 +103,10 @@ def load_library(path: str | None = None):
         "gemma4_qgeglu_forward": [vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int],
         "gemma4_qlinear_forward_greedy": [vp, vp, vp, ctypes.c_uint32, ctypes.c_float, vp, ctypes.c_int, vp, vp],
         "gemma4_qlinear_embed": [vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int],
+        "gemma4_qlora_create": [vp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float,
+                                ctypes.POINTER(vp)],
+        "gemma4_qlora_free": [vp],
+        "gemma4_qlinear_forward_lora": [vp, vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -298,6 +302,14 @@ class QuantizedLinear(_Handle):
             _dev_ptr(logits) if logits is not None else None, code, _dev_ptr(token), _dev_ptr(value)), self._lib)
         return token, value, logits
 
+    def forward_lora(self, x, lora, out=None, out_dtype=None, stream=None):
+        """forward plus a LoRA adapter's delta (native_model.cc:316-328); lora None is
+        the plain forward."""
+        handle = lora._handle if lora is not None else None
+        fn = lambda h, st, xp, rows, yp, code: self._lib.gemma4_qlinear_forward_lora(  # noqa: E731
+            h, handle, st, xp, rows, yp, code)
+        return _run_forward(fn, self._handle, self._lib, x, self.in_features, self.out_features, out, out_dtype, stream)
+
     def embed(self, ids, out_dtype=None, stream=None):
         """Rows ids of the dequantized weight, [len(ids), K] (the quantized embedding
         gather, native_model.cc:364-376).  ids: int32 device tensor; rows outside
@@ -377,6 +389,37 @@ class QuantizedGeGLU(_Handle):
         out = torch.empty((2, self.out_features, self.in_features), dtype=torch.float32, device="cuda")
         check(self._lib.gemma4_qlinear_dequantize(self._handle, _stream_ptr(stream), _dev_ptr(out)), self._lib)
         return out
+
+
+class LoraAdapter:
+    """One LoRA module on the current device: A [rank, K] and B [N, rank] (float32, as
+    the reference casts lora_A / lora_B, native_model.cc:3420-3426) and scale =
+    alpha / rank.  Used with QuantizedLinear.forward_lora."""
+
+    def __init__(self, a, b, scale: float):
+        self._lib = load_library()
+        self._handle = ctypes.c_void_p()
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        if a.ndim != 2 or b.ndim != 2 or b.shape[1] != a.shape[0]:
+            raise Gemma4Error(Status.ADAPTER, f"LoRA shapes do not chain: A {a.shape}, B {b.shape}")
+        self.rank, self.in_features = a.shape
+        self.out_features = b.shape[0]
+        self.scale = float(scale)
+        check(self._lib.gemma4_qlora_create(a.ctypes.data_as(ctypes.c_void_p), b.ctypes.data_as(ctypes.c_void_p),
+                                            self.rank, self.in_features, self.out_features, self.scale,
+                                            ctypes.byref(self._handle)), self._lib)
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None) is not None and self._handle.value:
+            check(self._lib.gemma4_qlora_free(self._handle), self._lib)
+            self._handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def quantized_matmul(x, w, scales, biases, transpose: bool = True, group_size: int = 64, bits: int = 4,

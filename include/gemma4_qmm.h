@@ -143,6 +143,26 @@ Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, c
  * output is [2, F, K]: the gate rows, then the up rows. */
 Gemma4Status gemma4_qlinear_dequantize(const Gemma4QLinear* linear, void* stream, float* w_dev);
 
+/* ---- LoRA adapters on a quantized projection ----
+ * Replaces quantized_linear's add_lora_delta_if_active (native_model.cc:316-328):
+ *     y = model_dtype(base + model_dtype((float32(x) . A^T) . B^T * scale))
+ * with the adapter module's A [rank, K] (lora_A.weight) and B [N, rank]
+ * (lora_B.weight) as float32 and scale = alpha / rank (native_model.cc:3376-3426).
+ * With y_dtype BF16 the base output and the delta are each rounded to bf16 and added
+ * in bf16 (the scale is bf16, model_scalar); F32 keeps everything fp32. */
+typedef struct Gemma4QLora Gemma4QLora;
+
+/* Copies A and B (host fp32, row-major) to the current device. */
+Gemma4Status gemma4_qlora_create(const float* a, const float* b, uint32_t rank, uint32_t in_features,
+                                 uint32_t out_features, float scale, Gemma4QLora** out);
+Gemma4Status gemma4_qlora_free(Gemma4QLora* lora);
+
+/* gemma4_qlinear_forward plus the adapter's delta; lora NULL is the plain forward.
+ * The adapter must match the projection's K and N and live on its device.  Uses a
+ * stream-ordered scratch of rows * rank * 4 bytes. */
+Gemma4Status gemma4_qlinear_forward_lora(const Gemma4QLinear* linear, const Gemma4QLora* lora, void* stream,
+                                         const uint16_t* x_dev, uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype);
+
 /* Quantized embedding gather — replaces quantized_embedding (native_model.cc:364-376:
  * take of the embed_tokens triple's rows, then dequantize; the same tied triple the
  * lm_head uses).  out[t, :] = s * q + b of row ids[t], for t < count:

@@ -253,3 +253,19 @@ def greedy(values) -> tuple:
     v = np.asarray(values, dtype=np.float32)
     idx = np.argmax(v, axis=-1)
     return idx.astype(np.int32), np.take_along_axis(v, idx[..., None], axis=-1)[..., 0]
+
+
+def lora_ops(x_bits, a, b, scale: float, base, bf16: bool = True) -> np.ndarray:
+    """add_lora_delta_if_active (native_model.cc:316-328) on a base output:
+    model_dtype(base + model_dtype((float32(x) @ A.T) @ B.T * scale)).  The two fp32
+    products are accumulated in float64 and rounded once to fp32 (an fp32 matmul's
+    own order is not pinned); with ``bf16`` the scale (model_scalar), base and delta
+    are bf16 and the sum is rounded to bf16.  Returns float32."""
+    x = bf16_bits_to_f32(x_bits).astype(np.float64)
+    t = (x @ np.asarray(a, np.float64).T).astype(np.float32)
+    d = (t.astype(np.float64) @ np.asarray(b, np.float64).T).astype(np.float32)
+    if bf16:
+        sc = round_to_bf16(np.float32(scale))
+        delta = round_to_bf16(d * sc)
+        return round_to_bf16(round_to_bf16(np.asarray(base, np.float32)) + delta)
+    return (np.asarray(base, np.float32) + d * np.float32(scale)).astype(np.float32)

@@ -1,0 +1,93 @@
+"""GPU parity of LoRA on a quantized projection (gemma4_qlinear_forward_lora) against
+the oracle (lora_ops over the exact base product), plus loading an adapter directory
+against a checkpoint.  Bars: fp32 max |y - y_ref| <= 2e-3 * RMS; bf16 max |y - y_ref|
+<= 1e-2 * RMS + two ulps of y_ref.  The bf16 bar allows two ulps (not the plain
+output's half): the base product is rounded to bf16 before the delta is added (the
+reference's order), so the fp32 accumulation can move that first rounding by an ulp,
+and the sum's own rounding can then land an ulp apart as well."""
+
+import json
+
+import numpy as np
+import pytest
+
+from helios_amd import loader as L
+from oracle import affine as A
+from oracle import c_oracle as C
+from test_gpu_parity import BF16_REL, F32_REL, dev_triple, dev_x, host_bits, random_triple
+
+pytestmark = pytest.mark.gpu
+
+
+def check_bf16_two_roundings(y_bits, want):
+    y = A.bf16_bits_to_f32(y_bits).astype(np.float64)
+    rms = float(np.sqrt(np.mean(want ** 2))) or 1.0
+    excess = np.abs(y - want) - 2 * A.bf16_ulp(want)
+    worst = float(np.max(excess)) / rms
+    return worst <= BF16_REL, worst
+
+
+@pytest.mark.parametrize("n,k,m,r", [(4096, 3840, 1, 16), (2048, 3840, 4, 8), (3840, 15360, 8, 16),
+                                     (300, 640, 17, 4), (256, 640, 64, 16), (512, 3840, 300, 32)])
+@pytest.mark.parametrize("f32", [False, True])
+def test_lora_forward(gpu_lib, n, k, m, r, f32):
+    import torch
+
+    tri = random_triple(n, k, n + k + r)
+    rng = np.random.default_rng(n + r)
+    a = (rng.standard_normal((r, k)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal((n, r)) * 0.02).astype(np.float32)
+    x = A.make_activations(m, k, seed=m + 5, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*tri))
+    lora = gpu_lib.LoraAdapter(a, b, 2.0)
+    dt = torch.float32 if f32 else torch.bfloat16
+    y = lin.forward_lora(dev_x(x), lora, out_dtype=dt)
+    y0 = lin.forward_lora(dev_x(x), None, out_dtype=dt)
+    yp = lin.forward(dev_x(x), out_dtype=dt)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, yp)  # no adapter: the plain forward
+    base = C.qmm_f64(x, *tri).astype(np.float32)
+    want = A.lora_ops(x, a, b, 2.0, base, bf16=not f32).astype(np.float64)
+    if f32:
+        ok, worst = A.check_f32_output(host_bits(y), want, F32_REL)
+    else:
+        ok, worst = check_bf16_two_roundings(host_bits(y), want)
+    assert ok, f"LoRA N={n} K={k} M={m} r={r}: worst error / RMS = {worst:.3e}"
+    lin.close()
+    lora.close()
+
+
+def test_lora_adapter_directory(gpu_lib, tmp_path):
+    import torch
+
+    k, n, r = 256, 128, 4
+    prefix = "language_model.model.layers.0.self_attn.q_proj"
+    tri = random_triple(n, k, 9)
+    L.write_safetensors(str(tmp_path / "model.safetensors"),
+                        {prefix + ".weight": tri[0], prefix + ".scales": ("BF16", tri[1]), prefix + ".biases": ("BF16", tri[2])})
+    ck = L.Checkpoint(str(tmp_path))
+    cfg = L.parse_quantization({"quantization": {"bits": 4, "group_size": 64}})
+    rng = np.random.default_rng(3)
+    a = A.round_to_bf16((rng.standard_normal((r, k)) * 0.05).astype(np.float32))
+    b = A.round_to_bf16((rng.standard_normal((n, r)) * 0.05).astype(np.float32))
+    ad = tmp_path / "adapter"
+    ad.mkdir()
+    L.write_safetensors(str(ad / "adapter_model.safetensors"), {
+        "base_model.model.model.layers.0.self_attn.q_proj.lora_A.weight": ("BF16", A.f32_to_bf16_bits(a)),
+        "base_model.model.model.layers.0.self_attn.q_proj.lora_B.weight": ("BF16", A.f32_to_bf16_bits(b)),
+        "base_model.model.model.layers.0.mlp.up_proj.lora_A.weight": ("BF16", A.f32_to_bf16_bits(a)),
+    })
+    (ad / "adapter_config.json").write_text(json.dumps({"r": r, "lora_alpha": 8, "target_modules": ["q_proj"]}))
+    mods = L.load_lora_adapter(str(ad), r, 8.0, ["q_proj"], ck, cfg)
+    assert list(mods) == [prefix] and mods[prefix].scale == 2.0
+    lin = L.load_linear(ck, cfg, prefix)
+    x = A.make_activations(2, k, seed=4)
+    y = lin.forward_lora(dev_x(x), mods[prefix])
+    torch.cuda.synchronize()
+    want = A.lora_ops(x, a, b, 2.0, C.qmm_f64(x, *tri).astype(np.float32), bf16=True)
+    ok, worst = check_bf16_two_roundings(host_bits(y), want.astype(np.float64))
+    assert ok, worst
+    with pytest.raises(gpu_lib.Gemma4Error):  # wrong rank: shape mismatch
+        L.load_lora_adapter(str(ad), r + 1, 8.0, ["q_proj"], ck, cfg)
+    lin.close()
+    mods[prefix].close()

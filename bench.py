@@ -288,6 +288,96 @@ def summarize_profiles(stats_dir: str, fetch_dir: str, write_dir: str, line_file
     print(json.dumps(traffic))
 
 
+def model_run(torch, Q, decode_steps: int = 128, prefill_tokens: int = 16384, chunk: int = 2048,
+              layers: int = 48) -> dict:
+    """The 48-layer Gemma-style 12B decoder's quantized matmuls (the other ops of the
+    model are not run): 16K-token chunked prefill (M = 2048 chunks) then 128 decode
+    steps at M = 1, each layer as qkv, o, the gate|up GeGLU pair and down, then the
+    greedy lm_head on the last position.  Weights are random 4-bit codes with bf16
+    scales and biases of a N(0, 0.02) weight's size, generated on the device (6.6 GB,
+    far beyond the 256 MiB Infinity Cache), activations N(0, 1).  Timed with events
+    around the launches only."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEED_BASE + 5)
+
+    def triple(n, k):
+        w = torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32, device="cuda", generator=g)
+        s = (torch.rand((n, k // 64), device="cuda", generator=g) * 0.003 + 0.002).bfloat16()
+        b = (torch.rand((n, k // 64), device="cuda", generator=g) * -0.02 - 0.01).bfloat16()
+        return w, s, b
+
+    net = []
+    for _ in range(layers):
+        net.append({"qkv": Q.QuantizedLinear(*triple(8192, HIDDEN)), "o": Q.QuantizedLinear(*triple(HIDDEN, 4096)),
+                    "mlp": Q.QuantizedGeGLU(triple(15360, HIDDEN), triple(15360, HIDDEN)),
+                    "down": Q.QuantizedLinear(*triple(HIDDEN, 15360))})
+    lm = Q.QuantizedLinear(*triple(262144, HIDDEN))
+    torch.cuda.synchronize()
+    # each projection's input and output, contiguous [chunk, width]; a pass over M rows
+    # uses the first M rows of each
+    xin = {k: torch.randn((chunk, k), device="cuda", generator=g).bfloat16() for k in (HIDDEN, 4096, 15360)}
+    yout = {n: torch.empty((chunk, n), device="cuda", dtype=torch.bfloat16) for n in (8192, HIDDEN, 15360)}
+
+    def step(m):
+        for L in net:
+            L["qkv"].forward(xin[HIDDEN][:m], out=yout[8192][:m])
+            L["o"].forward(xin[4096][:m], out=yout[HIDDEN][:m])
+            L["mlp"].forward(xin[HIDDEN][:m], out=yout[15360][:m])
+            L["down"].forward(xin[15360][:m], out=yout[HIDDEN][:m])
+
+    step(chunk)
+    step(1)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # prefill: 8 chunks of 2048 through every layer, then the head on the last row
+    e0.record()
+    for _ in range(prefill_tokens // chunk):
+        step(chunk)
+    lm.forward_greedy(xin[HIDDEN][:1], softcap=30.0)
+    e1.record()
+    torch.cuda.synchronize()
+    prefill_ms = e0.elapsed_time(e1)
+    # decode: a graph of one token (every layer + the greedy head), replayed
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        step(1)
+        lm.forward_greedy(xin[HIDDEN][:1], softcap=30.0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step(1)
+        lm.forward_greedy(xin[HIDDEN][:1], softcap=30.0)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(decode_steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    decode_ms = e0.elapsed_time(e1) / decode_steps
+    del graph
+    layer_w = sum(n * k // 2 + 4 * n * (k // 64) for _, n, k in LAYER)
+    lm_w = 262144 * HIDDEN // 2 + 4 * 262144 * (HIDDEN // 64)
+    step_bytes = layers * sum(algo_bytes(1, n, k) for _, n, k in LAYER) + algo_bytes(1, 262144, HIDDEN)
+    prefill_flops = layers * sum(algo_flops(prefill_tokens, n, k) for _, n, k in LAYER) + algo_flops(1, 262144, HIDDEN)
+    for L in net:
+        for h in L.values():
+            h.close()
+    lm.close()
+    return {
+        "workload": f"{layers}-layer Gemma-style 12B decoder, quantized matmuls only: {prefill_tokens}-token prefill "
+                    f"in chunks of {chunk}, then {decode_steps} decode steps (each layer qkv, o, gate|up GeGLU pair, "
+                    "down; greedy lm_head with softcap)",
+        "weights_bytes": layers * layer_w + lm_w,
+        "decode_ms_per_token": round(decode_ms, 4),
+        "decode_tokens_per_s": round(1e3 / decode_ms, 1),
+        "decode_GBps": round(step_bytes / (decode_ms * 1e-3) / 1e9, 1),
+        "prefill_ms": round(prefill_ms, 2),
+        "prefill_TFLOPS": round(prefill_flops / (prefill_ms * 1e-3) / 1e12, 1),
+        "prefill_tokens_per_s": round(prefill_tokens / (prefill_ms * 1e-3), 1),
+    }
+
+
 def cpu_baseline(host, target_s: float = 12.0) -> dict:
     """The oracle's fp32 qmm loop (OpenMP over rows) on this host's cores, on a
     bounded sample: whole decoder-layer steps at M=1, repeated until ~target_s."""
@@ -508,6 +598,14 @@ def main() -> int:
                      "roofline_frac_of_copy": round(gu_gbs / cg, 4),
                      "gemm_frac_of_dense": round(head["TFLOPS"] / dense, 4)}
 
+    model = None
+    if not args.quick:
+        log("48-layer decoder: 16K prefill + 128 decode steps (quantized matmuls only)")
+        try:
+            model = model_run(torch, Q)
+        except Exception as e:  # memory or build problems should not hide the headline
+            model = {"error": str(e)}
+
     cpu = None
     if not args.no_cpu:
         log("CPU baseline")
@@ -540,6 +638,7 @@ def main() -> int:
         "decode_per_projection": per_proj,
         "lm_head": lm,
         "prefill_gemm": gemm,
+        "model_48_layers": model,
         "practical_peaks": peaks,
     }
     print(json.dumps(out), flush=True)

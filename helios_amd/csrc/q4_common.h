@@ -153,7 +153,7 @@ __device__ __forceinline__ float round_bf16(float v) { return (float)(__bf16)v; 
 // plain operators).  g^3 is g*g*g: exact in fp32 for a bf16 g (at most 24
 // significant bits), and within an ulp of the reference's pow(g, 3) for an fp32 g.
 // gelu of a bf16 g in the bf16 op sequence: a function of g's 16 bits only, so the
-// GEMM epilogue reads it from a 65536-entry table built by this same code.
+// GEMM epilogue reads it from a table built by this same code (see kGeluTable).
 __device__ __forceinline__ float gelu_bf16(float g) {
 #pragma clang fp contract(off)
     const float c_tanh = 0.796875f;           // bf16(0.7978845608028654)
@@ -169,10 +169,38 @@ __device__ __forceinline__ float geglu_bf16(float gate, float up) {
     return round_bf16(gelu_bf16(round_bf16(gate)) * round_bf16(up));
 }
 
-// The same from the table of gelu_bf16 over all bf16 bit patterns.
-__device__ __forceinline__ float geglu_bf16_table(const uint16_t* __restrict__ table, float gate, float up) {
+// gelu_bf16 over all 65536 bf16 patterns needs a table only for biased exponents
+// 118..128 (|g| in [2^-9, 4)): below, 1 + t rounds to 1 and gelu = bf16(0.5 g);
+// above, 1 + t is 2 (g > 0: gelu = g) or 0 (g < 0: gelu = -0); +inf gives +inf,
+// -inf and NaN give NaN.  (Checked against the op sequence for every pattern.)
+constexpr int kGeluExpLo = 118;
+constexpr int kGeluExps = 11;
+constexpr int kGeluTable = 2 * kGeluExps * 128;  // entries [sign][exponent - 118][mantissa]
+
+// bf16 pattern of table entry i
+__host__ __device__ constexpr uint32_t gelu_table_pattern(int i) {
+    return ((uint32_t)(i / (kGeluExps * 128)) << 15) | ((uint32_t)(kGeluExpLo + (i / 128) % kGeluExps) << 7) |
+           (uint32_t)(i % 128);
+}
+
+// GeGLU from the table (kGeluTable bf16 values, e.g. staged in LDS) and the closed forms
+__device__ __forceinline__ float geglu_bf16_table(const uint16_t* table, float gate, float up) {
 #pragma clang fp contract(off)
-    const float gelu = __uint_as_float((uint32_t)table[f32_to_bf16(gate)] << 16);
+    const uint32_t b = f32_to_bf16(gate);
+    const float g = __uint_as_float(b << 16);
+    const uint32_t e = (b >> 7) & 0xFFu, neg = b >> 15, man = b & 0x7Fu;
+    const int idx = (int)((neg * kGeluExps + (e - kGeluExpLo)) * 128u + man);
+    const bool in_table = e >= (uint32_t)kGeluExpLo && e < (uint32_t)(kGeluExpLo + kGeluExps);
+    const float looked = __uint_as_float((uint32_t)table[in_table ? idx : 0] << 16);
+    float gelu;
+    if (in_table)
+        gelu = looked;
+    else if (e < (uint32_t)kGeluExpLo)
+        gelu = round_bf16(0.5f * g);
+    else if (e < 255u)
+        gelu = neg ? -0.0f : g;
+    else
+        gelu = (man == 0 && !neg) ? g : __uint_as_float(0xFFC00000u);
     return round_bf16(gelu * round_bf16(up));
 }
 

@@ -370,6 +370,18 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     // store takes its lane coordinates afresh (mbcnt), so nothing lane-dependent of
     // its own stays live across the main loop (which runs at the 256-VGPR limit).
     const int slane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+
+    // bf16 GeGLU: the gelu table (5.5 KiB) into the x ring's first slot, free now
+    const uint16_t* gtab = reinterpret_cast<const uint16_t*>(g_xs0);
+    if constexpr (OUT == kOutGegluBf16) {
+        constexpr int kTabChunks = kGeluTable * 2 / 16;
+        static_assert(kTabChunks <= 64 * kWaves && kTabChunks <= kXChunks, "one 16-byte chunk per thread");
+        wait_lds();  // this wave's operand reads have returned
+        lds_barrier();
+        const int t = wave * 64 + slane;
+        if (t < kTabChunks) g_xs0[t] = reinterpret_cast<const uint4*>(gelu_table)[t];
+        __syncthreads();
+    }
 #pragma unroll
     for (int i = 0; i < kMT; ++i) {
 #pragma unroll
@@ -377,9 +389,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
             const int rb = rbw + wn * kNT + j;
             if constexpr (OUT == kOutGegluBf16) {  // rows e and e + 1 share one GeGLU pass
                 // all values first, stores after the loop: with no store between them
-                // the table reads are issued together rather than waited for one by one
-                acc[i][j][0] = geglu2(OUT, slane & 15, acc[i][j][0], acc[i][j][1], gelu_table);
-                acc[i][j][2] = geglu2(OUT, slane & 15, acc[i][j][2], acc[i][j][3], gelu_table);
+                // the LDS table reads are issued together rather than waited for one by one
+                acc[i][j][0] = geglu2(OUT, slane & 15, acc[i][j][0], acc[i][j][1], gtab);
+                acc[i][j][2] = geglu2(OUT, slane & 15, acc[i][j][2], acc[i][j][3], gtab);
                 continue;
             }
             if constexpr (OUT == kOutGegluF32) {  // no memory reads: value and store together
@@ -388,7 +400,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
                 const int hn = geglu2_col(c, rb);
 #pragma unroll
                 for (int e = 0; e < 4; e += 2) {
-                    const float h = geglu2(OUT, c, acc[i][j][e], acc[i][j][e + 1], gelu_table);
+                    const float h = geglu2(OUT, c, acc[i][j][e], acc[i][j][e + 1], gtab);
                     const int mr = geglu2_row(c, m + e, m + e + 1);
                     if (mr < m_rows && hn < n_out) static_cast<float*>(y)[(long)mr * n_out + hn] = h;
                 }
@@ -478,10 +490,10 @@ __global__ void split_reduce_kernel(const float* __restrict__ part, void* __rest
     }
 }
 
-// gelu_bf16 of every bf16 bit pattern (the table the bf16 GeGLU epilogue reads)
+// gelu_bf16 of the table's bf16 patterns (the table the bf16 GeGLU epilogue reads)
 __global__ void gelu_table_kernel(uint16_t* __restrict__ table) {
-    const int b = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-    if (b < 65536) table[b] = f32_to_bf16(gelu_bf16(__uint_as_float((uint32_t)b << 16)));
+    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < kGeluTable) table[i] = f32_to_bf16(gelu_bf16(__uint_as_float(gelu_table_pattern(i) << 16)));
 }
 
 // h = GeGLU of the summed gate|up partial planes, in split order (deterministic).  One
@@ -543,7 +555,7 @@ size_t gemm_workspace_bytes(int m, const Layout& l) {
 }
 
 hipError_t launch_gelu_table(uint16_t* table, hipStream_t stream) {
-    hipLaunchKernelGGL(gelu_table_kernel, dim3(256), dim3(256), 0, stream, table);
+    hipLaunchKernelGGL(gelu_table_kernel, dim3((kGeluTable + 255) / 256), dim3(256), 0, stream, table);
     return hipGetLastError();
 }
 

@@ -88,13 +88,14 @@ size_t gemm_workspace_bytes(int m, const Layout& l);
 
 // Compute units of the current device (cached per device).
 int device_cus();
-// gelu_table: 65536 bf16 values from launch_gelu_table, read by the bf16 GeGLU
-// epilogue (out_mode 2); may be null for the other modes.
+// gelu_table: kGeluTable bf16 values (q4_common.h) from launch_gelu_table, staged in
+// LDS by the bf16 GeGLU epilogue (out_mode 2); may be null for the other modes.
 hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, int out_mode,
                        int n_out, const Layout& l, void* workspace, const uint16_t* gelu_table,
                        hipStream_t stream);
 
-// Fills table[65536] with gelu of every bf16 bit pattern, in the bf16 op sequence.
+// Fills table[kGeluTable] with gelu of the bf16 patterns that need a table, in the
+// bf16 op sequence.
 hipError_t launch_gelu_table(uint16_t* table, hipStream_t stream);
 
 // LoRA delta added in place to a projection output y [m, n] (bf16 or fp32) already

@@ -70,7 +70,7 @@ hipError_t scratch_pool(int device, hipMemPool_t* out) {
     return hipSuccess;
 }
 
-// The bf16 GeGLU epilogue's table of gelu over all bf16 patterns (128 KiB), built
+// The bf16 GeGLU epilogue's table of gelu over bf16 patterns (5.5 KiB), built
 // once per device when its first gate|up pair is created (create synchronizes, so
 // every later forward, on any stream, sees it complete).  Kept until the process ends.
 std::mutex g_table_mu;
@@ -81,7 +81,7 @@ hipError_t gelu_table(int device, const uint16_t** out) {
     std::lock_guard<std::mutex> lock(g_table_mu);
     if (g_gelu_tables[device] == nullptr) {
         uint16_t* t = nullptr;
-        hipError_t e = hipMalloc(&t, 65536 * sizeof(uint16_t));
+        hipError_t e = hipMalloc(&t, q4::kGeluTable * sizeof(uint16_t));
         if (e != hipSuccess) return e;
         e = q4::launch_gelu_table(t, nullptr);
         if (e == hipSuccess) e = hipStreamSynchronize(nullptr);

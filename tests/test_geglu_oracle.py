@@ -8,7 +8,10 @@ projection (native_model.cc:378-386), pinned without the reference:
 * in bf16, every one of the 65536 bf16 gate values stays within the error the
   per-op bf16 roundings allow of the float64 formula (a dropped or altered term
   fails somewhere over that range), and a hand-derived value pins the op order and
-  the round-half-to-even inside it.
+  the round-half-to-even inside it;
+* the prefill epilogue's compact gelu table (q4_common.h kGeluTable: entries only
+  for biased exponents 118..128, closed forms elsewhere) reproduces the op sequence
+  for every bf16 pattern, infinities and NaN included.
 """
 
 import numpy as np
@@ -81,3 +84,32 @@ def test_bf16_hand_derived_value():
     #   (without rounding 1 + t first it would be 1.3984375)
     assert float(A.geglu_ops(np.float32(1.5), np.float32(1.0), bf16=True).reshape(-1)[0]) == 1.390625
     assert abs(np.tanh(1.3125) - 0.864907) < 1e-6
+
+
+def test_compact_gelu_table_covers_every_pattern():
+    import warnings
+
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    g = A.bf16_bits_to_f32(bits.astype(np.uint16))
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        want = A.f32_to_bf16_bits(A.geglu_ops(g, np.ones_like(g), bf16=True))
+        e, neg, man = (bits >> 7) & 0xFF, bits >> 15, bits & 0x7F
+        lo, n_exp = 118, 11
+        idx = np.arange(2 * n_exp * 128)
+        pat = ((idx // (n_exp * 128)) << 15) | ((lo + (idx // 128) % n_exp) << 7) | (idx % 128)
+        table = A.f32_to_bf16_bits(A.geglu_ops(A.bf16_bits_to_f32(pat.astype(np.uint16)), np.ones(idx.size, np.float32),
+                                               bf16=True))
+        got = np.empty_like(want)
+        tab = (e >= lo) & (e < lo + n_exp)
+        got[tab] = table[((neg * n_exp + (e - lo)) * 128 + man)[tab]]
+        small = e < lo
+        got[small] = A.f32_to_bf16_bits(A.round_to_bf16(np.float32(0.5) * g[small]))
+        big = (e >= lo + n_exp) & (e < 255)
+        got[big & (neg == 0)] = bits[big & (neg == 0)]
+        got[big & (neg == 1)] = 0x8000
+        spec = e == 255
+        got[spec] = np.where((man[spec] == 0) & (neg[spec] == 0), bits[spec], 0xFFC0)
+    nan = np.isnan(A.bf16_bits_to_f32(want))
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.all(np.isnan(A.bf16_bits_to_f32(got[nan])))

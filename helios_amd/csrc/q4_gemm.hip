@@ -132,7 +132,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     tile_of((int)blockIdx.x, (int)gridDim.x, mtiles, ntiles, mt, nt);
     // split of K: groups [g_begin, g_end), whole octets; with several splits each
     // writes fp32 partial sums to its own [M, N] plane of y
-    const int g_begin = (int)blockIdx.y * g_split;
+    // (g_split is a whole number of octets; masked so the compiler knows g_begin % 8 == 0
+    // and with it the parity of every step below: no run-time selects or branches there)
+    const int g_begin = (int)blockIdx.y * (g_split & ~7);
     const int g_end = groups - g_begin < g_split ? groups : g_begin + g_split;
     const int p_end = (g_end + 1) >> 1;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -227,39 +229,50 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         int ln = threadIdx.x & 63;
         asm volatile("" : "+v"(ln));
         const int lcol = ln & 15, lkq = ln >> 4;
-        bf16x8 bq[kNT][2];
-        float s16[kNT];
         const uint2* sbl = reinterpret_cast<const uint2*>(wp + kWPair);
+        uint2 tw[kNT];      // this group's two tiled words of each row block
+        uint32_t swv[kNT];  // and its scale/bias word
 #pragma unroll
         for (int j = 0; j < kNT; ++j) {
             const int rbl = wn * kNT + j;
-            const uint4 t = wp[rbl * 64 + ln];
-            bq[j][0] = expand_word(gpar ? t.z : t.x);
-            bq[j][1] = expand_word(gpar ? t.w : t.y);
-            const uint2 sw = sbl[rbl * 16 + lcol];
-            s16[j] = bf16_lo(gpar ? sw.y : sw.x) * 16.0f;
+            tw[j] = reinterpret_cast<const uint2*>(wp + rbl * 64 + ln)[gpar];
+            swv[j] = reinterpret_cast<const uint32_t*>(sbl + rbl * 16 + lcol)[gpar];
         }
         auto a_frag = [&](int i, int h) {
             const int r = wm * kWM + 16 * i + lcol;
             return __builtin_bit_cast(bf16x8, xs[r * 8 + ((4 * h + lkq) ^ ((r >> 1) & 7))]);
         };
-        // the wave's 32 tiles in one stream, software-pipelined: tile t's two products
-        // are issued, then tile t-2's scale FMAs, which do not wait for them, so the
-        // matrix core and the VALU work at the same time
+        // The wave's 32 tiles in one stream, software-pipelined and kept in this order
+        // (a scheduling fence after each tile): tile t's two products, then tile t-3's
+        // scale FMAs, which do not wait for them; row 0 expands each row block's words
+        // just before its first products, and the next row's A operands are read one
+        // row ahead.  Left to itself the compiler expands all words first and then
+        // issues long runs of products with no VALU work beside them.
         constexpr int kTiles = kMT * kNT;
-        constexpr int kLag = 2;
+        constexpr int kLag = 3;
+        bf16x8 bq[kNT][2];
+        float s16[kNT];
         f32x4 p[kLag + 1];
-        bf16x8 a0, a1;
+        bf16x8 a0 = a_frag(0, 0), a1 = a_frag(0, 1), n0, n1;
 #pragma unroll
         for (int t = 0; t < kTiles + kLag; ++t) {
             if (t < kTiles) {
                 const int i = t / kNT, j = t % kNT;
-                if (j == 0) {
-                    a0 = a_frag(i, 0);
-                    a1 = a_frag(i, 1);
+                if (i == 0) {
+                    bq[j][0] = expand_word(tw[j].x);
+                    bq[j][1] = expand_word(tw[j].y);
+                    s16[j] = bf16_lo(swv[j]) * 16.0f;
+                }
+                if (j == 0 && i + 1 < kMT) {
+                    n0 = a_frag(i + 1, 0);
+                    n1 = a_frag(i + 1, 1);
                 }
                 p[t % (kLag + 1)] = mfma16x16x32(a0, bq[j][0], zero);
                 p[t % (kLag + 1)] = mfma16x16x32(a1, bq[j][1], p[t % (kLag + 1)]);
+                if (j == kNT - 1) {
+                    a0 = n0;
+                    a1 = n1;
+                }
                 hook(t);
             }
             if (t >= kLag) {
@@ -269,6 +282,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
                 for (int e = 0; e < 4; ++e)
                     acc[i][j][e] = __builtin_fmaf(s16[j], p[u % (kLag + 1)][e], acc[i][j][e]);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
     // bias term of the octet: A operands and scale/bias words from g_xab
@@ -314,11 +328,13 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         lds_barrier();
         if ((g & 7) == 0 && g > g_begin) bias();
         if (issues_xa(g)) dma_xa(g >> 3);
+        // the pair's scale words (waves 0, 1), issued here rather than inside the
+        // product stream, which then has no branch
+        if ((g & 1) == 0 && wave < 2) dma_s((g + 2) >> 1, wp2);
         const bool pair = (g & 1) == 0;
         compute(xs, wp, g & 1, [&](int t) {
             if (t == 1 || t == 3 || t == 5 || t == 7) dma_x(g + 2, t >> 1, xs2);
             if (pair && (t == 9 || t == 11)) dma_w((g + 2) >> 1, (t - 9) >> 1, wp2);
-            if (pair && t == 13 && wave < 2) dma_s((g + 2) >> 1, wp2);
         });
     };
 

@@ -22,7 +22,7 @@ namespace {
 // row i of an MFMA result depends only on row i of its A operand, so A rows >= M
 // may hold anything: they only feed accumulator rows that are never stored.
 //
-// XLDS = true (M <= 4, x small): the workgroup first copies x[M,K] into LDS with
+// XLDS = true (x[M,K] up to 64 KiB): the workgroup first copies x into LDS with
 // one cooperative wave of loads issued before the weight loads, so the x operands
 // cost LDS reads instead of a chain of L2 round trips.  XLDS = false (M up to 16):
 // each wave reads its x operands from global memory, one group pair ahead.
@@ -529,6 +529,15 @@ constexpr int kRowsMinBlocks = 768;
 constexpr int kRowsMaxBlocks = 4096;
 constexpr int kRowsWaves = 4;
 constexpr int kRowsPerCu = 2;
+// one workgroup per row block with x staged in LDS (decode_kernel<MT, 4, true>, 8
+// waves of 4 pairs, one pass): for K of at most 32 pairs and up to this many row
+// blocks (twice as many for M > 1) it is ahead of the streaming kernel at every M
+// (0.5-0.8 us at M = 1, 1-3 us at M = 8 for q/k/v/o and their fused qkv, 1.2 us for
+// gate at M = 4 and 8); it is behind for the gate|up pair, the lm_head, down (K of
+// 120 pairs) and gate at M = 1 (the row kernel's case).
+constexpr int kXLdsMaxPairs = 32;
+constexpr int kXLdsMaxBlocks = 512;
+constexpr size_t kXLdsMaxBytes = 64 * 1024;
 
 
 template <int MT>
@@ -548,6 +557,13 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
                                tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb);
             return hipGetLastError();
         }
+    }
+    const size_t x_bytes = (size_t)m * l.k * 2;
+    if (l.gp <= kXLdsMaxPairs && x_bytes <= kXLdsMaxBytes && l.nb <= kXLdsMaxBlocks * (MT > 1 ? 2 : 1)) {
+        const int waves = (l.gp + GPW - 1) / GPW;  // <= 8, each wave one pass of <= 4 pairs
+        hipLaunchKernelGGL((decode_kernel<MT, GPW, true>), dim3(l.nb), dim3(64 * waves), x_bytes, stream, tiles, sb,
+                           x, op, m, l.n, l.k, l.gp, waves);
+        return hipGetLastError();
     }
     if (lds_bytes + static_lds <= kLdsPerCu) {
         // persistent streaming kernel: 4 pairs per chunk, up to 8 waves per workgroup

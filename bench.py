@@ -136,6 +136,14 @@ def graph_ms(torch, fn, replays: int, warmup: int) -> float:
     return ms
 
 
+def graph_ms_steady(torch, fn, settle_ms: float = 50.0, time_ms: float = 20.0) -> float:
+    """graph_ms for the per-shape sweeps: the clock ramps for a few milliseconds once
+    the GPU gets busy, so replays run untimed for about settle_ms first and the timed
+    replays cover about time_ms (both from a first estimate of one replay)."""
+    est = max(graph_ms(torch, fn, replays=3, warmup=1), 1e-3)
+    return graph_ms(torch, fn, replays=max(10, int(time_ms / est) + 1), warmup=max(2, int(settle_ms / est) + 1))
+
+
 def kernel_us(torch, make, m: int, k: int, n: int, xdev, wbytes: int, reps_per_graph: int = 40) -> float:
     """Average duration of one forward launch (of make(), output [m, n]): back-to-back
     launches over rotated weight copies, captured in a graph and replayed."""
@@ -148,7 +156,7 @@ def kernel_us(torch, make, m: int, k: int, n: int, xdev, wbytes: int, reps_per_g
         for i in range(launches):
             lins[i % copies].forward(xdev[:m], out=y)
 
-    ms = graph_ms(torch, fn, replays=10, warmup=2)
+    ms = graph_ms_steady(torch, fn)
     for lin in lins:
         lin.close()
     return ms * 1e3 / launches
@@ -425,8 +433,8 @@ def cpu_baseline(host, target_s: float = 12.0) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (skip the per-shape sweeps)")
@@ -572,7 +580,7 @@ def main() -> int:
             for name, n, k in shapes:
                 ym = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
                 lin = Q.QuantizedLinear(*host[name])
-                ms = graph_ms(torch, lambda: lin.forward(xk[k], out=ym), replays=10, warmup=2)
+                ms = graph_ms_steady(torch, lambda: lin.forward(xk[k], out=ym))
                 lin.close()
                 tflops = algo_flops(m, n, k) / (ms * 1e-3) / 1e12
                 gemm[f"{name}_m{m}"] = {"us": round(ms * 1e3, 1), "TFLOPS": round(tflops, 1),
@@ -581,7 +589,7 @@ def main() -> int:
             if not args.quick:  # the GeGLU pair: gate and up in one GEMM, h = geglu(gate, up)
                 hm = torch.empty((m, f_gu), dtype=torch.bfloat16, device="cuda")
                 pair = Q.QuantizedGeGLU(host["gate_proj"], host["up_proj"])
-                ms = graph_ms(torch, lambda: pair.forward(xk[k_gu], out=hm), replays=10, warmup=2)
+                ms = graph_ms_steady(torch, lambda: pair.forward(xk[k_gu], out=hm))
                 pair.close()
                 tflops = algo_flops(m, 2 * f_gu, k_gu) / (ms * 1e-3) / 1e12
                 gemm[f"{PAIR}_m{m}"] = {"us": round(ms * 1e3, 1), "TFLOPS": round(tflops, 1),

@@ -1,7 +1,7 @@
 """CPU oracle for MLX-format affine quantized matmul — TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg
-import this module, and only as the checker.  The product path
+import this module, and only to check results.  The product path
 (``helios_amd``) never does.
 
 numpy restatement of what the reference reaches through
@@ -149,7 +149,7 @@ def qmm_f64(x_bits, wq, scales, biases, group_size: int = GROUP_SIZE, bits: int 
 
 
 # ---------------------------------------------------------------------------
-# tolerance checks (applied beyond the output format's own rounding)
+# tolerance checks (the acceptance bounds, applied beyond the output format's own rounding)
 # ---------------------------------------------------------------------------
 
 def check_bf16_output(y_bits, y_exact, rel: float = 1e-2):

@@ -1,6 +1,6 @@
 """ctypes binding of the C oracle (oracle/q4_oracle.c) — TEST INFRASTRUCTURE ONLY.
 
-The C restatement is the fast checker for full-size shapes and the CPU baseline
+The C restatement is the fast reference for full-size shapes and the CPU baseline
 the benchmark times; it is cross-checked against the numpy restatement in
 tests/test_oracle.py.
 """

@@ -142,6 +142,18 @@ struct OutParams {
     float cap;                 // greedy modes: the softcap (0: none)
 };
 
+// Output parameters of the 16-row slab `slab` of a launch: y (or h, or the logits)
+// and the greedy keys advance by 16 rows.  Decode kernels launched over M > 16 rows
+// take their slab from blockIdx.y.
+__device__ __forceinline__ OutParams slab_params(OutParams op, int slab, int n_rows) {
+    const bool geglu = op.mode == kOutGegluBf16 || op.mode == kOutGegluF32;
+    const bool f32 = op.mode == kOutF32 || op.mode == kOutGegluF32 || op.mode == kOutGreedyF32;
+    const long row0 = 16L * slab;
+    if (op.y != nullptr) op.y = static_cast<char*>(op.y) + row0 * (geglu ? op.n_out : n_rows) * (f32 ? 4 : 2);
+    if (op.part != nullptr) op.part += row0 * op.nb;
+    return op;
+}
+
 __device__ __forceinline__ float round_bf16(float v) { return (float)(__bf16)v; }
 
 // GeGLU of native_model.cc:378-386, op by op as the reference's array ops evaluate

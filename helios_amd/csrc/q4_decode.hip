@@ -33,10 +33,15 @@ namespace {
 // as zero without branches; zero tiles with zero scale/bias add nothing.
 template <int MT, int GPW, bool XLDS>
 __global__ __launch_bounds__(1024) void decode_kernel(
-    const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x,
-    OutParams op, int m_rows, int n_rows, int k, int gpairs, int waves) {
+    const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x_in,
+    OutParams op_in, int m_total, int n_rows, int k, int gpairs, int waves) {
     constexpr int R = MT < 4 ? MT : 4;
     extern __shared__ uint4 xs_lds[];  // XLDS: x[M][K] as bf16, 16 B per entry
+    // this workgroup's 16-row slab (blockIdx.y) of the launch's m_total rows
+    const int slab = (int)blockIdx.y;
+    const int m_rows = m_total - 16 * slab < 16 ? m_total - 16 * slab : 16;
+    const uint16_t* __restrict__ x = x_in + (size_t)slab * 16 * k;
+    const OutParams op = slab_params(op_in, slab, n_rows);
     const int rb = blockIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -178,11 +183,16 @@ __device__ __forceinline__ uint32_t scale_word(uint2 sv, int pair, int gi, int c
 // Per row block the waves meet once in LDS (ping-pong buffers, one barrier).
 template <int MT, int GPW>
 __global__ __launch_bounds__(512) void decode_stream_kernel(
-    const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x,
-    OutParams op, int m_rows, int n_rows, int k, int gpairs, int nblocks, int waves) {
+    const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x_in,
+    OutParams op_in, int m_total, int n_rows, int k, int gpairs, int nblocks, int waves) {
     constexpr int R = MT < 4 ? MT : 4;
     constexpr int kPad = GPW * 128;  // zero columns after each x row
     extern __shared__ uint4 lds[];
+    // this workgroup's 16-row slab (blockIdx.y) of the launch's m_total rows
+    const int slab = (int)blockIdx.y;
+    const int m_rows = m_total - 16 * slab < 16 ? m_total - 16 * slab : 16;
+    const uint16_t* __restrict__ x = x_in + (size_t)slab * 16 * k;
+    const OutParams op = slab_params(op_in, slab, n_rows);
     // layout: x rows [m_rows][k + kPad] bf16, then -X table [2*(gpairs+GPW)][16] fp32
     __shared__ float red[2][8][R * 64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -540,13 +550,18 @@ constexpr int kXLdsMaxBlocks = 512;
 constexpr size_t kXLdsMaxBytes = 64 * 1024;
 
 
+// One launch over all m rows: slabs of 16 rows along the grid's y dimension (the
+// workgroups of one row block in different slabs run close together, so the weights
+// come from HBM about once).  MT = 16 whenever m > 16.
 template <int MT>
 hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, const OutParams& op, int m,
                      const Layout& l, hipStream_t stream) {
     constexpr int GPW = 4;
     constexpr int R = MT < 4 ? MT : 4;
+    const int ms = m < 16 ? m : 16;  // rows per slab
+    const unsigned slabs = (unsigned)((m + 15) / 16);
     const size_t static_lds = 2 * 8 * R * 64 * sizeof(float);
-    const size_t lds_bytes = (size_t)m * (l.k + GPW * 128) * 2 + (size_t)(l.gp + GPW) * 2 * 16 * 4;
+    const size_t lds_bytes = (size_t)ms * (l.k + GPW * 128) * 2 + (size_t)(l.gp + GPW) * 2 * 16 * 4;
     if constexpr (MT == 1) {
         if (l.nb >= kRowsMinBlocks && l.nb <= kRowsMaxBlocks && lds_bytes <= kLdsPerCu && op.mode < kOutGreedyBf16) {
             // many row blocks: one wave per block, no cross-wave reduction
@@ -558,11 +573,11 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
             return hipGetLastError();
         }
     }
-    const size_t x_bytes = (size_t)m * l.k * 2;
+    const size_t x_bytes = (size_t)ms * l.k * 2;
     if (l.gp <= kXLdsMaxPairs && x_bytes <= kXLdsMaxBytes && l.nb <= kXLdsMaxBlocks * (MT > 1 ? 2 : 1)) {
         const int waves = (l.gp + GPW - 1) / GPW;  // <= 8, each wave one pass of <= 4 pairs
-        hipLaunchKernelGGL((decode_kernel<MT, GPW, true>), dim3(l.nb), dim3(64 * waves), x_bytes, stream, tiles, sb,
-                           x, op, m, l.n, l.k, l.gp, waves);
+        hipLaunchKernelGGL((decode_kernel<MT, GPW, true>), dim3(l.nb, slabs), dim3(64 * waves), x_bytes, stream, tiles,
+                           sb, x, op, m, l.n, l.k, l.gp, waves);
         return hipGetLastError();
     }
     if (lds_bytes + static_lds <= kLdsPerCu) {
@@ -576,12 +591,12 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
         const int capacity = device_cus() * per_cu;
         const int per_wg = (l.nb + capacity - 1) / capacity;
         const int grid = (l.nb + per_wg - 1) / per_wg;
-        hipLaunchKernelGGL((decode_stream_kernel<MT, GPW>), dim3(grid), dim3(64 * waves), lds_bytes, stream, tiles,
-                           sb, x, op, m, l.n, l.k, l.gp, l.nb, waves);
+        hipLaunchKernelGGL((decode_stream_kernel<MT, GPW>), dim3(grid, slabs), dim3(64 * waves), lds_bytes, stream,
+                           tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb, waves);
         return hipGetLastError();
     }
     const Split sp = choose_split(l.gp, MT);
-    const dim3 grid(l.nb), block(64 * sp.waves);
+    const dim3 grid(l.nb, slabs), block(64 * sp.waves);
     if (sp.gpw == 6)
         hipLaunchKernelGGL((decode_kernel<MT, 6, false>), grid, block, 0, stream, tiles, sb, x, op, m, l.n, l.k, l.gp, sp.waves);
     else
@@ -605,27 +620,10 @@ int device_cus() {
 
 hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, const OutParams& op, int m,
                          const Layout& l, hipStream_t stream) {
-    const bool f32 = op.mode == kOutF32 || op.mode == kOutGegluF32 || op.mode == kOutGreedyF32;
-    const size_t ysz = f32 ? 4 : 2;
-    const size_t ycols = (op.mode == kOutGegluBf16 || op.mode == kOutGegluF32) ? (size_t)op.n_out : (size_t)l.n;
-    for (int m0 = 0; m0 < m; m0 += 16) {
-        const int mc = (m - m0) < 16 ? (m - m0) : 16;
-        const uint16_t* xs = x + (size_t)m0 * l.k;
-        OutParams slab = op;
-        if (op.y != nullptr) slab.y = static_cast<char*>(op.y) + (size_t)m0 * ycols * ysz;
-        if (op.part != nullptr) slab.part = op.part + (size_t)m0 * op.nb;
-        hipError_t e;
-        if (mc == 1)
-            e = launch_mt<1>(tiles, sb, xs, slab, mc, l, stream);
-        else if (mc == 2)
-            e = launch_mt<2>(tiles, sb, xs, slab, mc, l, stream);
-        else if (mc <= 4)
-            e = launch_mt<4>(tiles, sb, xs, slab, mc, l, stream);
-        else
-            e = launch_mt<16>(tiles, sb, xs, slab, mc, l, stream);
-        if (e != hipSuccess) return e;
-    }
-    return hipSuccess;
+    if (m == 1) return launch_mt<1>(tiles, sb, x, op, m, l, stream);
+    if (m == 2) return launch_mt<2>(tiles, sb, x, op, m, l, stream);
+    if (m <= 4) return launch_mt<4>(tiles, sb, x, op, m, l, stream);
+    return launch_mt<16>(tiles, sb, x, op, m, l, stream);
 }
 
 // argmax over the blocks' best keys: one workgroup per row (deterministic: the max of

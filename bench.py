@@ -477,7 +477,7 @@ def main() -> int:
           for k in {k for _, _, k in LAYER}}
     f_gu, k_gu = step_nk[PAIR]
     gu_bytes = pair_algo_bytes(1, f_gu, k_gu)
-    gu_kernel = f"{DOM_KERNEL}<1,4,3> gate|up GeGLU pair F={f_gu} K={k_gu} M=1"
+    gu_kernel = f"{DOM_KERNEL}<1,4,2> gate|up GeGLU pair F={f_gu} K={k_gu} M=1"
 
     def pair_us(m):
         return kernel_us(torch, maker(PAIR), m, k_gu, f_gu, xs[k_gu], wbytes_of[PAIR])

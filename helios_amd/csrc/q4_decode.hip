@@ -568,7 +568,7 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
             int grid = (l.nb + kRowsWaves - 1) / kRowsWaves;
             const int cap = device_cus() * kRowsPerCu;
             if (grid > cap) grid = cap;
-            hipLaunchKernelGGL((decode_rows_kernel<MT, GPW, 3>), dim3(grid), dim3(64 * kRowsWaves), lds_bytes, stream,
+            hipLaunchKernelGGL((decode_rows_kernel<MT, GPW, 2>), dim3(grid), dim3(64 * kRowsWaves), lds_bytes, stream,
                                tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb);
             return hipGetLastError();
         }

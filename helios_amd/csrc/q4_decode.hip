@@ -466,12 +466,10 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(
             for (int gi = 0; gi < 2; ++gi) {
                 xo[i][gi][0] = __builtin_bit_cast(bf16x8, xp[i * 16 + gi * 8]);
                 xo[i][gi][1] = __builtin_bit_cast(bf16x8, xp[i * 16 + gi * 8 + 4]);
-                if constexpr (R == 1) {
-                    xn[i][gi] = zero;
-                    xn[i][gi][0] = xtab[(gpb + i) * 32 + gi * 16 + 4 * kq];
-                } else {
-                    xn[i][gi] = *reinterpret_cast<const f32x4*>(xtab + (gpb + i) * 32 + gi * 16 + 4 * kq);
-                }
+                // whole 16-byte table entries even at M = 1: rows >= M of the table are
+                // never written, but they only seed accumulator rows that are never
+                // stored, and a full read saves the three moves that zero them
+                xn[i][gi] = *reinterpret_cast<const f32x4*>(xtab + (gpb + i) * 32 + gi * 16 + 4 * kq);
                 sbw[i][gi] = scale_word(sv[b], i, gi, col);
             }
         }

@@ -23,13 +23,11 @@
 namespace q4 {
 namespace {
 
-constexpr int kBM = 256;              // workgroup tile rows (M)
+constexpr int kBM = 256;              // workgroup tile rows (M), the taller of the two tile shapes
 constexpr int kBN = 256;              // workgroup tile columns (N)
 constexpr int kWaves = 8;             // 2 (M) x 4 (N) waves, two per SIMD
 constexpr int kRB = kBN / 16;         // 16-row weight blocks per workgroup tile
-constexpr int kWM = 128;              // wave tile rows
 constexpr int kWN = 64;               // wave tile columns
-constexpr int kMT = kWM / 16;         // 16x16 tiles per wave along M
 constexpr int kNT = kWN / 16;         // 16x16 tiles per wave along N
 constexpr int kXChunks = kBM * 8;     // 16-byte chunks of one x group tile (256 rows x 64 bf16)
 
@@ -121,13 +119,20 @@ __shared__ uint4 g_wp1[kWPair + kSPair];
 __shared__ uint4 g_xab[16 * 64 + kRB * 4 * 16 / 2];
 
 
-template <int OUT>
+template <int OUT, int BM>
 __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ tiles, const uint2* __restrict__ sb,
                                                    const uint16_t* __restrict__ x, const uint4* __restrict__ xaug,
                                                    void* __restrict__ y, int m_rows, int n_rows, int k, int groups,
                                                    int gpairs, int mtiles, int ntiles, int octets, uint32_t tile_bytes,
                                                    uint32_t sb_bytes, int g_split, long split_stride, int n_out,
                                                    const uint16_t* __restrict__ gelu_table) {
+    // BM = 256: 2 x 4 waves of 128 x 64; BM = 128: 2 x 4 waves of 64 x 64 (more
+    // workgroups for small M without splitting K)
+    static_assert(BM == 256 || BM == 128, "tile rows");
+    constexpr int kWM = BM / 2;                   // wave tile rows
+    constexpr int kMT = kWM / 16;                 // 16x16 tiles per wave along M
+    constexpr int kXParts = BM * 8 / (64 * kWaves);  // 16-byte x loads per wave per group
+    constexpr int kXaParts = BM / 128;            // bias A-operand loads per wave per octet
     int mt, nt;
     tile_of((int)blockIdx.x, (int)gridDim.x, mtiles, ntiles, mt, nt);
     // split of K: groups [g_begin, g_end), whole octets; with several splits each
@@ -151,7 +156,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)k * 2u);
     const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles, tile_bytes);
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, sb_bytes);
-    const __amdgpu_buffer_rsrc_t ars = make_rsrc(xaug, (uint32_t)(mtiles * 16 * octets) * 1024u);
+    const __amdgpu_buffer_rsrc_t ars = make_rsrc(xaug, (uint32_t)(mtiles * (BM / 16) * octets) * 1024u);
 
     // DMA issue.  Per lane, the offsets are fixed for the whole K loop (rows past M and
     // row blocks past N at kOutOfRange) and computed once here; the step moves them by
@@ -160,15 +165,15 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     // last group or pair the resource is swapped for an empty one: zeros, into slots
     // nobody reads again.  Branch-free, so they can sit anywhere in the product stream.
     const __amdgpu_buffer_rsrc_t zrs = make_rsrc(x, 0u);
-    uint32_t xv[4];  // x of a group, part u: 16-byte chunk q of the 256 x 64 tile, row r,
-                     // chunk c of the row, stored at position c ^ ((r >> 1) & 7) of its LDS
-                     // row (swizzle: conflict-free MFMA operand reads)
+    uint32_t xv[kXParts];  // x of a group, part u: 16-byte chunk q of the BM x 64 tile, row r,
+                           // chunk c of the row, stored at position c ^ ((r >> 1) & 7) of its
+                           // LDS row (swizzle: conflict-free MFMA operand reads)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kXParts; ++u) {
         const int q = (8 * u + wave) * 64 + lane;
         const int r = q >> 3;
         const int c = (q & 7) ^ ((r >> 1) & 7);
-        const int row = mt * kBM + r;
+        const int row = mt * BM + r;
         xv[u] = row < m_rows ? ((uint32_t)row * (uint32_t)k + (uint32_t)(8 * c)) * 2u : kOutOfRange;
     }
     uint32_t wv[2];  // tiled words of a pair, part t: row block 2w + t, one 16-byte word per lane
@@ -192,17 +197,17 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         dma16(p < p_end ? srs : zrs, wdst + kWPair + 64 * wave, sv, (uint32_t)p * 128u);
     };
     auto dma_xa_part = [&](int o, int u) {
-        const int m16 = 2 * wave + u;
-        dma16(ars, g_xab + m16 * 64, (uint32_t)lane * 16u, (uint32_t)(((mt * 16 + m16) * octets + o) * 1024));
+        const int m16 = kXaParts * wave + u;
+        dma16(ars, g_xab + m16 * 64, (uint32_t)lane * 16u, (uint32_t)(((mt * (BM / 16) + m16) * octets + o) * 1024));
     };
-    // bias operands of octet o: the A side (two 16-byte loads) and the scale/bias words
+    // bias operands of octet o: the A side (kXaParts 16-byte loads) and the scale/bias words
     // of its four group pairs for row blocks 2w, 2w+1 (lane l: row block 2w + l/32,
     // 16-byte chunk l%32 of the row block's 512 contiguous bytes)
     auto dma_xa = [&](int o) {
         int ln = threadIdx.x & 63;
         asm volatile("" : "+v"(ln));
-        dma_xa_part(o, 0);
-        dma_xa_part(o, 1);
+#pragma unroll
+        for (int u = 0; u < kXaParts; ++u) dma_xa_part(o, u);
         const int rb = rbw + 2 * wave + (ln >> 5);
         const int chunk = ln & 31;
         const bool ok = (rb < nblocks) & (4 * o + (chunk >> 3) < gpairs);
@@ -310,14 +315,16 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     // (past the end they read zeros), so the counts are fixed.
     auto issues_xa = [&](int g) { return (g & 7) == 1 && g > g_begin + 1; };
     auto issued = [&](int g) {  // loads this wave issues at step g
-        return 4 + ((g & 1) == 0 ? 2 + (wave < 2 ? 1 : 0) : 0) + (issues_xa(g) ? 3 : 0);
+        return kXParts + ((g & 1) == 0 ? 2 + (wave < 2 ? 1 : 0) : 0) + (issues_xa(g) ? kXaParts + 1 : 0);
     };
     auto step = [&](int g, const uint4* xs, const uint4* wp, uint4* xs2, uint4* wp2) {
         if (g == g_begin) {
             wait_vm_lds<0>();
         } else {
             switch (issued(g - 1)) {
+                case 2: wait_vm_lds<2>(); break;
                 case 4: wait_vm_lds<4>(); break;
+                case 5: wait_vm_lds<5>(); break;
                 case 6: wait_vm_lds<6>(); break;
                 case 7: wait_vm_lds<7>(); break;
                 case 9: wait_vm_lds<9>(); break;
@@ -333,7 +340,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         if ((g & 1) == 0 && wave < 2) dma_s((g + 2) >> 1, wp2);
         const bool pair = (g & 1) == 0;
         compute(xs, wp, g & 1, [&](int t) {
-            if (t == 1 || t == 3 || t == 5 || t == 7) dma_x(g + 2, t >> 1, xs2);
+            if ((t & 1) && (t >> 1) < kXParts) dma_x(g + 2, t >> 1, xs2);
             if (pair && (t == 9 || t == 11)) dma_w((g + 2) >> 1, (t - 9) >> 1, wp2);
         });
     };
@@ -341,7 +348,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     // prologue: x of the split's first two groups, its first pair, bias operands of its
     // first octet
 #pragma unroll
-    for (int part = 0; part < 4; ++part) {
+    for (int part = 0; part < kXParts; ++part) {
         dma_x(g_begin, part, g_xs0);
         dma_x(g_begin + 1, part, g_xs1);
     }
@@ -412,7 +419,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
             }
             if constexpr (OUT == kOutGegluF32) {  // no memory reads: value and store together
                 const int c = slane & 15;
-                const int m = mt * kBM + wm * kWM + 16 * i + 4 * (slane >> 4);
+                const int m = mt * BM + wm * kWM + 16 * i + 4 * (slane >> 4);
                 const int hn = geglu2_col(c, rb);
 #pragma unroll
                 for (int e = 0; e < 4; e += 2) {
@@ -422,7 +429,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
                 }
                 continue;
             }
-            const int m = mt * kBM + wm * kWM + 16 * i + 4 * kq;
+            const int m = mt * BM + wm * kWM + 16 * i + 4 * kq;
             {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -445,7 +452,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         for (int i = 0; i < kMT; ++i) {
 #pragma unroll
             for (int j = 0; j < kNT; ++j) {
-                const int m = mt * kBM + wm * kWM + 16 * i + 4 * (slane >> 4);
+                const int m = mt * BM + wm * kWM + 16 * i + 4 * (slane >> 4);
                 const int hn = geglu2_col(c, rbw + wn * kNT + j);
 #pragma unroll
                 for (int e = 0; e < 4; e += 2) {
@@ -535,32 +542,37 @@ __global__ void split_geglu_kernel(const float* __restrict__ part, void* __restr
 
 }  // namespace
 
-// Split of K over workgroups when the output tiles alone leave CUs idle: the count
-// (whole octets per split) minimises rounds-of-workgroups x octets-per-split, plus
-// the partial sums' extra traffic.
+// Tile shape and split of K.  For each tile height (256 rows, or 128 rows with half
+// the products per group step) and split count (whole octets per split), the cost is
+// rounds-of-workgroups x octets-per-split x the measured step time, plus the partial
+// sums' extra traffic; the cheapest wins.
 GemmPlan plan_gemm(int m, const Layout& l) {
     GemmPlan p;
     const int octets = (l.g + 7) / 8;
-    const long tiles = (long)((m + kBM - 1) / kBM) * ((l.n + kBN - 1) / kBN);
     const long cus = device_cus();
-    const double step_us = 2.0, bytes_per_us = 4.0e6;
-    double best = 0;
-    for (int s = 1; s <= octets && s <= kMaxSplits; ++s) {
-        const int per = (octets + s - 1) / s;
-        const int used = (octets + per - 1) / per;  // splits that get work
-        if (used != s) continue;
-        const size_t part = s > 1 ? (size_t)s * m * l.n * 4 : 0;
-        if (part > kMaxPartialBytes) break;
-        const double rounds = (double)((tiles * s + cus - 1) / cus);
-        const double t = rounds * per * 8 * step_us + (s > 1 ? 3.0 + 2.0 * part / bytes_per_us : 0.0);
-        if (s == 1 || t < best) {
-            best = t;
-            p.splits = s;
-            p.g_split = per * 8;
-            p.part_bytes = part;
+    const double bytes_per_us = 6.0e6;  // partial sums written and read back, largely through the caches
+    double best = -1.0;
+    for (int bm : {256, 128}) {
+        const double step_us = bm == 256 ? 2.0 : 1.15;  // one 64-wide group step (measured)
+        const long tiles = (long)((m + bm - 1) / bm) * ((l.n + kBN - 1) / kBN);
+        for (int s = 1; s <= octets && s <= kMaxSplits; ++s) {
+            const int per = (octets + s - 1) / s;
+            const int used = (octets + per - 1) / per;  // splits that get work
+            if (used != s) continue;
+            const size_t part = s > 1 ? (size_t)s * m * l.n * 4 : 0;
+            if (part > kMaxPartialBytes) break;
+            const double rounds = (double)((tiles * s + cus - 1) / cus);
+            const double t = rounds * per * 8 * step_us + (s > 1 ? 3.0 + part / bytes_per_us : 0.0);
+            if (best < 0.0 || t < best) {
+                best = t;
+                p.bm = bm;
+                p.splits = s;
+                p.g_split = per * 8;
+                p.part_bytes = part;
+            }
         }
     }
-    const size_t m16 = ((size_t)m + kBM - 1) / kBM * (kBM / 16);
+    const size_t m16 = ((size_t)m + p.bm - 1) / p.bm * (p.bm / 16);
     p.xaug_bytes = m16 * octets * 64 * 16;
     return p;
 }
@@ -580,7 +592,7 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
                        hipStream_t stream) {
     const GemmPlan plan = plan_gemm(m, l);
     const int octets = (l.g + 7) / 8;
-    const int mtiles = (m + kBM - 1) / kBM;
+    const int mtiles = (m + plan.bm - 1) / plan.bm;
     const int ntiles = (l.n + kBN - 1) / kBN;
     uint4* xaug = static_cast<uint4*>(workspace);
     float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.xaug_bytes);
@@ -588,7 +600,7 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
         (size_t)m * l.k * 2 > kMaxBufferBytes || plan.xaug_bytes > kMaxBufferBytes)
         return hipErrorInvalidValue;
     {
-        const long total = (long)mtiles * (kBM / 16) * octets * 64;
+        const long total = (long)mtiles * (plan.bm / 16) * octets * 64;
         const int block = 256;
         hipLaunchKernelGGL(xaug_kernel, dim3((unsigned)((total + block - 1) / block)), dim3(block), 0, stream, x, xaug, m,
                            l.k, l.g, octets, total);
@@ -599,8 +611,14 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     const uint32_t tb = (uint32_t)l.tile_bytes(), sbb = (uint32_t)l.sb_bytes();
     const long elems = (long)m * l.n;
     if (plan.splits > 1) {
-        hipLaunchKernelGGL((gemm_kernel<kOutF32>), grid, block, 0, stream, tiles, sb, x, xaug, (void*)part, m, l.n, l.k,
-                           l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, elems, n_out, gelu_table);
+        if (plan.bm == 128)
+            hipLaunchKernelGGL((gemm_kernel<kOutF32, 128>), grid, block, 0, stream, tiles, sb, x, xaug, (void*)part, m,
+                               l.n, l.k, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, elems, n_out,
+                               gelu_table);
+        else
+            hipLaunchKernelGGL((gemm_kernel<kOutF32, 256>), grid, block, 0, stream, tiles, sb, x, xaug, (void*)part, m,
+                               l.n, l.k, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, elems, n_out,
+                               gelu_table);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const int rblock = 256;
@@ -623,9 +641,15 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
                                plan.splits);
         return hipGetLastError();
     }
-#define Q4_GEMM_LAUNCH(MODE)                                                                                     \
-    hipLaunchKernelGGL((gemm_kernel<MODE>), grid, block, 0, stream, tiles, sb, x, xaug, y, m, l.n, l.k, l.g, l.gp, \
-                       mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L, n_out, gelu_table)
+#define Q4_GEMM_LAUNCH(MODE)                                                                                    \
+    do {                                                                                                        \
+        if (plan.bm == 128)                                                                                     \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 128>), grid, block, 0, stream, tiles, sb, x, xaug, y, m, l.n, l.k, \
+                               l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L, n_out, gelu_table);   \
+        else                                                                                                    \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 256>), grid, block, 0, stream, tiles, sb, x, xaug, y, m, l.n, l.k, \
+                               l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L, n_out, gelu_table);   \
+    } while (0)
     switch (out_mode) {
         case kOutF32: Q4_GEMM_LAUNCH(kOutF32); break;
         case kOutGegluBf16: Q4_GEMM_LAUNCH(kOutGegluBf16); break;

@@ -76,6 +76,7 @@ hipError_t launch_greedy_reduce(const unsigned long long* part, int nb, int rows
 // group sums of x and, when K is split over workgroups, the fp32 partial sums
 // (gemm_workspace_bytes(m, l) bytes, device memory, 16-byte aligned).
 struct GemmPlan {
+    int bm = 256;            // output tile rows: 256, or 128 for small M
     int splits = 1;          // workgroups along K per output tile
     int g_split = 0;         // groups per split (whole octets)
     size_t xaug_bytes = 0;   // group sums of x

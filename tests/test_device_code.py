@@ -43,7 +43,7 @@ def gemm_asm():
 
 def test_lds_dma_sgpr_hazards_covered(gemm_asm):
     kernels = list(_kernels(gemm_asm))
-    assert len(kernels) == 4  # bf16 / fp32 outputs, bf16 / fp32 GeGLU pairs
+    assert len(kernels) == 8  # bf16 / fp32 outputs, bf16 / fp32 GeGLU pairs; 256- and 128-row tiles
     for name, lines in kernels:
         dmas = 0
         for i, line in enumerate(lines):

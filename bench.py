@@ -90,17 +90,37 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def quantized_layer():
-    """The seven projections, quantized on the host from seeded weights."""
-    from oracle import affine as A
-    from oracle import c_oracle as C
+def synthetic_weights(n: int, k: int, seed: int):
+    """MLX-format triple (host numpy: uint32 codes, bf16 scale and bias bits) of a
+    seeded W ~ N(0, 0.02) [n, k] rounded to bf16, quantized 4-bit group-64 with the
+    package's quantizer (on the GPU when there is one)."""
+    import torch
+    from helios_amd.quantize import quantize
 
-    host = {}
-    for i, (name, n, k) in enumerate(LAYER):
-        rng = np.random.Generator(np.random.PCG64(SEED_BASE + 1000 + i))
-        w = rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
-        host[name] = C.quantize(A.round_to_bf16(w))
-    return host
+    rng = np.random.Generator(np.random.PCG64(seed))
+    w = torch.from_numpy(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    if torch.cuda.is_available():
+        w = w.cuda()
+    wq, s, b = quantize(w.bfloat16())
+    return (wq.cpu().numpy().view(np.uint32), s.view(torch.int16).cpu().numpy().view(np.uint16),
+            b.view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+def synthetic_activations(m: int, k: int, seed: int, outliers: bool = False) -> np.ndarray:
+    """bf16 bits of a seeded x ~ N(0, 1) [m, k]; with ``outliers`` 1% of the entries
+    are scaled by 20 (the prefill configuration's activation outliers)."""
+    import torch
+
+    rng = np.random.Generator(np.random.PCG64(seed))
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    if outliers:
+        x = np.where(rng.random((m, k)) < 0.01, x * np.float32(20), x).astype(np.float32)
+    return torch.from_numpy(x).bfloat16().view(torch.int16).numpy().view(np.uint16)
+
+
+def quantized_layer():
+    """The seven projections from seeded weights."""
+    return {name: synthetic_weights(n, k, SEED_BASE + 1000 + i) for i, (name, n, k) in enumerate(LAYER)}
 
 
 def fused_triple(host, names):
@@ -389,11 +409,10 @@ def model_run(torch, Q, decode_steps: int = 128, prefill_tokens: int = 16384, ch
 def cpu_baseline(host, target_s: float = 12.0) -> dict:
     """The oracle's fp32 qmm loop (OpenMP over rows) on this host's cores, on a
     bounded sample: whole decoder-layer steps at M=1, repeated until ~target_s."""
-    from oracle import affine as A
     from oracle import c_oracle as C
 
     threads = min(os.cpu_count() or 1, 16)
-    xs = {k: A.make_activations(1, k, seed=SEED_BASE + k) for k in {k for _, _, k in LAYER}}
+    xs = {k: synthetic_activations(1, k, seed=SEED_BASE + k) for k in {k for _, _, k in LAYER}}
     outs = {name: np.empty((1, n), np.float32) for name, n, _ in LAYER}
     step_bytes = sum(algo_bytes(1, n, k) for _, n, k in LAYER)
 
@@ -438,6 +457,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (skip the per-shape sweeps)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="the headline prefill GEMM (gate_proj, M=2048) only, one JSON line (for rocprofv3)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="time only the dominant kernel and a 1 GiB copy (the program rocprofv3 passes run)")
     ap.add_argument("--summarize-profiles", nargs=5, metavar=("STATS_DIR", "FETCH_DIR", "WRITE_DIR", "LINE", "CMD"),
@@ -454,7 +475,6 @@ def main() -> int:
 
     import helios_amd
     from helios_amd import qmm as Q
-    from oracle import affine as A
 
     helios_amd.load_library()
     torch.cuda.set_device(0)
@@ -473,7 +493,7 @@ def main() -> int:
             return lambda: Q.QuantizedGeGLU(host["gate_proj"], host["up_proj"])
         return lambda: Q.QuantizedLinear(*fused[name])
 
-    xs = {k: torch.from_numpy(A.make_activations(16, k, seed=SEED_BASE + k).view(np.int16)).view(torch.bfloat16).cuda()
+    xs = {k: torch.from_numpy(synthetic_activations(16, k, seed=SEED_BASE + k).view(np.int16)).view(torch.bfloat16).cuda()
           for k in {k for _, _, k in LAYER}}
     f_gu, k_gu = step_nk[PAIR]
     gu_bytes = pair_algo_bytes(1, f_gu, k_gu)
@@ -481,6 +501,18 @@ def main() -> int:
 
     def pair_us(m):
         return kernel_us(torch, maker(PAIR), m, k_gu, f_gu, xs[k_gu], wbytes_of[PAIR])
+
+    if args.gemm_only:
+        n_g, k_g = step_nk_gate = (15360, HIDDEN)
+        xg = torch.from_numpy(synthetic_activations(2048, k_g, seed=SEED_BASE + 2 + k_g, outliers=True).view(np.int16)) \
+            .view(torch.bfloat16).cuda()
+        yg = torch.empty((2048, n_g), dtype=torch.bfloat16, device="cuda")
+        lin = Q.QuantizedLinear(*host["gate_proj"])
+        ms = graph_ms_steady(torch, lambda: lin.forward(xg, out=yg))
+        lin.close()
+        print(json.dumps({"shape": "gate_proj M=2048 N=15360 K=3840", "us": round(ms * 1e3, 1),
+                          "TFLOPS": round(algo_flops(2048, n_g, k_g) / (ms * 1e-3) / 1e12, 1)}), flush=True)
+        return 0
 
     if args.roofline_only:
         us_gu = pair_us(1)
@@ -552,13 +584,8 @@ def main() -> int:
             per_proj[f"{PAIR}_m{m}"] = {"us": round(us, 2),
                                         "GBps": round(pair_algo_bytes(m, f_gu, k_gu) / (us * 1e-6) / 1e9, 1)}
         try:
-            from oracle import c_oracle as C
-
             log("quantizing lm_head 262144x3840")
-            rng = np.random.Generator(np.random.PCG64(SEED_BASE + 3000))
-            lm_w = rng.standard_normal((262144, HIDDEN), dtype=np.float32) * np.float32(0.02)
-            lm_triple = C.quantize(A.round_to_bf16(lm_w))
-            del lm_w
+            lm_triple = synthetic_weights(262144, HIDDEN, SEED_BASE + 3000)
             lm = {}
             for m in (1, 8, 16):
                 us = kernel_us(torch, lambda: Q.QuantizedLinear(*lm_triple), m, HIDDEN, 262144, xs[HIDDEN],
@@ -575,7 +602,7 @@ def main() -> int:
         gemm = {}
         shapes = LAYER if not args.quick else [l for l in LAYER if l[0] == "gate_proj"]
         for m in ((512, 2048) if not args.quick else (2048,)):
-            xk = {k: torch.from_numpy(A.make_activations(m, k, seed=SEED_BASE + 2 + k, outliers=True).view(np.int16))
+            xk = {k: torch.from_numpy(synthetic_activations(m, k, seed=SEED_BASE + 2 + k, outliers=True).view(np.int16))
                   .view(torch.bfloat16).cuda() for k in {k for _, _, k in shapes}}
             for name, n, k in shapes:
                 ym = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")

@@ -8,6 +8,7 @@ epilogue (native_model.cc:934-949, :378-386).  ``helios_amd.qmm`` is the Python
 binding of that ABI.
 """
 
+from .quantize import quantize  # noqa: F401
 from .qmm import (  # noqa: F401
     Gemma4Error,
     QuantizedGeGLU,

@@ -1,4 +1,5 @@
-// Decode-shape affine-Q4 matmul on gfx950: y[M,N] = x[M,K] . W^T for M <= 16.
+// Decode-shape affine-Q4 matmul on gfx950: y[M,N] = x[M,K] . W^T for M < 32, in
+// 16-row slabs (one launch; slab = blockIdx.y).
 //
 // Bandwidth-bound: every weight byte is read once from HBM with 16-byte coalesced
 // loads (one 1 KiB tile per wave-load), scales/biases once per group, nibbles are
@@ -10,8 +11,11 @@
 // costs nothing here: the matrix cores are far from busy at this arithmetic
 // intensity, and the VALU work per weight stays at ~1.2 ops.
 //
-// Work split: one workgroup per 16-row block; its WAVES waves split the group pairs
-// of K and meet in LDS for a split-K sum (no atomics, no second pass).
+// Three kernels, chosen per shape in launch_mt: decode_kernel (one workgroup per
+// 16-row block, its waves split the group pairs of K and meet in LDS for a split-K
+// sum: no atomics, no second pass), decode_stream_kernel (the same split, persistent
+// workgroups walking row blocks) and decode_rows_kernel (M = 1: one wave per row
+// block).
 #include "q4_common.h"
 #include "q4_kernels.h"
 
@@ -169,8 +173,8 @@ __device__ __forceinline__ uint32_t scale_word(uint2 sv, int pair, int gi, int c
     return (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)(gi ? sv.y : sv.x));
 }
 
-// Persistent streaming variant for M <= 4 (x staged in LDS).  Each workgroup walks
-// row blocks blockIdx.x, blockIdx.x + gridDim.x, ...; its waves split K and stream
+// Persistent streaming variant (x staged in LDS, up to 16 rows per slab).  Each
+// workgroup walks row blocks blockIdx.x, blockIdx.x + gridDim.x, ...; its waves split K and stream
 // their weight tiles in chunks of GPW group pairs, double-buffered, so the loads for
 // the next chunk (possibly of the next row block) are in flight while the current
 // one is multiplied.  Per workgroup, once:
@@ -347,8 +351,8 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
     if (c < chunks) compute(wa, sa, c);
 }
 
-// Row-block-per-wave variant for M <= 4 when N has many row blocks (gate|up, the
-// lm_head).  Every wave owns whole 16-row blocks (wave w of the grid takes blocks w,
+// Row-block-per-wave variant, launched for M = 1 when N has many row blocks (gate
+// and the gate|up pair).  Every wave owns whole 16-row blocks (wave w of the grid takes blocks w,
 // w + total waves, ...), so there is no cross-wave reduction and no barrier after x
 // is staged, and each wave keeps NBUF chunks of GPW tiles in flight across block
 // boundaries.  x is staged in LDS once per workgroup, with the table of -X_g per

@@ -63,7 +63,7 @@ hipError_t launch_embed(const uint4* tiles, const uint2* sb, const int32_t* ids,
 // F for the GeGLU modes (h is [M, F]) and unused otherwise.
 struct OutParams;
 
-// Decode path, M <= 16 rows per launch (the launcher walks larger M in 16-row slabs).
+// Decode path, any M in one launch (16-row slabs along the grid's y dimension).
 hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, const OutParams& op, int m,
                          const Layout& l, hipStream_t stream);
 

@@ -185,7 +185,7 @@ __device__ __forceinline__ uint32_t scale_word(uint2 sv, int pair, int gi, int c
 //     the group, seeded from that table.  Table rows >= M are never written: they
 //     only reach accumulator rows that are never stored.
 // Per row block the waves meet once in LDS (ping-pong buffers, one barrier).
-template <int MT, int GPW>
+template <int MT, int GPW, int NBUF>
 __global__ __launch_bounds__(512) void decode_stream_kernel(
     const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x_in,
     OutParams op_in, int m_total, int n_rows, int k, int gpairs, int nblocks, int waves) {
@@ -214,8 +214,8 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
     float* negx = reinterpret_cast<float*>(lds + m_rows * row16);  // [2 * (gpairs + GPW)][16]
 
     static_assert(GPW == 4, "one 8-byte load per lane covers a chunk's scale words");
-    uint4 wa[GPW], wb[GPW];
-    uint2 sa, sbv2;  // scale words of a chunk: lane (col, kq) holds pair kq, column col
+    uint4 w[NBUF][GPW];
+    uint2 sv[NBUF];  // scale words of a chunk: lane (col, kq) holds pair kq, column col
     // Chunks past the workgroup's last are issued too, against an empty range (zeros,
     // no memory traffic): every loop iteration then issues the same loads, which keeps
     // the compiler's wait counts exact (a conditional issue makes it wait for both
@@ -268,11 +268,11 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
                 if (c < xchunks && (lane & 7) == 0) negx[(cr >> 3) * 16 + row] = -sum;
             }
         };
-        // first batch of x, then both weight buffers, then the batch is stored: in
+        // first batch of x, then every weight buffer, then the batch is stored: in
         // straight-line code, so waiting for x leaves the weight loads in flight
         load_x(0);
-        issue(wa, sa, 0);
-        issue(wb, sbv2, 1);
+#pragma unroll
+        for (int b = 0; b < NBUF; ++b) issue(w[b], sv[b], b);
         store_x(0);
         for (int c0 = 4 * nthr; c0 < xchunks; c0 += 4 * nthr) {  // rows past 2048 elements per thread
             load_x(c0);
@@ -340,15 +340,18 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
         }
     };
 
-    // two chunks in flight: compute one buffer, then refill it two chunks ahead
+    // NBUF chunks in flight: compute one buffer, then refill it NBUF chunks ahead
     int c = 0;
-    for (; c + 1 < chunks; c += 2) {
-        compute(wa, sa, c);
-        issue(wa, sa, c + 2);
-        compute(wb, sbv2, c + 1);
-        issue(wb, sbv2, c + 3);
+    for (; c + NBUF <= chunks; c += NBUF) {
+#pragma unroll
+        for (int b = 0; b < NBUF; ++b) {
+            compute(w[b], sv[b], c + b);
+            issue(w[b], sv[b], c + b + NBUF);
+        }
     }
-    if (c < chunks) compute(wa, sa, c);
+#pragma unroll
+    for (int b = 0; b + 1 < NBUF; ++b)  // fewer than NBUF chunks remain
+        if (c + b < chunks) compute(w[b], sv[b], c + b);
 }
 
 // Row-block-per-wave variant, launched for M = 1 when N has many row blocks (gate
@@ -593,8 +596,15 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
         const int capacity = device_cus() * per_cu;
         const int per_wg = (l.nb + capacity - 1) / capacity;
         const int grid = (l.nb + per_wg - 1) / per_wg;
-        hipLaunchKernelGGL((decode_stream_kernel<MT, GPW>), dim3(grid, slabs), dim3(64 * waves), lds_bytes, stream,
-                           tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb, waves);
+        // one workgroup per CU and a long walk (the lm_head at M = 8: 126 vs 135 us):
+        // four chunks per wave in flight.  Not for short walks (down and the gate|up
+        // pair at M = 2-16 were 5-15% slower: the deeper prefetch delays x staging).
+        if (per_cu == 1 && per_wg >= 16)
+            hipLaunchKernelGGL((decode_stream_kernel<MT, GPW, 4>), dim3(grid, slabs), dim3(64 * waves), lds_bytes,
+                               stream, tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb, waves);
+        else
+            hipLaunchKernelGGL((decode_stream_kernel<MT, GPW, 2>), dim3(grid, slabs), dim3(64 * waves), lds_bytes,
+                               stream, tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb, waves);
         return hipGetLastError();
     }
     const Split sp = choose_split(l.gp, MT);

@@ -197,7 +197,7 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
     const int m_rows = m_total - 16 * slab < 16 ? m_total - 16 * slab : 16;
     const uint16_t* __restrict__ x = x_in + (size_t)slab * 16 * k;
     const OutParams op = slab_params(op_in, slab, n_rows);
-    // layout: x rows [m_rows][k + kPad] bf16, then -X table [2*(gpairs+GPW)][16] fp32
+    // layout: x rows [m_rows][k + kPad + 8] bf16, then -X table [2*(gpairs+GPW)][16] fp32
     __shared__ float red[2][8][R * 64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -209,7 +209,9 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
     const int my_blocks = (nblocks - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     const int chunks = my_blocks * passes;
     const int arow = col < m_rows ? col : m_rows - 1;  // any valid row for A rows >= M
-    const int row16 = (k + kPad) >> 3;                 // x row stride in 16-byte units
+    // x row stride in 16-byte units: odd (one unit past the padding), so the 16 rows
+    // one operand read touches fall in different LDS banks
+    const int row16 = ((k + kPad) >> 3) + 1;
     const int groups = k >> 6;
     float* negx = reinterpret_cast<float*>(lds + m_rows * row16);  // [2 * (gpairs + GPW)][16]
 
@@ -585,13 +587,14 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
                            sb, x, op, m, l.n, l.k, l.gp, waves);
         return hipGetLastError();
     }
-    if (lds_bytes + static_lds <= kLdsPerCu) {
+    const size_t stream_lds = lds_bytes + (size_t)ms * 16;  // x rows one 16-byte unit longer
+    if (stream_lds + static_lds <= kLdsPerCu) {
         // persistent streaming kernel: 4 pairs per chunk, up to 8 waves per workgroup
         int waves = (l.gp + GPW - 1) / GPW;
         if (waves > 8) waves = 8;
         if (waves > l.gp) waves = l.gp;
         int per_cu = 20 / waves > 0 ? 20 / waves : 1;
-        const int lds_fit = (int)(kLdsPerCu / (lds_bytes + static_lds));
+        const int lds_fit = (int)(kLdsPerCu / (stream_lds + static_lds));
         if (per_cu > lds_fit) per_cu = lds_fit;
         const int capacity = device_cus() * per_cu;
         const int per_wg = (l.nb + capacity - 1) / capacity;
@@ -600,10 +603,10 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
         // four chunks per wave in flight.  Not for short walks (down and the gate|up
         // pair at M = 2-16 were 5-15% slower: the deeper prefetch delays x staging).
         if (per_cu == 1 && per_wg >= 16)
-            hipLaunchKernelGGL((decode_stream_kernel<MT, GPW, 4>), dim3(grid, slabs), dim3(64 * waves), lds_bytes,
+            hipLaunchKernelGGL((decode_stream_kernel<MT, GPW, 4>), dim3(grid, slabs), dim3(64 * waves), stream_lds,
                                stream, tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb, waves);
         else
-            hipLaunchKernelGGL((decode_stream_kernel<MT, GPW, 2>), dim3(grid, slabs), dim3(64 * waves), lds_bytes,
+            hipLaunchKernelGGL((decode_stream_kernel<MT, GPW, 2>), dim3(grid, slabs), dim3(64 * waves), stream_lds,
                                stream, tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb, waves);
         return hipGetLastError();
     }

@@ -39,30 +39,43 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // xaug[m16][octet][lane] (16 B), lane (m = l%16, kq = l/16), element e ->
 // group 8*octet + 2*kq + e/4, term e%4 in {Xh, Xl, -16 Xh, -16 Xl}.
 // ---------------------------------------------------------------------------
-__global__ void xaug_kernel(const uint16_t* __restrict__ x, uint4* __restrict__ xaug, int m_rows, int k,
-                            int groups, int octets, long total) {
-    const long tid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (tid >= total) return;
-    const int lane = (int)(tid & 63);
-    const long t = tid >> 6;
-    const int o = (int)(t % octets);
-    const long mb = t / octets;
-    const long m = mb * 16 + (lane & 15);
-    const int kq = lane >> 4;
+// One 512-thread workgroup per 1 KiB block (16 rows x one octet): eight lanes sum one
+// (row, group) from its 128 contiguous bytes, two rounds cover the 16 x 8 pairs, the
+// sums meet in LDS and one wave packs the block.
+__global__ __launch_bounds__(512) void xaug_kernel(const uint16_t* __restrict__ x, uint4* __restrict__ xaug,
+                                                   int m_rows, int k, int groups, int octets) {
+    __shared__ float gsum[8][16];  // [group within the octet][row within the block]
+    const int unit = (int)blockIdx.x;  // 16-row block * octets + octet
+    const int o = unit % octets;
+    const long mb = unit / octets;
+    const int t = (int)threadIdx.x;
+    const int c = t & 7;  // 16-byte chunk of the group
+    uint4 v[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {  // both loads in flight before any sum
+        const int p = (t >> 3) + 64 * r;
+        const long m = mb * 16 + (p & 15);
+        const int g = 8 * o + (p >> 4);
+        v[r] = (m < m_rows && g < groups) ? *reinterpret_cast<const uint4*>(x + m * k + 64 * g + 8 * c)
+                                          : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int p = (t >> 3) + 64 * r;
+        float sum = ((bf16_lo(v[r].x) + bf16_hi(v[r].x)) + (bf16_lo(v[r].y) + bf16_hi(v[r].y))) +
+                    ((bf16_lo(v[r].z) + bf16_hi(v[r].z)) + (bf16_lo(v[r].w) + bf16_hi(v[r].w)));
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        sum += __shfl_xor(sum, 4);
+        if (c == 0) gsum[p >> 4][p & 15] = sum;
+    }
+    __syncthreads();
+    if (t >= 64) return;
+    const int kq = t >> 4;
     uint32_t w[4];
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
-        const int g = 8 * o + 2 * kq + gi;
-        float sum = 0.f;
-        if (m < m_rows && g < groups) {
-            const uint4* src = reinterpret_cast<const uint4*>(x + m * k + 64 * g);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const uint4 v = src[c];
-                sum += bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y) + bf16_lo(v.z) + bf16_hi(v.z) +
-                       bf16_lo(v.w) + bf16_hi(v.w);
-            }
-        }
+        const float sum = gsum[2 * kq + gi][t & 15];
         const uint16_t xh = f32_to_bf16(sum);
         const uint16_t xl = f32_to_bf16(sum - __uint_as_float((uint32_t)xh << 16));
         const uint16_t nxh = f32_to_bf16(-16.0f * __uint_as_float((uint32_t)xh << 16));
@@ -70,7 +83,7 @@ __global__ void xaug_kernel(const uint16_t* __restrict__ x, uint4* __restrict__ 
         w[2 * gi] = (uint32_t)xh | ((uint32_t)xl << 16);
         w[2 * gi + 1] = (uint32_t)nxh | ((uint32_t)nxl << 16);
     }
-    xaug[tid] = make_uint4(w[0], w[1], w[2], w[3]);
+    xaug[(long)unit * 64 + t] = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // B operand of the bias MFMA from one scale/bias word pair: [b0 b0 s0 s0 b1 b1 s1 s1]
@@ -600,10 +613,8 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
         (size_t)m * l.k * 2 > kMaxBufferBytes || plan.xaug_bytes > kMaxBufferBytes)
         return hipErrorInvalidValue;
     {
-        const long total = (long)mtiles * (plan.bm / 16) * octets * 64;
-        const int block = 256;
-        hipLaunchKernelGGL(xaug_kernel, dim3((unsigned)((total + block - 1) / block)), dim3(block), 0, stream, x, xaug, m,
-                           l.k, l.g, octets, total);
+        const long units = (long)mtiles * (plan.bm / 16) * octets;  // 1 KiB blocks
+        hipLaunchKernelGGL(xaug_kernel, dim3((unsigned)units), dim3(512), 0, stream, x, xaug, m, l.k, l.g, octets);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -266,7 +266,9 @@ def summarize_profiles(stats_dir: str, fetch_dir: str, write_dir: str, line_file
         return sum(vals) / len(vals), len(vals)
 
     is_dom = lambda n: DOM_KERNEL in n  # noqa: E731
-    is_copy = lambda n: "copy" in n.lower()  # noqa: E731
+    # the runtime's blit kernel of the 1 GiB device copy (torch's own dtype-conversion
+    # kernels also carry "copy" in their names)
+    is_copy = lambda n: "rocclr_copybuffer" in n.lower()  # noqa: E731
     fetch_rows = _csv_rows(fetch_dir, "counter_collection.csv")
     write_rows = _csv_rows(write_dir, "counter_collection.csv")
     f_dom, n_fd = per_dispatch(fetch_rows, "FETCH_SIZE", is_dom)

@@ -217,6 +217,26 @@ def test_forward_many_row_blocks_per_workgroup(gpu_lib, m, n, k):
     assert_close(y, C.qmm_f64(x, wq, s, b), f"tall m={m}")
 
 
+@pytest.mark.parametrize("f32", [False, True])
+@pytest.mark.parametrize("m,n,k", [(5, 48, 15360), (8, 3840, 15360), (13, 40, 14976), (16, 3840, 15360),
+                                   (16, 48, 4096), (16, 33 * 16, 14976)])
+def test_forward_decode_x_beyond_lds(gpu_lib, m, n, k, f32):
+    """Decode launches whose x is too long for LDS (down_proj's K = 15360 from M = 5,
+    o_proj's 4096 at M = 16, 117 pairs): the variant that reads x from global memory,
+    ragged row counts and a last slab of fewer than 16 rows."""
+    import torch
+
+    wq, s, b = random_triple(n, k, seed=61 + m + n)
+    x = A.make_activations(m, k, seed=62 + m, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    y = lin.forward(dev_x(x), out_dtype=torch.float32 if f32 else torch.bfloat16)
+    y2 = lin.forward(dev_x(x), out_dtype=torch.float32 if f32 else torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)  # deterministic
+    assert_close(y, C.qmm_f64(x, wq, s, b), f"x beyond LDS m={m} n={n} k={k}")
+    lin.close()
+
+
 # ---------------------------------------------------------------- prefill (GEMM path)
 
 # K = 64, 576, 1088: one group, and a last octet of one group (9, 17 groups)

@@ -175,11 +175,14 @@ __device__ __forceinline__ uint32_t scale_word(uint2 sv, int pair, int gi, int c
 
 // Persistent streaming variant (x staged in LDS, up to 16 rows per slab).  Each
 // workgroup walks row blocks blockIdx.x, blockIdx.x + gridDim.x, ...; its waves split K and stream
-// their weight tiles in chunks of GPW group pairs, double-buffered, so the loads for
-// the next chunk (possibly of the next row block) are in flight while the current
-// one is multiplied.  Per workgroup, once:
+// their weight tiles in chunks of GPW group pairs, NBUF chunks in flight (two, or
+// four for long walks at one workgroup per CU), so the loads for the next chunks
+// (possibly of the next row blocks) are in flight while the current one is
+// multiplied.  Per workgroup, once:
 //   * x[M][K] is copied to LDS, each row zero-padded by GPW pairs so that operand
-//     reads need no bounds tests (zero tiles past a wave's range meet finite x);
+//     reads need no bounds tests (zero tiles past a wave's range meet finite x), and
+//     one 16-byte unit more so that rows sit an odd number of units apart (the 16
+//     rows of an operand read then fall in different banks);
 //   * -X_g (the group sums of x, negated) is summed while x is copied and kept in
 //     LDS in accumulator layout, so each row block needs only the two products of
 //     the group, seeded from that table.  Table rows >= M are never written: they

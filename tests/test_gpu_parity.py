@@ -200,6 +200,25 @@ def test_forward_rejects_misaligned_x(gpu_lib):
     assert e.value.status == gpu_lib.Status.INVALID_ARGUMENT and "aligned" in e.value.message
 
 
+@pytest.mark.parametrize("m", [0, 1, 4, 33])
+@pytest.mark.parametrize("n,k", [(1, 64), (15, 192), (17, 64)])
+def test_forward_empty_rows_and_partial_row_blocks(gpu_lib, m, n, k):
+    """M = 0 returns an empty result without a launch; N of 1, 15 and 17 leave a row
+    block mostly or partly empty, on the decode (M = 1, 4) and GEMM (M = 33) paths."""
+    import torch
+
+    wq, s, b = random_triple(n, k, seed=71 + n + k)
+    x = A.make_activations(m, k, seed=72 + m, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    for f32 in (False, True):
+        y = lin.forward(dev_x(x), out_dtype=torch.float32 if f32 else torch.bfloat16)
+        torch.cuda.synchronize()
+        assert tuple(y.shape) == (m, n)
+        if m:
+            assert_close(y, C.qmm_f64(x, wq, s, b), f"m={m} n={n} k={k} f32={f32}")
+    lin.close()
+
+
 @pytest.mark.parametrize("m", [1, 3, 4])
 @pytest.mark.parametrize("n,k", [(131072 + 48, 128), (32768 + 40, 256)])
 def test_forward_many_row_blocks_per_workgroup(gpu_lib, m, n, k):

@@ -594,7 +594,11 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
         return hipGetLastError();
     }
     const size_t stream_lds = lds_bytes + (size_t)ms * 16;  // x rows one 16-byte unit longer
-    if (stream_lds + static_lds <= kLdsPerCu) {
+    // K of a multiple of 8 pairs beyond 64 (down_proj) at M = 3-4: the one-pass global-x
+    // variant below is ahead of streaming (12.0 vs 12.6 us at M = 3, 12.5 vs 13.7 at 4;
+    // behind at M = 2)
+    const bool one_pass = MT >= 4 && l.gp % 8 == 0 && l.gp / 8 <= 16 && l.gp / 4 > 16;
+    if (!one_pass && stream_lds + static_lds <= kLdsPerCu) {
         // persistent streaming kernel: 4 pairs per chunk, up to 8 waves per workgroup
         int waves = (l.gp + GPW - 1) / GPW;
         if (waves > 8) waves = 8;

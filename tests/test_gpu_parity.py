@@ -237,12 +237,14 @@ def test_forward_many_row_blocks_per_workgroup(gpu_lib, m, n, k):
 
 
 @pytest.mark.parametrize("f32", [False, True])
-@pytest.mark.parametrize("m,n,k", [(5, 48, 15360), (8, 3840, 15360), (13, 40, 14976), (16, 3840, 15360),
+@pytest.mark.parametrize("m,n,k", [(3, 48, 15360), (4, 40, 15360), (5, 48, 15360), (8, 3840, 15360),
+                                   (13, 40, 14976), (16, 3840, 15360),
                                    (16, 48, 4096), (16, 33 * 16, 14976)])
 def test_forward_decode_x_beyond_lds(gpu_lib, m, n, k, f32):
-    """Decode launches whose x is too long for LDS (down_proj's K = 15360 from M = 5,
-    o_proj's 4096 at M = 16, 117 pairs): the variant that reads x from global memory,
-    ragged row counts and a last slab of fewer than 16 rows."""
+    """Decode launches that read x from global memory: x too long for LDS (down_proj's
+    K = 15360 from M = 5, o_proj's 4096 at M = 16, 117 pairs) and down_proj-like K at
+    M = 3-4 (one pass of 8 pairs per wave); ragged row counts and a last slab of fewer
+    than 16 rows."""
     import torch
 
     wq, s, b = random_triple(n, k, seed=61 + m + n)

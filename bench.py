@@ -15,14 +15,22 @@ see algo_bytes) / measured step time, with the weights already resident in HBM, 
 the step.  The loop rotates over enough distinct weight copies (>= 512 MiB) that
 the 256 MiB Infinity Cache cannot serve them.
 
-Also reported: the dominant kernel's roofline (the gate|up GeGLU pair at M=1, timed
-per launch from graph replays of back-to-back launches), every projection at M = 1,
-4, 8, the lm_head at M = 1, 8, 16, the prefill GEMM at M = 512 and 2048 (the seven
-projections and the GeGLU pair), and the CPU baseline (the oracle's fp32 loop on the
-host cores, on a bounded sample of the same work).
+The headline replays run `--warmup` times, then untimed for `--settle-ms` of wall
+time (the GPU's clock ramps for a few milliseconds once it gets busy, so a handful of
+replays would time the ramp), then exactly `--steps` timed replays.
+
+Also reported: the single GEMV of config 1 (gate_proj's shape at M=1) as its own
+field, the dominant kernel's roofline (the gate|up GeGLU pair at M=1, timed per launch
+from graph replays of back-to-back launches), every projection at M = 1, 4, 8, the
+lm_head at M = 1, 8, 16, the prefill GEMM at M = 256 (the reference's long-context
+chunk), 512 and 2048 (the seven projections, the GeGLU pair and the real 12B's
+full-attention shapes), practical peaks (a 1 GiB copy, a read-only streaming kernel,
+hipBLASLt on the gate shape), and the CPU baseline (the oracle's fp32 loop on the host
+cores, on bounded samples of configs 1-4, all threads and one thread).
 
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--quick]
     python bench.py --roofline-only   # the dominant kernel and a 1 GiB copy only (for rocprofv3)
+    python bench.py --prefill-only    # the prefill GEMM sweep only (for rocprofv3 kernel traces)
 
 `roofline.traffic` is the HBM bytes one launch of the dominant kernel moves, from
 rocprofv3 FETCH_SIZE and WRITE_SIZE passes over `--roofline-only`, each scaled by
@@ -128,10 +136,28 @@ def fused_triple(host, names):
     return tuple(np.ascontiguousarray(np.concatenate([p[j] for p in parts], axis=0)) for j in range(3))
 
 
-def graph_ms(torch, fn, replays: int, warmup: int) -> float:
-    """Captures fn() in a HIP graph, replays it warmup + replays times on the
-    current stream and returns ms per replay over exactly `replays` timed replays
-    (HIP events on the stream the kernels run on, synchronized on both sides)."""
+def settle(torch, replay, settle_ms: float) -> int:
+    """Replays untimed until settle_ms of wall time have passed (the GPU's clock ramps
+    for a few milliseconds once it gets busy); returns the replays spent.  Batches are
+    synchronized, so the wall time is the GPU's."""
+    t0 = time.perf_counter()
+    n, batch = 0, 1
+    while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        t1 = time.perf_counter()
+        for _ in range(batch):
+            replay()
+        torch.cuda.synchronize()
+        n += batch
+        if (time.perf_counter() - t1) * 1e3 < 2.0:
+            batch *= 2
+    return n
+
+
+def graph_ms(torch, fn, replays: int, warmup: int, settle_ms: float = 0.0, info: dict | None = None) -> float:
+    """Captures fn() in a HIP graph, replays it `warmup` times, then (settle_ms > 0)
+    untimed until settle_ms of wall time have passed, and returns ms per replay over
+    exactly `replays` timed replays (HIP events on the stream the kernels run on,
+    synchronized on both sides)."""
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
@@ -143,6 +169,11 @@ def graph_ms(torch, fn, replays: int, warmup: int) -> float:
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
+    if settle_ms > 0:
+        n = settle(torch, g.replay, settle_ms)
+        if info is not None:
+            info["settle_replays"] = n
+            info["settle_ms"] = settle_ms
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     cur = torch.cuda.current_stream()
@@ -200,6 +231,39 @@ def copy_gbs(torch, nbytes: int = COPY_BYTES, reps: int = 20) -> float:
     ms = t0.elapsed_time(t1) / reps
     del src, dst
     return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
+def read_gbs(torch, nbytes: int = COPY_BYTES, reps: int = 20) -> dict:
+    """Practical HBM read rate: the read-only streaming kernel of libhbm_probe.so
+    (each wave one contiguous 8 KiB run per step, neighbouring waves neighbouring
+    runs) over nbytes, the best over a few grid sizes; graph-replayed after a wall-time
+    settle, timed with events on the replay stream."""
+    import ctypes
+
+    from helios_amd import build as hbuild
+
+    lib = ctypes.CDLL(hbuild.PROBE_PATH)
+    lib.hbm_read_probe.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    lib.hbm_read_probe.restype = ctypes.c_int
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    best = None
+    for per_cu in (2, 4, 8):
+        wgs = cus * per_cu
+        sink = torch.empty(wgs * 4, dtype=torch.int32, device="cuda")
+
+        def fn():
+            st = torch.cuda.current_stream().cuda_stream
+            if lib.hbm_read_probe(buf.data_ptr(), nbytes, sink.data_ptr(), wgs, ctypes.c_void_p(st)) != 0:
+                raise RuntimeError("hbm_read_probe launch failed")
+
+        ms = graph_ms(torch, fn, replays=reps, warmup=2, settle_ms=30.0)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        if best is None or gbs > best["GBps"]:
+            best = {"GBps": round(gbs, 1), "workgroups_per_cu": per_cu, "bytes": nbytes}
+        del sink
+    del buf
+    return best
 
 
 def dense_gemm_tflops(torch, m: int, n: int, k: int, reps: int = 20) -> float:
@@ -318,6 +382,71 @@ def summarize_profiles(stats_dir: str, fetch_dir: str, write_dir: str, line_file
     print(json.dumps(traffic))
 
 
+PREFILL_MS = (256, 512, 2048)
+
+
+def prefill_sweep_names(ms=PREFILL_MS):
+    """The forwards of `--prefill-only` in the order it runs them."""
+    names = []
+    for m in ms:
+        names += [f"{n}_m{m}" for n, _, _ in list(LAYER) + list(FULL_ATTENTION)] + [f"{PAIR}_m{m}"]
+    return names
+
+
+def summarize_trace(db_path: str, out_md: str, command: str) -> None:
+    """Per-shape kernel durations of `bench.py --prefill-only` from a rocprofv3
+    --kernel-trace database (rocpd SQLite).  Each shape's handle is created (one
+    repack launch) before its forwards, which split the trace into the sweep's shapes
+    in order; every forward launches xaug_kernel, the GEMM and (when K is split) the
+    split-K reduction.  Reported: the median duration of each kernel and of the whole
+    forward (first launch start to last launch end) over the shape's graph replays."""
+    import re
+    import sqlite3
+
+    rows = list(sqlite3.connect(db_path).execute(
+        "select name, grid_x, grid_y, workgroup_x, duration, start from kernels order by start"))
+
+    def short(n):
+        n = n.replace("(anonymous namespace)::", "").replace("void ", "").replace("q4::", "")
+        return re.sub(r"\(.*", "", n)
+
+    shapes = []  # per shape: list of forwards, each a list of launches
+    for r in rows:
+        if "q4::" not in r[0]:
+            continue
+        s = short(r[0])
+        if s.startswith("repack"):
+            if not shapes or shapes[-1]:
+                shapes.append([])
+        elif s.startswith("xaug") and shapes:
+            shapes[-1].append([r])
+        elif shapes and shapes[-1]:
+            shapes[-1][-1].append(r)
+    names = prefill_sweep_names()
+    md = ["# Prefill GEMM sweep: kernel durations per forward", "", "Command (from the repository root):", "",
+          "```", command, "```", "",
+          "Per shape: the launches of one forward (kernel: workgroups x K splits) and their median durations over "
+          "the shape's graph replays; the forward's span runs from its first launch's start to its last launch's "
+          "end.", "",
+          "| shape | launches | forwards | median us per kernel | forward span us |", "|---|---|---:|---|---:|"]
+    for name, fwds in zip(names, shapes):
+        if not fwds:
+            continue
+        sig = max(set(tuple((short(p[0]), p[1] // max(p[3], 1), p[2]) for p in f) for f in fwds),
+                  key=lambda k: sum(1 for f in fwds if len(f) == len(k)))
+        same = [f for f in fwds if len(f) == len(sig)]
+        cols = list(zip(*[[p[4] for p in f] + [f[-1][5] + f[-1][4] - f[0][5]] for f in same]))
+        med = [sorted(c)[len(c) // 2] / 1e3 for c in cols]
+        desc = ", ".join(f"{k} {g}x{y}" for k, g, y in sig)
+        md.append(f"| {name} | {desc} | {len(same)} | {' / '.join(f'{x:.2f}' for x in med[:-1])} | "
+                  f"{med[-1]:.2f} |")
+    if len(shapes) != len(names):
+        md += ["", f"(trace holds {len(shapes)} shapes, the sweep {len(names)}: labels may not line up)"]
+    with open(out_md, "w") as f:
+        f.write("\n".join(md) + "\n")
+    print("\n".join(md))
+
+
 def model_run(torch, Q, decode_steps: int = 128, prefill_tokens: int = 16384, chunk: int = 2048,
               layers: int = 48) -> dict:
     """The 48-layer Gemma-style 12B decoder's quantized matmuls (the other ops of the
@@ -408,47 +537,132 @@ def model_run(torch, Q, decode_steps: int = 128, prefill_tokens: int = 16384, ch
     }
 
 
-def cpu_baseline(host, target_s: float = 12.0) -> dict:
-    """The oracle's fp32 qmm loop (OpenMP over rows) on this host's cores, on a
-    bounded sample: whole decoder-layer steps at M=1, repeated until ~target_s."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(host, lm_triple=None, scale: float = 1.0) -> dict:
+    """The oracle's fp32 qmm loop (dequantize a row's groups, then dot; OpenMP over
+    rows) on this host's cores, on bounded samples of four configurations, each timed
+    on all threads and on 1 thread: the single GEMV (gate_proj shape, M = 1), the
+    decoder layer's seven projections at M = 1 (the headline's workload and `value`),
+    the lm_head at M = 1, and the seven projections at the prefill chunk M = 512.
+    Samples that would take long on one thread use the first rows of each weight
+    (the rate per byte or per flop does not depend on which rows).  Threads: the
+    OMP_NUM_THREADS of the environment (the host's CPU share), else os.cpu_count()."""
     from oracle import c_oracle as C
 
-    threads = min(os.cpu_count() or 1, 16)
-    xs = {k: synthetic_activations(1, k, seed=SEED_BASE + k) for k in {k for _, _, k in LAYER}}
-    outs = {name: np.empty((1, n), np.float32) for name, n, _ in LAYER}
-    step_bytes = sum(algo_bytes(1, n, k) for _, n, k in LAYER)
+    env_threads = os.environ.get("OMP_NUM_THREADS", "")
+    threads = int(env_threads) if env_threads.isdigit() and int(env_threads) > 0 else (os.cpu_count() or 1)
+    xs = {(m, k): synthetic_activations(m, k, seed=SEED_BASE + 7 * m + k) for m in (1, 512)
+          for k in {k for _, _, k in LAYER}}
 
-    def one_step():
-        for name, n, k in LAYER:
-            C.qmm_f32(xs[k], *host[name], threads=threads, out=outs[name])
+    def rows(tri, r):
+        return tuple(np.ascontiguousarray(a[:r]) for a in tri) if r < tri[0].shape[0] else tri
 
-    def timed(target):
-        one_step()
+    def timed(fn, target):
+        fn()  # warm (page in, thread pool up)
         t0 = time.perf_counter()
         reps = 0
         while True:
-            one_step()
+            fn()
             reps += 1
             el = time.perf_counter() - t0
-            if el >= target or reps >= 2000:
+            if el >= target:
                 return reps, el
 
-    reps, el = timed(target_s)
-    nthreads_all = threads
-    threads = 1
-    reps1, el1 = timed(target_s / 3)
-    threads = nthreads_all
+    def run(parts, m, nthreads, target, row_frac=1.0):
+        """parts: [(triple, k)]; returns (reps, seconds, bytes per rep, flops per rep)."""
+        work = [(rows(tri, max(16, int(tri[0].shape[0] * row_frac))), k) for tri, k in parts]
+        outs = [np.empty((m, t[0].shape[0]), np.float32) for t, _ in work]
+
+        def fn():
+            for (t, k), o in zip(work, outs):
+                C.qmm_f32(xs[(m, k)], *t, threads=nthreads, out=o)
+
+        reps, el = timed(fn, target * scale)
+        nb = sum(algo_bytes(m, t[0].shape[0], k) for t, k in work)
+        fl = sum(algo_flops(m, t[0].shape[0], k) for t, k in work)
+        return reps, el, nb, fl
+
+    layer = [(host[name], k) for name, _, k in LAYER]
+    cases = [("config1_gemv_m1", [(host["gate_proj"], HIDDEN)], 1, 2.0, 1.0, 1.0, "GB/s"),
+             ("config2_layer_m1", layer, 1, 4.0, 2.0, 1.0, "GB/s"),
+             ("config3_prefill_m512", layer, 512, 4.0, 2.0, 1 / 32, "GFLOP/s")]
+    if lm_triple is not None:
+        cases.insert(2, ("config4_lm_head_m1", [(lm_triple, HIDDEN)], 1, 3.0, 1.5, 1 / 16, "GB/s"))
+    out = {}
+    for name, parts, m, t_all, t_one, frac_one, unit in cases:
+        res = {}
+        for label, nthr, target, frac in (("all_threads", threads, t_all, 1.0), ("one_thread", 1, t_one, frac_one)):
+            reps, el, nb, fl = run(parts, m, nthr, target, frac)
+            rate = nb * reps / el / 1e9 if unit == "GB/s" else fl * reps / el / 1e9
+            res[label] = {"value": round(rate, 3), "reps": reps, "seconds": round(el, 2),
+                          "rows_fraction": frac}
+        res["unit"] = unit
+        out[name] = res
+    head = out["config2_layer_m1"]["all_threads"]
     return {
-        "value": round(step_bytes * reps / el / 1e9, 3),
+        "value": head["value"],
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{reps} decoder-layer steps (7 projections, M=1) in {el:.1f} s; C restatement of the "
-                  f"fp32 dequantize-and-dot loop (oracle/q4_oracle.c), OpenMP over rows, {threads} threads",
-        "value_1_core": round(step_bytes * reps1 / el1 / 1e9, 3),
-        "sample_1_core": f"{reps1} of the same steps in {el1:.1f} s on 1 thread",
+        "sample": f"{head['reps']} decoder-layer steps (7 projections, M=1) in {head['seconds']} s on {threads} "
+                  "threads; C restatement of the fp32 dequantize-and-dot loop (oracle/q4_oracle.c), OpenMP over "
+                  "rows; 1-thread and other configurations under 'configs'",
+        "cpu_model": cpu_model(),
+        "threads_source": "OMP_NUM_THREADS" if env_threads.isdigit() else "os.cpu_count()",
         "host_cpus": os.cpu_count(),
+        "configs": out,
     }
+
+
+# the real 12B's full-attention layers (native_model.cc:795-798, :820-827): q 3840 -> 8192,
+# k 3840 -> 512 (no v_proj: k doubles as v), o 8192 -> 3840
+FULL_ATTENTION = [("full_q_proj", 8192, 3840), ("full_k_proj", 512, 3840), ("full_o_proj", 3840, 8192)]
+
+
+def prefill_sweep(torch, Q, host, ms, shapes, pair: bool, full_attention: bool) -> dict:
+    """Prefill GEMM lines: each projection of `shapes` (and, optionally, the gate|up
+    GeGLU pair and the full-attention shapes) at every M of ms, graph-replayed after a
+    wall-time settle; activations N(0, 1) with 1% outliers x20."""
+    out = {}
+    extra = {}
+    if full_attention:
+        for i, (name, n, k) in enumerate(FULL_ATTENTION):
+            extra[name] = synthetic_weights(n, k, SEED_BASE + 6000 + i)
+    all_shapes = list(shapes) + (list(FULL_ATTENTION) if full_attention else [])
+    for m in ms:
+        xk = {k: torch.from_numpy(synthetic_activations(m, k, seed=SEED_BASE + 2 + k, outliers=True).view(np.int16))
+              .view(torch.bfloat16).cuda() for k in {k for _, _, k in all_shapes}}
+        for name, n, k in all_shapes:
+            ym = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+            lin = Q.QuantizedLinear(*(host[name] if name in host else extra[name]))
+            ms_ = graph_ms_steady(torch, lambda: lin.forward(xk[k], out=ym))
+            lin.close()
+            tflops = algo_flops(m, n, k) / (ms_ * 1e-3) / 1e12
+            out[f"{name}_m{m}"] = {"us": round(ms_ * 1e3, 1), "TFLOPS": round(tflops, 1),
+                                   "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
+            del ym
+        if pair:  # the GeGLU pair: gate and up in one GEMM, h = geglu(gate, up)
+            f, k = 15360, HIDDEN
+            hm = torch.empty((m, f), dtype=torch.bfloat16, device="cuda")
+            pr = Q.QuantizedGeGLU(host["gate_proj"], host["up_proj"])
+            ms_ = graph_ms_steady(torch, lambda: pr.forward(xk[k], out=hm))
+            pr.close()
+            tflops = algo_flops(m, 2 * f, k) / (ms_ * 1e-3) / 1e12
+            out[f"{PAIR}_m{m}"] = {"us": round(ms_ * 1e3, 1), "TFLOPS": round(tflops, 1),
+                                   "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
+            del hm
+        del xk
+    return out
 
 
 def main() -> int:
@@ -461,13 +675,23 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="headline only (skip the per-shape sweeps)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="the headline prefill GEMM (gate_proj, M=2048) only, one JSON line (for rocprofv3)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="the prefill GEMM sweep only (the seven projections at M = 256, 512, 2048 and the "
+                         "full-attention shapes), one JSON line (for rocprofv3 kernel traces)")
+    ap.add_argument("--settle-ms", type=float, default=100.0,
+                    help="untimed wall time of headline replays after the warm-up replays (the clock ramps)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="time only the dominant kernel and a 1 GiB copy (the program rocprofv3 passes run)")
     ap.add_argument("--summarize-profiles", nargs=5, metavar=("STATS_DIR", "FETCH_DIR", "WRITE_DIR", "LINE", "CMD"),
                     help="write the profiles/ summaries from rocprofv3 output over --roofline-only (no GPU)")
+    ap.add_argument("--summarize-trace", nargs=3, metavar=("RESULTS_DB", "OUT_MD", "CMD"),
+                    help="write a per-shape summary of a rocprofv3 kernel trace of --prefill-only (no GPU)")
     args = ap.parse_args()
     if args.summarize_profiles:
         summarize_profiles(*args.summarize_profiles)
+        return 0
+    if args.summarize_trace:
+        summarize_trace(*args.summarize_trace)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -516,6 +740,11 @@ def main() -> int:
                           "TFLOPS": round(algo_flops(2048, n_g, k_g) / (ms * 1e-3) / 1e12, 1)}), flush=True)
         return 0
 
+    if args.prefill_only:
+        print(json.dumps(prefill_sweep(torch, Q, host, PREFILL_MS, LAYER, pair=True, full_attention=True)),
+              flush=True)
+        return 0
+
     if args.roofline_only:
         us_gu = pair_us(1)
         cgbs = copy_gbs(torch)
@@ -539,13 +768,15 @@ def main() -> int:
         return fn
 
     # --- headline: one decoder layer's projections at M=1 (4 launches), graph-replayed ---
-    log(f"timing decode step M=1 ({args.warmup} warmup + {args.steps} timed replays)")
-    ms_step = graph_ms(torch, step_fn(1), args.steps, args.warmup) / copies
+    log(f"timing decode step M=1 ({args.warmup} warmup replays, {args.settle_ms:.0f} ms settle, "
+        f"{args.steps} timed replays)")
+    settle_info = {}
+    ms_step = graph_ms(torch, step_fn(1), args.steps, args.warmup, settle_ms=args.settle_ms, info=settle_info) / copies
     step_bytes = sum(algo_bytes(1, n, k) for _, n, k in LAYER)
     value = step_bytes / (ms_step * 1e-3) / 1e9
     step_by_m = {}
     for m in ((4, 8) if not args.quick else ()):
-        ms_m = graph_ms(torch, step_fn(m), max(10, args.steps // 4), 2) / copies
+        ms_m = graph_ms(torch, step_fn(m), max(10, args.steps // 4), 2, settle_ms=50.0) / copies
         step_by_m[f"m{m}"] = {"ms_per_step": round(ms_m, 5),
                               "GBps": round(sum(algo_bytes(m, n, k) for _, n, k in LAYER) / (ms_m * 1e-3) / 1e9, 1)}
     for lin_set in layers:
@@ -571,8 +802,18 @@ def main() -> int:
     if traffic_rec is not None:
         roofline["traffic_source"] = traffic_rec.get("source")
 
+    # --- config 1: the single GEMV (x [1, 3840], W [15360, 3840]) ---
+    n1, k1 = dims["gate_proj"]
+    us1 = kernel_us(torch, lambda: Q.QuantizedLinear(*host["gate_proj"]), 1, k1, n1, xs[k1],
+                    n1 * k1 // 2 + 4 * n1 * (k1 // 64))
+    gbs1 = algo_bytes(1, n1, k1) / (us1 * 1e-6) / 1e9
+    gemv1 = {"shape": f"x [1, {k1}] . W[{n1}, {k1}]^T (gate_proj), 4-bit group 64, bf16 y", "us": round(us1, 2),
+             "GBps": round(gbs1, 1), "frac_hbm_peak": round(gbs1 / HBM_PEAK_GBS, 4),
+             "algo_bytes": algo_bytes(1, n1, k1)}
+
     per_proj = {}
     lm = None
+    lm_triple = None
     if not args.quick:
         for m in (1, 4, 8):
             for name, n, k in LAYER:
@@ -593,46 +834,29 @@ def main() -> int:
                 us = kernel_us(torch, lambda: Q.QuantizedLinear(*lm_triple), m, HIDDEN, 262144, xs[HIDDEN],
                                262144 * HIDDEN // 2 + 4 * 262144 * (HIDDEN // 64), reps_per_graph=4)
                 lm[f"m{m}"] = {"us": round(us, 1), "GBps": round(algo_bytes(m, 262144, HIDDEN) / (us * 1e-6) / 1e9, 1)}
-            del lm_triple
         except Exception as e:  # memory or build problems should not hide the headline
             lm = {"error": str(e)}
 
-    # --- prefill GEMM: the seven projections at M = 512, 2048 (gate at M=2048 headlines) ---
+    # --- prefill GEMM: the seven projections at M = 256, 512, 2048 (gate at M=2048 headlines) ---
     gemm = None
     peaks = None
     if not args.no_gemm:
-        gemm = {}
-        shapes = LAYER if not args.quick else [l for l in LAYER if l[0] == "gate_proj"]
-        for m in ((512, 2048) if not args.quick else (2048,)):
-            xk = {k: torch.from_numpy(synthetic_activations(m, k, seed=SEED_BASE + 2 + k, outliers=True).view(np.int16))
-                  .view(torch.bfloat16).cuda() for k in {k for _, _, k in shapes}}
-            for name, n, k in shapes:
-                ym = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-                lin = Q.QuantizedLinear(*host[name])
-                ms = graph_ms_steady(torch, lambda: lin.forward(xk[k], out=ym))
-                lin.close()
-                tflops = algo_flops(m, n, k) / (ms * 1e-3) / 1e12
-                gemm[f"{name}_m{m}"] = {"us": round(ms * 1e3, 1), "TFLOPS": round(tflops, 1),
-                                        "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
-                del ym
-            if not args.quick:  # the GeGLU pair: gate and up in one GEMM, h = geglu(gate, up)
-                hm = torch.empty((m, f_gu), dtype=torch.bfloat16, device="cuda")
-                pair = Q.QuantizedGeGLU(host["gate_proj"], host["up_proj"])
-                ms = graph_ms_steady(torch, lambda: pair.forward(xk[k_gu], out=hm))
-                pair.close()
-                tflops = algo_flops(m, 2 * f_gu, k_gu) / (ms * 1e-3) / 1e12
-                gemm[f"{PAIR}_m{m}"] = {"us": round(ms * 1e3, 1), "TFLOPS": round(tflops, 1),
-                                        "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
-                del hm
-            del xk
+        if args.quick:
+            gemm = prefill_sweep(torch, Q, host, (2048,), [l for l in LAYER if l[0] == "gate_proj"], pair=False,
+                                 full_attention=False)
+        else:
+            gemm = prefill_sweep(torch, Q, host, (256, 512, 2048), LAYER, pair=True, full_attention=True)
         head = gemm["gate_proj_m2048"]
         gemm["headline"] = {"shape": "gate_proj M=2048 N=15360 K=3840", **head}
         if not args.quick:
-            log("practical peaks: 1 GiB copy, dense bf16 GEMM (hipBLASLt) on the gate shape")
+            log("practical peaks: 1 GiB copy, 1 GiB read, dense bf16 GEMM (hipBLASLt) on the gate shape")
             dense = dense_gemm_tflops(torch, 2048, 15360, HIDDEN)
             cg = copy_gbs(torch)
-            peaks = {"copy_GBps": round(cg, 1), "dense_bf16_gemm_TFLOPS_gate_m2048": round(dense, 1),
-                     "roofline_frac_of_copy": round(gu_gbs / cg, 4),
+            rd = read_gbs(torch)
+            peaks = {"copy_GBps": round(cg, 1), "read_GBps": rd["GBps"], "read_probe": rd,
+                     "dense_bf16_gemm_TFLOPS_gate_m2048": round(dense, 1),
+                     "roofline_frac_of_read": round(gu_gbs / rd["GBps"], 4),
+                     "gemv_config1_frac_of_read": round(gbs1 / rd["GBps"], 4),
                      "gemm_frac_of_dense": round(head["TFLOPS"] / dense, 4)}
 
     model = None
@@ -646,7 +870,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log("CPU baseline")
-        cpu = cpu_baseline(host)
+        cpu = cpu_baseline(host, lm_triple)
 
     out = {
         "metric": METRIC,
@@ -669,6 +893,8 @@ def main() -> int:
             "weight_copies_rotated": copies,
         },
         "pct_hbm_peak": round(value / HBM_PEAK_GBS * 100, 2),
+        "headline_settle": settle_info,
+        "config1_gemv_m1": gemv1,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "decode_step_by_m": step_by_m,

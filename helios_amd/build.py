@@ -22,6 +22,9 @@ LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
 SOURCES = ["qmm_runtime.cpp", "q4_layout.hip", "q4_decode.hip", "q4_gemm.hip", "q4_lora.hip"]
 ARCH = "gfx950"
+# measurement aid for the benchmark (a read-only HBM streaming kernel), its own library
+PROBE_SOURCES = ["hbm_probe.hip"]
+PROBE_PATH = os.path.join(LIB_DIR, "libhbm_probe.so")
 
 
 def hipcc() -> str:
@@ -58,16 +61,16 @@ def device_asm(source: str) -> str:
             return f.read()
 
 
-def build(verbose: bool = False) -> str:
+def _link(sources, path: str, verbose: bool) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
+    tmp = path + ".tmp"
     cmd = [hipcc()] + DEVICE_FLAGS + [
         "-fPIC",
         "-shared",
         "-Wall",
         "-I", os.path.join(ROOT, "include"),
         "-o", tmp,
-    ] + [os.path.join(CSRC, s) for s in SOURCES]
+    ] + [os.path.join(CSRC, s) for s in sources]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -77,8 +80,14 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{errs}")
     if errs.strip() and verbose:
         print(errs, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, path)
+    return path
+
+
+def build(verbose: bool = False) -> str:
+    """Builds libgemma4_qmm.so and the benchmark's libhbm_probe.so; returns the former."""
+    _link(PROBE_SOURCES, PROBE_PATH, verbose)
+    return _link(SOURCES, LIB_PATH, verbose)
 
 
 if __name__ == "__main__":

@@ -23,9 +23,17 @@ constexpr int kGreedyMaxRows = 16;  // rows per greedy-head call (decode and ver
 constexpr uint64_t kLoraMagic = 0x47454d344c4f5241ULL;  // "GEM4LORA"
 thread_local char g_last_error[512] = "";
 
-Gemma4Status fail(Gemma4Status status, const std::string& message) {
-    std::snprintf(g_last_error, sizeof(g_last_error), "%s", message.c_str());
+// Records the message (truncated to the buffer) and returns status.  The const char*
+// forms build no std::string, so they cannot throw: catch blocks use them.
+Gemma4Status fail_nothrow(Gemma4Status status, const char* message) noexcept {
+    std::snprintf(g_last_error, sizeof(g_last_error), "%s", message);
     return status;
+}
+
+Gemma4Status fail(Gemma4Status status, const char* message) noexcept { return fail_nothrow(status, message); }
+
+Gemma4Status fail(Gemma4Status status, const std::string& message) noexcept {
+    return fail_nothrow(status, message.c_str());
 }
 
 Gemma4Status ok() {
@@ -364,18 +372,27 @@ Gemma4Status run_forward(const Gemma4QLinear* linear, void* stream, const uint16
 extern "C" {
 
 Gemma4Status gemma4_qmm_runtime_version(Gemma4QmmVersionInfo* out) {
-    if (out == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qmm_runtime_version requires a non-null out pointer");
-    out->abi_version = GEMMA4_QMM_ABI_VERSION;
-    out->backend_name = "gemma4_qmm";
-    out->backend_version = "gfx950-hip-affine-q4";
-    return ok();
+    try {
+        if (out == nullptr)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qmm_runtime_version requires a non-null out pointer");
+        out->abi_version = GEMMA4_QMM_ABI_VERSION;
+        out->backend_name = "gemma4_qmm";
+        out->backend_version = "gfx950-hip-affine-q4";
+        return ok();
+    } catch (...) {
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qmm_runtime_version: unexpected native exception");
+    }
 }
 
 Gemma4Status gemma4_qmm_get_last_error(char* buffer, size_t buffer_len) {
-    if (buffer == nullptr || buffer_len == 0)
-        return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qmm_get_last_error requires a writable buffer");
-    std::snprintf(buffer, buffer_len, "%s", g_last_error);
-    return GEMMA4_OK;
+    try {
+        if (buffer == nullptr || buffer_len == 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qmm_get_last_error requires a writable buffer");
+        std::snprintf(buffer, buffer_len, "%s", g_last_error);
+        return GEMMA4_OK;
+    } catch (...) {
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qmm_get_last_error: unexpected native exception");
+    }
 }
 
 Gemma4Status gemma4_qlinear_create(const Gemma4QLinearDesc* desc, const uint32_t* weight,
@@ -389,7 +406,7 @@ Gemma4Status gemma4_qlinear_create(const Gemma4QLinearDesc* desc, const uint32_t
             return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_create requires non-null weight, scales and biases");
         return create_from_host(desc, &weight, &scales, &biases, 1, "gemma4_qlinear_create", out);
     } catch (...) {
-        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_create: unexpected native exception");
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_create: unexpected native exception");
     }
 }
 
@@ -408,7 +425,7 @@ Gemma4Status gemma4_qlinear_create_device(const Gemma4QLinearDesc* desc, const u
         return create_from_device(desc, Triple{weight_dev, scales_dev, biases_dev}, nullptr, stream,
                                   "gemma4_qlinear_create_device", out);
     } catch (...) {
-        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_create_device: unexpected native exception");
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_create_device: unexpected native exception");
     }
 }
 
@@ -428,7 +445,7 @@ Gemma4Status gemma4_qgeglu_create(const Gemma4QLinearDesc* desc, const uint32_t*
         const uint16_t* b[2] = {gate_biases, up_biases};
         return create_from_host(desc, w, s, b, 2, "gemma4_qgeglu_create", out);
     } catch (...) {
-        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qgeglu_create: unexpected native exception");
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qgeglu_create: unexpected native exception");
     }
 }
 
@@ -450,32 +467,42 @@ Gemma4Status gemma4_qgeglu_create_device(const Gemma4QLinearDesc* desc, const ui
         return create_from_device(desc, Triple{gate_weight_dev, gate_scales_dev, gate_biases_dev}, &up, stream,
                                   "gemma4_qgeglu_create_device", out);
     } catch (...) {
-        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qgeglu_create_device: unexpected native exception");
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qgeglu_create_device: unexpected native exception");
     }
 }
 
 Gemma4Status gemma4_qlinear_free(Gemma4QLinear* linear) {
-    if (linear == nullptr) return ok();
-    if (!valid_handle(linear)) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_free received an invalid handle");
-    DeviceGuard guard;
-    (void)guard.enter(linear->device);
-    release(linear);
-    delete linear;
-    return ok();
+    try {
+        if (linear == nullptr) return ok();
+        if (!valid_handle(linear))
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_free received an invalid handle");
+        DeviceGuard guard;
+        (void)guard.enter(linear->device);
+        release(linear);
+        delete linear;
+        return ok();
+    } catch (...) {
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_free: unexpected native exception");
+    }
 }
 
 Gemma4Status gemma4_qlinear_info(const Gemma4QLinear* linear, Gemma4QLinearInfo* out) {
-    if (out == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_info requires a non-null out pointer");
-    if (!valid_handle(linear)) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_info received an invalid handle");
-    std::memset(out, 0, sizeof(*out));
-    out->out_features = linear->desc.out_features;
-    out->in_features = linear->desc.in_features;
-    out->bits = linear->desc.bits;
-    out->group_size = linear->desc.group_size;
-    out->device_bytes = linear->layout.tile_bytes() + linear->layout.sb_bytes();
-    out->device = linear->device;
-    out->flags = linear->pair_rows ? GEMMA4_QLINEAR_GEGLU_PAIR : 0u;
-    return ok();
+    try {
+        if (out == nullptr) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_info requires a non-null out pointer");
+        if (!valid_handle(linear))
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_info received an invalid handle");
+        std::memset(out, 0, sizeof(*out));
+        out->out_features = linear->desc.out_features;
+        out->in_features = linear->desc.in_features;
+        out->bits = linear->desc.bits;
+        out->group_size = linear->desc.group_size;
+        out->device_bytes = linear->layout.tile_bytes() + linear->layout.sb_bytes();
+        out->device = linear->device;
+        out->flags = linear->pair_rows ? GEMMA4_QLINEAR_GEGLU_PAIR : 0u;
+        return ok();
+    } catch (...) {
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_info: unexpected native exception");
+    }
 }
 
 Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
@@ -483,7 +510,7 @@ Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, c
     try {
         return run_forward(linear, stream, x_dev, rows, y_dev, y_dtype, false, "gemma4_qlinear_forward");
     } catch (...) {
-        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward: unexpected native exception");
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward: unexpected native exception");
     }
 }
 
@@ -492,7 +519,7 @@ Gemma4Status gemma4_qgeglu_forward(const Gemma4QLinear* pair, void* stream, cons
     try {
         return run_forward(pair, stream, x_dev, rows, h_dev, h_dtype, true, "gemma4_qgeglu_forward");
     } catch (...) {
-        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qgeglu_forward: unexpected native exception");
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qgeglu_forward: unexpected native exception");
     }
 }
 
@@ -551,7 +578,7 @@ Gemma4Status gemma4_qlinear_forward_greedy(const Gemma4QLinear* linear, void* st
         if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);
         return ok();
     } catch (...) {
-        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward_greedy: unexpected native exception");
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward_greedy: unexpected native exception");
     }
 }
 
@@ -589,20 +616,25 @@ Gemma4Status gemma4_qlora_create(const float* a, const float* b, uint32_t rank, 
         *out = h;
         return ok();
     } catch (...) {
-        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlora_create: unexpected native exception");
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlora_create: unexpected native exception");
     }
 }
 
 Gemma4Status gemma4_qlora_free(Gemma4QLora* lora) {
-    if (lora == nullptr) return ok();
-    if (lora->magic != kLoraMagic) return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlora_free received an invalid handle");
-    DeviceGuard guard;
-    (void)guard.enter(lora->device);
-    (void)hipFree(lora->a);
-    (void)hipFree(lora->b);
-    lora->magic = 0;
-    delete lora;
-    return ok();
+    try {
+        if (lora == nullptr) return ok();
+        if (lora->magic != kLoraMagic)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlora_free received an invalid handle");
+        DeviceGuard guard;
+        (void)guard.enter(lora->device);
+        (void)hipFree(lora->a);
+        (void)hipFree(lora->b);
+        lora->magic = 0;
+        delete lora;
+        return ok();
+    } catch (...) {
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlora_free: unexpected native exception");
+    }
 }
 
 Gemma4Status gemma4_qlinear_forward_lora(const Gemma4QLinear* linear, const Gemma4QLora* lora, void* stream,
@@ -638,7 +670,7 @@ Gemma4Status gemma4_qlinear_forward_lora(const Gemma4QLinear* linear, const Gemm
         if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);
         return ok();
     } catch (...) {
-        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward_lora: unexpected native exception");
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward_lora: unexpected native exception");
     }
 }
 
@@ -669,7 +701,7 @@ Gemma4Status gemma4_qlinear_embed(const Gemma4QLinear* linear, void* stream, con
         if (e != hipSuccess) return hip_fail((name + ": launch").c_str(), e);
         return ok();
     } catch (...) {
-        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_embed: unexpected native exception");
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_embed: unexpected native exception");
     }
 }
 
@@ -692,7 +724,7 @@ Gemma4Status gemma4_qlinear_dequantize(const Gemma4QLinear* linear, void* stream
         if (e != hipSuccess) return hip_fail("gemma4_qlinear_dequantize: launch", e);
         return ok();
     } catch (...) {
-        return fail(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_dequantize: unexpected native exception");
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_dequantize: unexpected native exception");
     }
 }
 

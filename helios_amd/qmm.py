@@ -222,6 +222,14 @@ class _Handle:
         check(self._lib.gemma4_qlinear_info(self._handle, ctypes.byref(info)), self._lib)
         return {f: getattr(info, f) for f, _ in _Info._fields_}
 
+    @property
+    def device(self):
+        """The torch device that holds the handle's weights (outputs allocated by
+        this object go there, whatever the current device is)."""
+        import torch
+
+        return torch.device("cuda", self.info()["device"])
+
     def close(self) -> None:
         if getattr(self, "_handle", None) is not None and self._handle.value:
             check(self._lib.gemma4_qlinear_free(self._handle), self._lib)
@@ -329,7 +337,7 @@ class QuantizedLinear(_Handle):
     def dequantize(self, stream=None):
         import torch
 
-        out = torch.empty((self.out_features, self.in_features), dtype=torch.float32, device="cuda")
+        out = torch.empty((self.out_features, self.in_features), dtype=torch.float32, device=self.device)
         check(self._lib.gemma4_qlinear_dequantize(self._handle, _stream_ptr(stream), _dev_ptr(out)), self._lib)
         return out
 
@@ -386,7 +394,7 @@ class QuantizedGeGLU(_Handle):
         """fp32 [2, F, K]: the gate rows, then the up rows (bit-exact)."""
         import torch
 
-        out = torch.empty((2, self.out_features, self.in_features), dtype=torch.float32, device="cuda")
+        out = torch.empty((2, self.out_features, self.in_features), dtype=torch.float32, device=self.device)
         check(self._lib.gemma4_qlinear_dequantize(self._handle, _stream_ptr(stream), _dev_ptr(out)), self._lib)
         return out
 

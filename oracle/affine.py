@@ -36,13 +36,28 @@ BITS = 4
 # ---------------------------------------------------------------------------
 
 def f32_to_bf16_bits(a) -> np.ndarray:
-    """fp32 -> bf16 bit patterns (uint16), round-to-nearest-even, NaN kept quiet."""
-    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x007FFFFF) != 0)
-    lsb = (u >> 16) & 1
-    r = ((u + 0x7FFF + lsb) >> 16).astype(np.uint16)
-    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    """fp32 -> bf16 bit patterns (uint16), round-to-nearest-even, NaN kept quiet.
+
+    In uint32: u + 0x7FFF + lsb cannot wrap for a finite or infinite u (at most
+    0xFF800000 + 0x8000); NaNs, which could, are replaced afterwards."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    r = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+    nan = (u & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+    if nan.any():
+        r[nan] = ((u[nan] >> np.uint32(16)) | np.uint32(0x40)).astype(np.uint16)
     return r
+
+
+def f64_to_bf16_bits(a) -> np.ndarray:
+    """float64 -> bf16 bit patterns with ONE round-to-nearest-even (going through
+    float32 first would round twice: a value just above a bf16 midpoint can land on
+    the midpoint in float32 and then tie to even the other way).  Finite values in
+    the normal bf16 range."""
+    u = np.ascontiguousarray(a, dtype=np.float64).view(np.uint64)
+    drop = np.uint64(45)  # 52 - 7 fraction bits
+    lsb = (u >> drop) & np.uint64(1)
+    r = (u + np.uint64((1 << 44) - 1) + lsb) & ~np.uint64((1 << 45) - 1)
+    return (r.view(np.float64).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
 
 
 def bf16_bits_to_f32(b) -> np.ndarray:
@@ -166,6 +181,27 @@ def check_bf16_output(y_bits, y_exact, rel: float = 1e-2):
     return worst <= bound + 1e-30, (worst / rms if rms > 0 else worst)
 
 
+def check_bf16_rounding(y_bits, y_exact, acc_rel: float = 1e-4):
+    """The tighter property of a bf16 output computed by fp32 accumulation of exact
+    products: each output is the round-to-nearest-even of some value within
+    acc_rel * RMS(y_exact) of the exact result, i.e.
+        |y - y_exact| <= ulp_bf16(y)/2 + acc_rel * RMS(y_exact)
+    (values that round to y lie within half an ulp of y, also at a binade edge).
+    Wherever the accumulation error stays below the distance to the nearest
+    rounding boundary, y equals RNE(y_exact) exactly.  Returns (ok, worst excess
+    over ulp(y)/2 as a fraction of RMS, fraction of outputs equal to RNE(y_exact))."""
+    y_bits = np.asarray(y_bits, dtype=np.uint16)
+    y = bf16_bits_to_f32(y_bits).astype(np.float64)
+    y_exact = np.asarray(y_exact, dtype=np.float64)
+    if not y.size:
+        return True, 0.0, 1.0
+    rms = float(np.sqrt(np.mean(y_exact ** 2)))
+    excess = np.abs(y - y_exact) - 0.5 * bf16_ulp(y)
+    worst = float(excess.max())
+    equal = float(np.mean(f64_to_bf16_bits(y_exact) == y_bits))
+    return worst <= acc_rel * rms + 1e-30, (worst / rms if rms > 0 else worst), equal
+
+
 def check_f32_output(y, y_exact, rel: float = 2e-3):
     """fp32 output: max |y - y_exact| <= rel * RMS(y_exact).  Returns (ok, max_err/rms)."""
     y = np.asarray(y, dtype=np.float64)
@@ -180,11 +216,21 @@ def check_f32_output(y, y_exact, rel: float = 2e-3):
 # ---------------------------------------------------------------------------
 
 def make_weights(n: int, k: int, seed: int, std: float = 0.02, group_size: int = GROUP_SIZE,
-                 bits: int = BITS):
-    """W ~ N(0, std) in fp32, rounded to bf16 (how bf16 checkpoints arise), then quantized."""
+                 bits: int = BITS, chunk_rows: int = 8192):
+    """W ~ N(0, std) in fp32, rounded to bf16 (how bf16 checkpoints arise), then quantized.
+
+    Generated and quantized `chunk_rows` rows at a time (quantization is per row, and
+    the generator's stream continues across calls), which bounds the temporaries of a
+    262144-row weight; the result equals one whole-matrix pass."""
     rng = np.random.Generator(np.random.PCG64(seed))
-    w = rng.standard_normal((n, k), dtype=np.float32) * np.float32(std)
-    return quantize(round_to_bf16(w), group_size, bits)
+    wq = np.empty((n, k * bits // 32), np.uint32)
+    s = np.empty((n, k // group_size), np.uint16)
+    b = np.empty((n, k // group_size), np.uint16)
+    for r0 in range(0, n, chunk_rows):
+        r1 = min(n, r0 + chunk_rows)
+        w = rng.standard_normal((r1 - r0, k), dtype=np.float32) * np.float32(std)
+        wq[r0:r1], s[r0:r1], b[r0:r1] = quantize(round_to_bf16(w), group_size, bits)
+    return wq, s, b
 
 
 def make_activations(m: int, k: int, seed: int, outliers: bool = False) -> np.ndarray:

@@ -126,30 +126,35 @@ int oracle_qmm_f64(const uint16_t* x, int64_t m, int64_t k, const uint32_t* wq,
     if (!x || !wq || !scales || !biases || !y || m < 0 || !valid_shape(n, k, group, bits)) return -1;
     const int64_t words_per_row = k * bits / 32;
     const int64_t groups_per_row = k / group;
-    double* wrow = (double*)malloc((size_t)k * sizeof(double));
     double* xrow = (double*)malloc((size_t)(k * (m > 0 ? m : 1)) * sizeof(double));
-    if (!wrow || !xrow) {
-        free(wrow);
-        free(xrow);
-        return -1;
-    }
+    if (!xrow) return -1;
     for (int64_t i = 0; i < m * k; ++i) xrow[i] = (double)oracle_bf16_to_f32(x[i]);
-    for (int64_t r = 0; r < n; ++r) {
-        for (int64_t c = 0; c < k; ++c) {
-            const double s = (double)oracle_bf16_to_f32(scales[r * groups_per_row + c / group]);
-            const double b = (double)oracle_bf16_to_f32(biases[r * groups_per_row + c / group]);
-            wrow[c] = s * (double)q_at(wq, words_per_row, r, c, bits) + b;
+    int failed = 0;
+    /* Rows of W are independent and each output is summed in column order by one
+     * thread, so the result does not depend on the thread count. */
+#pragma omp parallel reduction(| : failed)
+    {
+        double* wrow = (double*)malloc((size_t)k * sizeof(double));
+        if (!wrow) failed = 1;
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < n; ++r) {
+            if (!wrow) continue;
+            for (int64_t c = 0; c < k; ++c) {
+                const double s = (double)oracle_bf16_to_f32(scales[r * groups_per_row + c / group]);
+                const double b = (double)oracle_bf16_to_f32(biases[r * groups_per_row + c / group]);
+                wrow[c] = s * (double)q_at(wq, words_per_row, r, c, bits) + b;
+            }
+            for (int64_t i = 0; i < m; ++i) {
+                double acc = 0.0;
+                const double* xi = xrow + i * k;
+                for (int64_t c = 0; c < k; ++c) acc += xi[c] * wrow[c];
+                y[i * n + r] = acc;
+            }
         }
-        for (int64_t i = 0; i < m; ++i) {
-            double acc = 0.0;
-            const double* xi = xrow + i * k;
-            for (int64_t c = 0; c < k; ++c) acc += xi[c] * wrow[c];
-            y[i * n + r] = acc;
-        }
+        free(wrow);
     }
-    free(wrow);
     free(xrow);
-    return 0;
+    return failed ? -1 : 0;
 }
 
 int oracle_max_threads(void) {

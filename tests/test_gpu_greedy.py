@@ -17,7 +17,7 @@ import pytest
 
 from oracle import affine as A
 from oracle import c_oracle as C
-from test_gpu_parity import BF16_REL, F32_REL, dev_triple, dev_x, host_bits, random_triple
+from test_gpu_parity import BF16_REL, F32_REL, dev_triple, dev_x, host_bits, lm_head_triple, random_triple
 
 pytestmark = pytest.mark.gpu
 
@@ -91,19 +91,31 @@ def test_greedy_ties_go_to_the_lowest_index(gpu_lib):
     lin.close()
 
 
-def test_greedy_lm_head_full_vocab(gpu_lib):
+@pytest.mark.parametrize("m", [1, 8, 16])
+@pytest.mark.parametrize("f32", [False, True])
+def test_greedy_lm_head_full_vocab(gpu_lib, m, f32):
+    """The full 262144-token head at decode (M = 1) and verify blocks (M = 8, 16; the
+    four-chunks-in-flight decode kernel): logits, values and tokens against the
+    oracle, with and without returning the logits."""
     import torch
 
-    n, k = 262144, 3840
-    wq, s, b = A.make_weights(n, k, seed=20260630 + 3000)
-    x = A.make_activations(1, k, seed=33)
+    wq, s, b = lm_head_triple()
+    x = A.make_activations(m, 3840, seed=33 + m)
     lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
-    tok, val, logits = lin.forward_greedy(dev_x(x), softcap=30.0, return_logits=True)
+    dt = torch.float32 if f32 else torch.bfloat16
+    tok, val, logits = lin.forward_greedy(dev_x(x), softcap=30.0, out_dtype=dt, return_logits=True)
+    tok2, val2, _ = lin.forward_greedy(dev_x(x), softcap=30.0, out_dtype=dt)
     torch.cuda.synchronize()
-    sc = _oracle(x, (wq, s, b), 30.0, True)
-    ok, worst = A.check_bf16_output(host_bits(logits), sc, BF16_REL)
-    assert ok, f"lm_head logits: worst error / RMS = {worst:.3e}"
-    _check_token(tok.cpu().numpy(), sc, bf16=True)
+    sc = _oracle(x, (wq, s, b), 30.0, bf16=not f32)
+    lg = host_bits(logits)
+    ok, worst = (A.check_f32_output(lg, sc, F32_REL) if f32 else A.check_bf16_output(lg, sc, BF16_REL))
+    assert ok, f"lm_head m={m} logits: worst error / RMS = {worst:.3e}"
+    tok, val = tok.cpu().numpy(), val.cpu().numpy()
+    assert np.array_equal(tok, tok2.cpu().numpy()) and np.array_equal(val.view(np.uint32),
+                                                                      val2.cpu().numpy().view(np.uint32))
+    lgf = lg if f32 else A.bf16_bits_to_f32(lg)
+    assert np.array_equal(val, lgf[np.arange(m), tok])
+    _check_token(tok, sc, bf16=not f32)
     lin.close()
 
 

@@ -7,8 +7,19 @@ Bars (written here, applied in every test below):
     (the half ulp is the rounding any bf16 output makes);
   where y_exact is the oracle's float64 accumulation of exact products.
 The kernel's own error is far below these bars (fp32 accumulation of exact
-products); the tests also report the measured ratio.
+products), so the decode and prefill projection tests also assert the tighter
+property the kernels have:
+  * bf16 output: each output is the round-to-nearest-even of a value within
+    ACC_REL * RMS(y_exact) of y_exact (A.check_bf16_rounding), and at least
+    RNE_FRAC of the outputs equal RNE(y_exact) exactly (a truncating or otherwise
+    wrong rounding would match about half);
+  * where the correctly rounded outputs themselves meet north_star's literal bar
+    max |y - y_exact| <= 1e-2 * RMS (no half-ulp allowance), the kernel's do too
+    (decode inputs without outliers: bf16 rounding alone can exceed the literal bar
+    only when the largest output sits in a binade whose half ulp is > 1e-2 * RMS).
 """
+
+import functools
 
 import numpy as np
 import pytest
@@ -20,6 +31,11 @@ pytestmark = pytest.mark.gpu
 
 BF16_REL = 1e-2
 F32_REL = 2e-3
+ACC_REL = 1e-4   # fp32 accumulation of exact products (measured up to ~7e-5 with outliers)
+# outputs equal to the correctly rounded exact value: the rest are those within the
+# accumulation error of a rounding boundary (measured 98.4-100%; with 1% outliers x20
+# the group sums carry more of the error).  A wrong rounding mode gives about 50%.
+RNE_FRAC = 0.95
 
 # (N, K) of the reference's projections at the benchmark configurations
 PROJ = {
@@ -70,6 +86,31 @@ def assert_close(y_dev, y_exact, what=""):
         ok, worst = A.check_f32_output(host_bits(y_dev), y_exact, F32_REL)
     assert ok, f"{what}: worst error / RMS = {worst:.3e}"
     return worst
+
+
+def assert_rounded(y_dev, y_exact, what="", literal=False):
+    """bf16 output: one rounding of a value within ACC_REL * RMS of the exact result,
+    RNE(exact) on at least RNE_FRAC of the outputs; with `literal`, north_star's
+    max |err| <= 1e-2 * RMS wherever RNE(exact) itself meets it."""
+    y = host_bits(y_dev)
+    ok, worst, equal = A.check_bf16_rounding(y, y_exact, ACC_REL)
+    assert ok, f"{what}: error beyond ulp/2 = {worst:.3e} x RMS"
+    assert equal >= RNE_FRAC, f"{what}: only {equal:.4%} of outputs equal RNE(exact)"
+    if literal:
+        y_exact = np.asarray(y_exact, np.float64)
+        rms = float(np.sqrt(np.mean(y_exact ** 2)))
+        rne_err = float(np.max(np.abs(A.bf16_bits_to_f32(A.f64_to_bf16_bits(y_exact)) - y_exact)))
+        err = float(np.max(np.abs(A.bf16_bits_to_f32(y).astype(np.float64) - y_exact)))
+        if rne_err <= BF16_REL * rms:
+            assert err <= BF16_REL * rms, f"{what}: literal bar: max |err| = {err / rms:.3e} x RMS"
+    return equal
+
+
+@functools.lru_cache(maxsize=1)
+def lm_head_triple():
+    """The lm_head weight triple (262144 x 3840, W ~ N(0, 0.02) quantized), built once
+    per test process."""
+    return A.make_weights(262144, 3840, seed=20260630 + 3000)
 
 
 @pytest.mark.parametrize("n,k", [(16, 64), (48, 128), (40, 192), (33, 640), (4096, 3840)])
@@ -144,21 +185,53 @@ def test_forward_decode_projections(gpu_lib, proj, m):
     torch.cuda.synchronize()
     y_exact = C.qmm_f64(x, wq, s, b)
     assert_close(y_bf, y_exact, f"{proj} m={m} bf16")
+    assert_rounded(y_bf, y_exact, f"{proj} m={m} bf16", literal=True)
     worst = assert_close(y_f32, y_exact, f"{proj} m={m} f32")
-    assert worst < 1e-4  # exact products + fp32 accumulation: far inside the bar
+    assert worst < ACC_REL  # exact products + fp32 accumulation: far inside the bar
     lin.close()
 
 
-def test_lm_head_decode(gpu_lib):
+@pytest.mark.parametrize("m", [1, 8, 16])
+def test_lm_head_decode_and_verify(gpu_lib, m):
+    """The lm_head (262144 x 3840) at decode M = 1 and at the verify blocks M = 8 and
+    16 (native_model.cc:1782-1795, called at :2006 with the block of
+    gemma4_mlx.h:77-79), bf16 and fp32 logits against the oracle on every output.
+    At M = 8 and 16 one workgroup fits a CU and each walks 64 row blocks: the
+    decode kernel with four chunks per wave in flight."""
     import torch
 
-    n, k = 262144, 3840
-    wq, s, b = A.make_weights(n, k, seed=20260630 + 3000)
-    x = A.make_activations(1, k, seed=31)
+    wq, s, b = lm_head_triple()
+    x = A.make_activations(m, 3840, seed=31 + m)
     lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
-    y = lin.forward(dev_x(x))
+    xd = dev_x(x)
+    y_bf = lin.forward(xd)
+    y_f = lin.forward(xd, out_dtype=torch.float32)
     torch.cuda.synchronize()
-    assert_close(y, C.qmm_f64(x, wq, s, b), "lm_head m=1")
+    y_exact = C.qmm_f64(x, wq, s, b)
+    assert_close(y_bf, y_exact, f"lm_head m={m} bf16")
+    assert_rounded(y_bf, y_exact, f"lm_head m={m} bf16", literal=True)
+    assert assert_close(y_f, y_exact, f"lm_head m={m} f32") < ACC_REL
+    lin.close()
+
+
+@pytest.mark.parametrize("m,n", [(9, 70000), (16, 70000), (14, 76800), (8, 76800 + 40)])
+def test_forward_decode_four_chunks_in_flight(gpu_lib, m, n):
+    """Mid-size N at K = 3840 and M = 8-16: LDS admits one workgroup per CU and each
+    walks 17-19 row blocks, so the decode kernel keeps four chunks in flight and its
+    tail runs 1, 2 or 3 chunks after the last full round of four (4375 blocks over
+    244 workgroups of 18 or 17; 4800 over 253 of 19 or 18; a ragged last block)."""
+    import torch
+
+    k = 3840
+    wq, s, b = random_triple(n, k, seed=5150 + m)
+    x = A.make_activations(m, k, seed=5151 + m, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    y = lin.forward(dev_x(x), out_dtype=torch.float32)
+    y_bf = lin.forward(dev_x(x))
+    torch.cuda.synchronize()
+    y_exact = C.qmm_f64(x, wq, s, b)
+    assert assert_close(y, y_exact, f"m={m} n={n} f32") < ACC_REL
+    assert_rounded(y_bf, y_exact, f"m={m} n={n} bf16")
     lin.close()
 
 
@@ -280,24 +353,29 @@ def test_gemm_small_shapes(gpu_lib, n, k, m, f32):
         assert worst < 5e-4
 
 
-@pytest.mark.parametrize("proj", ["q_proj", "k_proj", "o_proj", "gate_proj", "down_proj"])
-def test_gemm_prefill_projections_m512(gpu_lib, proj):
+@pytest.mark.parametrize("proj", sorted(PROJ))
+@pytest.mark.parametrize("m", [512, 2048])
+def test_gemm_prefill_projections(gpu_lib, proj, m):
+    """Config 3's seven projections at the prefill chunks M = 512 and 2048, activations
+    with 1% outliers x20."""
     import torch
 
     n, k = PROJ[proj]
     triple = A.make_weights(n, k, seed=20260630 + 2000 + sorted(PROJ).index(proj))
-    x = A.make_activations(512, k, seed=512, outliers=True)
+    x = A.make_activations(m, k, seed=m, outliers=True)
     lin = gpu_lib.QuantizedLinear(*dev_triple(*triple))
     xd = dev_x(x)
     y_bf = lin.forward(xd)
     y_f = lin.forward(xd, out_dtype=torch.float32)
     torch.cuda.synchronize()
     # full-size prefill is too large for the float64 CPU oracle in full: sample rows
-    rows = np.random.default_rng(1).choice(512, 24, replace=False)
+    rows = np.random.default_rng(1).choice(m, 24, replace=False)
     rows.sort()
     y_exact = C.qmm_f64(np.ascontiguousarray(x[rows]), *triple)
-    assert_close(y_bf[torch.from_numpy(rows).cuda()], y_exact, f"{proj} m=512 bf16")
-    worst = assert_close(y_f[torch.from_numpy(rows).cuda()], y_exact, f"{proj} m=512 f32")
+    rt = torch.from_numpy(rows).cuda()
+    assert_close(y_bf[rt], y_exact, f"{proj} m={m} bf16")
+    assert_rounded(y_bf[rt], y_exact, f"{proj} m={m} bf16")
+    worst = assert_close(y_f[rt], y_exact, f"{proj} m={m} f32")
     assert worst < 5e-4
     # every row block of the output is written (no stale tiles): compare the f32 and
     # bf16 results everywhere, which agree to bf16 rounding

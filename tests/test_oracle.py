@@ -285,6 +285,53 @@ def test_tolerance_helpers_accept_exact_and_reject_planted_error():
     assert not A.check_bf16_output(A.f32_to_bf16_bits(bad.astype(np.float32)), y)[0]
 
 
+def test_f64_to_bf16_rounds_once():
+    """Agrees with the float32 conversion where float32 holds the value exactly, and
+    rounds a value just past a bf16 midpoint away from it (float32 first would tie
+    to even): 1 + 2^-8 + 2^-40 -> 1 + 2^-7, 1 + 2^-8 -> 1 (tie to even),
+    1 + 3 * 2^-8 -> 1 + 2^-6 (tie to even, upwards), negative values alike."""
+    v = A.bf16_bits_to_f32(np.arange(0x0080, 0x7F00, 7, dtype=np.uint16)).astype(np.float64)
+    v = np.concatenate([v, -v, v * (1 + 2.0 ** -9), v * (1 + 2.0 ** -8)])
+    assert np.array_equal(A.f64_to_bf16_bits(v), A.f32_to_bf16_bits(v.astype(np.float32)))
+    cases = {1 + 2.0 ** -8 + 2.0 ** -40: 1 + 2.0 ** -7, 1 + 2.0 ** -8: 1.0, 1 + 3 * 2.0 ** -8: 1 + 2.0 ** -6,
+             -(1 + 2.0 ** -8 + 2.0 ** -40): -(1 + 2.0 ** -7), 1 + 2.0 ** -8 - 2.0 ** -40: 1.0}
+    got = A.bf16_bits_to_f32(A.f64_to_bf16_bits(np.array(list(cases)))).astype(np.float64)
+    assert np.array_equal(got, np.array(list(cases.values())))
+    assert A.f32_to_bf16_bits(np.float32(1 + 2.0 ** -8 + 2.0 ** -40)) == 0x3F80  # the double rounding
+
+
+def test_bf16_rounding_helper_pins_one_rounding_of_a_near_exact_value():
+    """check_bf16_rounding accepts RNE(exact) and RNE(exact + small accumulation
+    error), and rejects a value rounded the wrong way on a large output (one ulp off
+    where the accumulation error cannot reach the boundary), a truncation, and an
+    error beyond acc_rel * RMS on a tiny output."""
+    rng = np.random.default_rng(19)
+    y = rng.standard_normal((4, 2000)) * 1.3
+    rms = float(np.sqrt(np.mean(y ** 2)))
+    rne = A.f64_to_bf16_bits(y)
+    ok, worst, equal = A.check_bf16_rounding(rne, y)
+    assert ok and equal == 1.0 and worst <= 0.0
+    # an accumulation error of 1e-5 RMS before the rounding: still one rounding of a
+    # near-exact value, and nearly every output equals RNE(exact)
+    noisy = A.f32_to_bf16_bits((y + rng.uniform(-1e-5, 1e-5, y.shape) * rms).astype(np.float32))
+    ok, _, equal = A.check_bf16_rounding(noisy, y)
+    assert ok and 0.99 < equal <= 1.0
+    # largest output moved one ulp: the exact value sits ~half an ulp (>> 1e-4 RMS)
+    # from where that rounding would need it
+    i = np.unravel_index(np.argmax(np.abs(y)), y.shape)
+    off = rne.copy()
+    off[i] = off[i] + 1
+    assert not A.check_bf16_rounding(off, y)[0]
+    # truncation instead of rounding: wrong on about half the outputs
+    trunc = (y.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    assert not A.check_bf16_rounding(trunc, y)[0]
+    # a tiny output carrying an error of 1e-3 RMS (far above its half ulp)
+    j = np.unravel_index(np.argmin(np.abs(y)), y.shape)
+    tiny = rne.copy()
+    tiny[j] = A.f32_to_bf16_bits(np.float32(y[j] + 1e-3 * rms))
+    assert not A.check_bf16_rounding(tiny, y)[0]
+
+
 # ---------------------------------------------------------------- GeGLU
 
 def test_geglu_matches_library_gelu_tanh():

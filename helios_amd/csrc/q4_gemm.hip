@@ -559,7 +559,7 @@ __global__ void split_geglu_kernel(const float* __restrict__ part, void* __restr
 // the products per group step) and split count (whole octets per split), the cost is
 // rounds-of-workgroups x octets-per-split x the measured step time, plus the partial
 // sums' extra traffic; the cheapest wins.
-GemmPlan plan_gemm(int m, const Layout& l) {
+GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
     GemmPlan p;
     const int octets = (l.g + 7) / 8;
     const long cus = device_cus();
@@ -574,6 +574,8 @@ GemmPlan plan_gemm(int m, const Layout& l) {
             if (used != s) continue;
             const size_t part = s > 1 ? (size_t)s * m * l.n * 4 : 0;
             if (part > kMaxPartialBytes) break;
+            const size_t m16 = ((size_t)m + bm - 1) / bm * (bm / 16);
+            if (m16 * octets * 64 * 16 + part > max_workspace) break;  // (more splits need more)
             const double rounds = (double)((tiles * s + cus - 1) / cus);
             const double t = rounds * per * 8 * step_us + (s > 1 ? 3.0 + part / bytes_per_us : 0.0);
             if (best < 0.0 || t < best) {
@@ -601,9 +603,10 @@ hipError_t launch_gelu_table(uint16_t* table, hipStream_t stream) {
 }
 
 hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, int out_mode,
-                       int n_out, const Layout& l, void* workspace, const uint16_t* gelu_table,
-                       hipStream_t stream) {
-    const GemmPlan plan = plan_gemm(m, l);
+                       int n_out, const Layout& l, void* workspace, size_t workspace_bytes,
+                       const uint16_t* gelu_table, hipStream_t stream) {
+    const GemmPlan plan = plan_gemm(m, l, workspace_bytes);
+    if (plan.xaug_bytes + plan.part_bytes > workspace_bytes) return hipErrorInvalidValue;
     const int octets = (l.g + 7) / 8;
     const int mtiles = (m + plan.bm - 1) / plan.bm;
     const int ntiles = (l.n + kBN - 1) / kBN;

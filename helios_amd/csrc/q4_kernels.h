@@ -74,7 +74,9 @@ hipError_t launch_greedy_reduce(const unsigned long long* part, int nb, int rows
 
 // Prefill path: fp32-exact factored GEMM on the matrix cores.  `workspace` holds the
 // group sums of x and, when K is split over workgroups, the fp32 partial sums
-// (gemm_workspace_bytes(m, l) bytes, device memory, 16-byte aligned).
+// (device memory, 256-byte aligned).  The plan is the cheapest whose workspace fits
+// in `workspace_bytes`; gemm_workspace_bytes(m, l) is what the unconstrained plan
+// needs, and with that much the launch runs the unconstrained plan.
 struct GemmPlan {
     int bm = 256;            // output tile rows: 256, or 128 for small M
     int splits = 1;          // workgroups along K per output tile
@@ -84,7 +86,7 @@ struct GemmPlan {
 };
 constexpr int kMaxSplits = 16;
 constexpr size_t kMaxPartialBytes = (size_t)1 << 30;
-GemmPlan plan_gemm(int m, const Layout& l);
+GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace = ~(size_t)0);
 size_t gemm_workspace_bytes(int m, const Layout& l);
 
 // Compute units of the current device (cached per device).
@@ -92,8 +94,8 @@ int device_cus();
 // gelu_table: kGeluTable bf16 values (q4_common.h) from launch_gelu_table, staged in
 // LDS by the bf16 GeGLU epilogue (out_mode 2); may be null for the other modes.
 hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, int out_mode,
-                       int n_out, const Layout& l, void* workspace, const uint16_t* gelu_table,
-                       hipStream_t stream);
+                       int n_out, const Layout& l, void* workspace, size_t workspace_bytes,
+                       const uint16_t* gelu_table, hipStream_t stream);
 
 // Fills table[kGeluTable] with gelu of the bf16 patterns that need a table, in the
 // bf16 op sequence.

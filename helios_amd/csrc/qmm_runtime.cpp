@@ -103,6 +103,78 @@ hipError_t gelu_table(int device, const uint16_t** out) {
     return hipSuccess;
 }
 
+// The allocation-free forward's scratch (gemma4_qlinear_forward_noalloc): one
+// file-scope device array, which every GPU the library runs on holds (its own copy,
+// at its own address) until the process ends.  In host code `scratch` names a host
+// stand-in, not device memory: its device address comes from hipGetSymbolAddress,
+// once per device with that device current, and only that address is used.
+constexpr size_t kStaticScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+
+// The current device's address of `scratch` (device must be current).
+hipError_t static_scratch(int device, char** out) {
+    if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (ptr == nullptr) return hipErrorInvalidSymbol;
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = static_cast<char*>(g_scratch_ptr[device]);
+    return hipSuccess;
+}
+
+// Device memory one forward call borrows for its kernels' scratch (8-bit handles'
+// [x | x], the GEMM's group sums and split-K partials): stream-ordered allocations
+// from the private pool, released on the same stream after the launches; or, for the
+// allocation-free entry point, consecutive 256-byte-aligned pieces of `scratch`.
+struct Scratch {
+    hipStream_t stream = nullptr;
+    int device = 0;
+    bool fixed = false;  // pieces of `scratch`: no allocation and nothing to release
+    char* base = nullptr;
+    size_t cap = 0, used = 0;
+    void* owned[2] = {};
+    int n_owned = 0;
+
+    // bytes still available (fixed mode; unlimited for the pool)
+    size_t room() const { return fixed ? cap - used : ~(size_t)0; }
+
+    hipError_t take(size_t bytes, void** out) {
+        *out = nullptr;
+        if (bytes == 0) return hipSuccess;
+        if (fixed) {
+            const size_t need = (bytes + 255) & ~(size_t)255;
+            if (need > cap - used) return hipErrorOutOfMemory;
+            *out = base + used;
+            used += need;
+            return hipSuccess;
+        }
+        if (n_owned == 2) return hipErrorInvalidValue;
+        hipMemPool_t pool = nullptr;
+        hipError_t e = scratch_pool(device, &pool);
+        if (e == hipSuccess) e = hipMallocFromPoolAsync(out, bytes, pool, stream);
+        if (e == hipSuccess) owned[n_owned++] = *out;
+        return e;
+    }
+
+    // queues the release of every pool allocation after the work on the stream
+    hipError_t release() {
+        hipError_t first = hipSuccess;
+        for (int i = 0; i < n_owned; ++i) {
+            const hipError_t e = hipFreeAsync(owned[i], stream);
+            if (first == hipSuccess) first = e;
+        }
+        n_owned = 0;
+        return first;
+    }
+};
+
 // Restores the caller's current device on scope exit.
 struct DeviceGuard {
     int saved = -1;
@@ -182,28 +254,27 @@ void release(Gemma4QLinear* h) {
 bool valid_handle(const Gemma4QLinear* h) { return h != nullptr && h->magic == kQLinearMagic; }
 
 // The x the kernels read: x itself, or for an 8-bit handle x' = [x | x] (rows x 2K) in
-// a stream-ordered scratch allocation that the caller frees on the same stream.
-Gemma4Status prepare_x(const Gemma4QLinear* h, const uint16_t* x, uint32_t rows, hipStream_t st, const std::string& name,
-                       const uint16_t** xk, void** scratch) {
+// the call's scratch.
+Gemma4Status prepare_x(const Gemma4QLinear* h, const uint16_t* x, uint32_t rows, Scratch& sc, const std::string& name,
+                       const uint16_t** xk) {
     *xk = x;
-    *scratch = nullptr;
     if (h->desc.bits != 8) return GEMMA4_OK;
     const size_t k = h->desc.in_features;
-    if ((size_t)rows * 2 * k * 2 > q4::kMaxBufferBytes)
+    const size_t bytes = (size_t)rows * 2 * k * 2;
+    if (bytes > q4::kMaxBufferBytes)
         return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, name + ": x exceeds 1 GiB for an 8-bit projection (split the rows)");
-    hipMemPool_t pool = nullptr;
-    hipError_t e = scratch_pool(h->device, &pool);
-    if (e != hipSuccess) return hip_fail((name + ": scratch pool").c_str(), e);
-    e = hipMallocFromPoolAsync(scratch, (size_t)rows * 2 * k * 2, pool, st);
+    if (bytes > sc.room())
+        return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
+                    name + ": [x | x] of an 8-bit projection needs " + std::to_string(bytes) +
+                        " bytes of scratch, more than the " + std::to_string(kStaticScratchBytes) +
+                        "-byte static scratch holds (split the rows)");
+    void* xs = nullptr;
+    hipError_t e = sc.take(bytes, &xs);
     if (e != hipSuccess)
         return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": x workspace allocation failed: " + hipGetErrorString(e));
-    e = q4::launch_duplicate_x(x, static_cast<uint16_t*>(*scratch), (int)rows, (int)k, st);
-    if (e != hipSuccess) {
-        (void)hipFreeAsync(*scratch, st);
-        *scratch = nullptr;
-        return hip_fail((name + ": x duplicate").c_str(), e);
-    }
-    *xk = static_cast<const uint16_t*>(*scratch);
+    e = q4::launch_duplicate_x(x, static_cast<uint16_t*>(xs), (int)rows, (int)k, sc.stream);
+    if (e != hipSuccess) return hip_fail((name + ": x duplicate").c_str(), e);
+    *xk = static_cast<const uint16_t*>(xs);
     return GEMMA4_OK;
 }
 
@@ -306,9 +377,49 @@ Gemma4Status create_from_device(const Gemma4QLinearDesc* desc, const Triple& mai
     return ok();
 }
 
-// Checks and dispatch shared by the plain and the GeGLU forward.
+// Launches one forward (checked arguments, device current) with its scratch from sc.
+Gemma4Status dispatch_forward(const Gemma4QLinear* linear, const uint16_t* x_dev, uint32_t rows, void* y_dev,
+                              Gemma4QmmDtype y_dtype, bool geglu, Scratch& sc, const std::string& name) {
+    const bool f32 = y_dtype == GEMMA4_QMM_F32;
+    const int mode = geglu ? (f32 ? q4::kOutGegluF32 : q4::kOutGegluBf16) : (f32 ? q4::kOutF32 : q4::kOutBf16);
+    const int n_out = linear->pair_rows;
+    Gemma4Status pst = prepare_x(linear, x_dev, rows, sc, name, &x_dev);
+    if (pst != GEMMA4_OK) return pst;
+    hipError_t e;
+    if ((int)rows < q4::kGemmMinRows) {
+        const q4::OutParams op{y_dev, nullptr, mode, n_out, 0, 0.0f};
+        e = q4::launch_decode(linear->tiles, linear->sb, x_dev, op, (int)rows, linear->layout, sc.stream);
+        if (e != hipSuccess) return hip_fail((name + ": decode launch").c_str(), e);
+        return GEMMA4_OK;
+    }
+    // group sums of x (and split-K partial sums): the unconstrained plan's workspace
+    // from the pool, or what the static scratch has left (the plan then splits K only
+    // as far as that room allows)
+    size_t ws_bytes = q4::gemm_workspace_bytes((int)rows, linear->layout);
+    if (sc.fixed) {
+        ws_bytes = sc.room();
+        const q4::GemmPlan plan = q4::plan_gemm((int)rows, linear->layout, ws_bytes);
+        if (plan.xaug_bytes + plan.part_bytes > ws_bytes)
+            return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
+                        name + ": the GEMM needs " + std::to_string(plan.xaug_bytes) + " bytes of scratch for " +
+                            std::to_string(rows) + " rows, more than the static scratch has left (" +
+                            std::to_string(ws_bytes) + " of " + std::to_string(kStaticScratchBytes) +
+                            " bytes; split the rows)");
+    }
+    void* ws = nullptr;
+    e = sc.take(sc.fixed ? 0 : ws_bytes, &ws);
+    if (sc.fixed) ws = sc.base + sc.used;
+    if (e != hipSuccess)
+        return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
+    e = q4::launch_gemm(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, mode, n_out, linear->layout, ws, ws_bytes,
+                        linear->gelu_table, sc.stream);
+    if (e != hipSuccess) return hip_fail((name + ": gemm launch").c_str(), e);
+    return GEMMA4_OK;
+}
+
+// Checks and dispatch shared by the plain, the GeGLU and the allocation-free forward.
 Gemma4Status run_forward(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev, uint32_t rows,
-                         void* y_dev, Gemma4QmmDtype y_dtype, bool geglu, const char* fn) {
+                         void* y_dev, Gemma4QmmDtype y_dtype, bool geglu, bool no_alloc, const char* fn) {
     const std::string name(fn);
     if (!valid_handle(linear)) return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " received an invalid handle");
     if (geglu && linear->pair_rows == 0)
@@ -331,39 +442,19 @@ Gemma4Status run_forward(const Gemma4QLinear* linear, void* stream, const uint16
     DeviceGuard guard;
     hipError_t e = guard.enter(linear->device);
     if (e != hipSuccess) return hip_fail((name + ": hipSetDevice").c_str(), e);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    const bool f32 = y_dtype == GEMMA4_QMM_F32;
-    const int mode = geglu ? (f32 ? q4::kOutGegluF32 : q4::kOutGegluBf16) : (f32 ? q4::kOutF32 : q4::kOutBf16);
-    const int n_out = linear->pair_rows;
-    void* xs = nullptr;
-    Gemma4Status pst = prepare_x(linear, x_dev, rows, st, name, &x_dev, &xs);
-    if (pst != GEMMA4_OK) return pst;
-    if ((int)rows < q4::kGemmMinRows) {
-        const q4::OutParams op{y_dev, nullptr, mode, n_out, 0, 0.0f};
-        e = q4::launch_decode(linear->tiles, linear->sb, x_dev, op, (int)rows, linear->layout, st);
-        const hipError_t ex = xs ? hipFreeAsync(xs, st) : hipSuccess;
-        if (e != hipSuccess) return hip_fail((name + ": decode launch").c_str(), e);
-        if (ex != hipSuccess) return hip_fail((name + ": x workspace release").c_str(), ex);
-        return ok();
+    Scratch sc;
+    sc.stream = static_cast<hipStream_t>(stream);
+    sc.device = linear->device;
+    if (no_alloc) {
+        e = static_scratch(linear->device, &sc.base);
+        if (e != hipSuccess) return hip_fail((name + ": static scratch address").c_str(), e);
+        sc.fixed = true;
+        sc.cap = kStaticScratchBytes;
     }
-    // group sums of x (and split-K partial sums) live in a stream-ordered scratch
-    // allocation for this call
-    const size_t ws_bytes = q4::gemm_workspace_bytes((int)rows, linear->layout);
-    hipMemPool_t pool = nullptr;
-    e = scratch_pool(linear->device, &pool);
-    void* ws = nullptr;
-    if (e == hipSuccess) e = hipMallocFromPoolAsync(&ws, ws_bytes, pool, st);
-    if (e != hipSuccess) {
-        if (xs) (void)hipFreeAsync(xs, st);
-        return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
-    }
-    e = q4::launch_gemm(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, mode, n_out, linear->layout, ws,
-                        linear->gelu_table, st);
-    const hipError_t ef = hipFreeAsync(ws, st);
-    const hipError_t ex = xs ? hipFreeAsync(xs, st) : hipSuccess;
-    if (e != hipSuccess) return hip_fail((name + ": gemm launch").c_str(), e);
-    if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);
-    if (ex != hipSuccess) return hip_fail((name + ": x workspace release").c_str(), ex);
+    const Gemma4Status st = dispatch_forward(linear, x_dev, rows, y_dev, y_dtype, geglu, sc, name);
+    const hipError_t er = sc.release();
+    if (st != GEMMA4_OK) return st;
+    if (er != hipSuccess) return hip_fail((name + ": workspace release").c_str(), er);
     return ok();
 }
 
@@ -508,7 +599,7 @@ Gemma4Status gemma4_qlinear_info(const Gemma4QLinear* linear, Gemma4QLinearInfo*
 Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
                                     uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype) {
     try {
-        return run_forward(linear, stream, x_dev, rows, y_dev, y_dtype, false, "gemma4_qlinear_forward");
+        return run_forward(linear, stream, x_dev, rows, y_dev, y_dtype, false, false, "gemma4_qlinear_forward");
     } catch (...) {
         return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward: unexpected native exception");
     }
@@ -517,9 +608,18 @@ Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, c
 Gemma4Status gemma4_qgeglu_forward(const Gemma4QLinear* pair, void* stream, const uint16_t* x_dev, uint32_t rows,
                                    void* h_dev, Gemma4QmmDtype h_dtype) {
     try {
-        return run_forward(pair, stream, x_dev, rows, h_dev, h_dtype, true, "gemma4_qgeglu_forward");
+        return run_forward(pair, stream, x_dev, rows, h_dev, h_dtype, true, false, "gemma4_qgeglu_forward");
     } catch (...) {
         return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qgeglu_forward: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qlinear_forward_noalloc(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
+                                            uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype) {
+    try {
+        return run_forward(linear, stream, x_dev, rows, y_dev, y_dtype, false, true, "gemma4_qlinear_forward_noalloc");
+    } catch (...) {
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_forward_noalloc: unexpected native exception");
     }
 }
 
@@ -551,30 +651,26 @@ Gemma4Status gemma4_qlinear_forward_greedy(const Gemma4QLinear* linear, void* st
         DeviceGuard guard;
         hipError_t e = guard.enter(linear->device);
         if (e != hipSuccess) return hip_fail((name + ": hipSetDevice").c_str(), e);
-        hipStream_t st = static_cast<hipStream_t>(stream);
-        hipMemPool_t pool = nullptr;
-        e = scratch_pool(linear->device, &pool);
-        if (e != hipSuccess) return hip_fail((name + ": scratch pool").c_str(), e);
+        Scratch sc;
+        sc.stream = static_cast<hipStream_t>(stream);
+        sc.device = linear->device;
         const int nb = linear->layout.nb;
         void* part = nullptr;
-        e = hipMallocFromPoolAsync(&part, (size_t)rows * nb * sizeof(unsigned long long), pool, st);
+        e = sc.take((size_t)rows * nb * sizeof(unsigned long long), &part);
         if (e != hipSuccess)
             return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
         const int mode = dtype == GEMMA4_QMM_F32 ? q4::kOutGreedyF32 : q4::kOutGreedyBf16;
         const q4::OutParams op{logits_dev, static_cast<unsigned long long*>(part), mode, 0, nb, softcap};
-        void* xs = nullptr;
-        const Gemma4Status pst = prepare_x(linear, x_dev, rows, st, name, &x_dev, &xs);
-        if (pst != GEMMA4_OK) {
-            (void)hipFreeAsync(part, st);
-            return pst;
+        Gemma4Status pst = prepare_x(linear, x_dev, rows, sc, name, &x_dev);
+        if (pst == GEMMA4_OK) {
+            e = q4::launch_decode(linear->tiles, linear->sb, x_dev, op, (int)rows, linear->layout, sc.stream);
+            if (e == hipSuccess)
+                e = q4::launch_greedy_reduce(static_cast<const unsigned long long*>(part), nb, (int)rows, token_dev,
+                                             value_dev, sc.stream);
+            if (e != hipSuccess) pst = hip_fail((name + ": launch").c_str(), e);
         }
-        e = q4::launch_decode(linear->tiles, linear->sb, x_dev, op, (int)rows, linear->layout, st);
-        if (e == hipSuccess)
-            e = q4::launch_greedy_reduce(static_cast<const unsigned long long*>(part), nb, (int)rows, token_dev,
-                                         value_dev, st);
-        if (xs) (void)hipFreeAsync(xs, st);
-        const hipError_t ef = hipFreeAsync(part, st);
-        if (e != hipSuccess) return hip_fail((name + ": launch").c_str(), e);
+        const hipError_t ef = sc.release();
+        if (pst != GEMMA4_OK) return pst;
         if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);
         return ok();
     } catch (...) {
@@ -650,7 +746,7 @@ Gemma4Status gemma4_qlinear_forward_lora(const Gemma4QLinear* linear, const Gemm
             if (valid_handle(linear) && lora->device != linear->device)
                 return fail(GEMMA4_ERR_ADAPTER, name + ": adapter and projection are on different devices");
         }
-        Gemma4Status st = run_forward(linear, stream, x_dev, rows, y_dev, y_dtype, false, name.c_str());
+        Gemma4Status st = run_forward(linear, stream, x_dev, rows, y_dev, y_dtype, false, false, name.c_str());
         if (st != GEMMA4_OK || lora == nullptr || rows == 0) return st;
         DeviceGuard guard;
         hipError_t e = guard.enter(linear->device);

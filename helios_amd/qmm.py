@@ -97,6 +97,7 @@ def load_library(path: str | None = None):
         "gemma4_qlinear_free": [vp],
         "gemma4_qlinear_info": [vp, ctypes.POINTER(_Info)],
         "gemma4_qlinear_forward": [vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int],
+        "gemma4_qlinear_forward_noalloc": [vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int],
         "gemma4_qlinear_dequantize": [vp, vp, vp],
         "gemma4_qgeglu_create": [ctypes.POINTER(_Desc), vp, vp, vp, vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qgeglu_create_device": [ctypes.POINTER(_Desc), vp, vp, vp, vp, vp, vp, vp, ctypes.POINTER(vp)],
@@ -278,6 +279,13 @@ class QuantizedLinear(_Handle):
                             self.out_features, out, out_dtype, stream)
 
     __call__ = forward
+
+    def forward_noalloc(self, x, out, stream=None):
+        """forward into a caller-owned `out` through gemma4_qlinear_forward_noalloc: no
+        device allocation by the library (its scratch is a static per-GPU array, so
+        overlapping calls on one GPU race; see include/gemma4_qmm.h)."""
+        return _run_forward(self._lib.gemma4_qlinear_forward_noalloc, self._handle, self._lib, x, self.in_features,
+                            self.out_features, out, out.dtype, stream)
 
     def forward_raw(self, x_ptr: int, rows: int, y_ptr: int, f32: bool = False, stream_ptr: int = 0) -> None:
         """Direct C-ABI call on raw device pointers (benchmark loops)."""

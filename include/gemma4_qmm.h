@@ -137,6 +137,23 @@ Gemma4Status gemma4_qlinear_info(const Gemma4QLinear* linear, Gemma4QLinearInfo*
 Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
                                     uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype);
 
+/* gemma4_qlinear_forward for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, hosts that forbid allocation): the same
+ * arguments, results and kernels, with every scratch buffer taken from a static
+ * 64 MiB device array that the library holds on each GPU it runs on until the
+ * process ends.  No counterpart in the reference (its MLX ops allocate per call).
+ * It calls no hipMalloc, hipFree or allocating library routine.  Scratch needs:
+ * none for 4-bit rows < 32; for rows >= 32 the GEMM's group sums of x (rows * K / 8
+ * bytes, rounded up to 128- or 256-row tiles), and split-K partial sums only as far
+ * as the array has room (fewer splits than gemma4_qlinear_forward may choose, so the
+ * fp32 summation order, and with it the last bits of some outputs, can differ from
+ * that call's); 8-bit handles add [x | x], rows * 4K bytes.  A call needing more
+ * than 64 MiB fails with GEMMA4_ERR_UNSUPPORTED_CONFIG (split the rows).  Every call
+ * on a GPU shares that GPU's array: calls that overlap in time on one GPU (other
+ * streams, other threads) race and must be serialized by the caller. */
+Gemma4Status gemma4_qlinear_forward_noalloc(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
+                                            uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype);
+
 /* Writes the fp32 dequantized weight W[N,K] = s*q + b (row-major) to w_dev —
  * mlx::core::dequantize (native_model.cc:364-376) with a float32 result.  Bit-exact:
  * the product s*q is exact in fp32, so the value is unique.  For a gate|up pair the

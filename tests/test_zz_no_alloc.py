@@ -1,0 +1,118 @@
+"""GPU check of gemma4_qlinear_forward_noalloc (the allocation-free forward) through
+the C ABI: on a sequence of calls in a row on one stream, each followed by a smaller
+one that reuses the same static scratch, its output equals gemma4_qlinear_forward's
+bit for bit where both run the same GEMM plan, and otherwise both meet the oracle's
+bars (fp32 within 2e-3 * RMS, bf16 within 1e-2 * RMS + ulp/2) and agree to within
+the fp32 accumulation error; a call needing more scratch than the array holds fails
+with UNSUPPORTED_CONFIG before any launch.  (This check has no counterpart in the
+reference: its MLX ops allocate per call.)"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import affine as A
+from oracle import c_oracle as C
+from test_gpu_parity import assert_close, dev_triple, dev_x, host_bits, random_triple
+
+pytestmark = pytest.mark.gpu
+
+
+def _both(lin, x, dtype):
+    import torch
+
+    ref = lin.forward(x, out_dtype=dtype)
+    got = torch.full_like(ref, float("nan"))  # stale contents must not survive
+    lin.forward_noalloc(x, got)
+    torch.cuda.synchronize()
+    return ref, got
+
+
+def _compare(ref, got, x_bits, tri, rows, what, bits=4):
+    import torch
+
+    if torch.equal(ref, got):
+        return True
+    # a different split of K (less room for partial sums): both within the bars
+    rt = torch.from_numpy(rows).cuda()
+    want = C.qmm_f64(np.ascontiguousarray(x_bits[rows]), *tri, bits=bits)
+    assert_close(got[rt], want, what + " (noalloc)")
+    assert_close(ref[rt], want, what + " (forward)")
+    if got.dtype == torch.float32:
+        rms = float(ref.float().pow(2).mean().sqrt())
+        assert float((got - ref).abs().max()) <= 1e-4 * rms, what
+    return False
+
+
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float32"])
+def test_noalloc_matches_forward_on_consecutive_calls(gpu_lib, dtype_name):
+    import torch
+
+    dtype = getattr(torch, dtype_name)
+    cases = [  # (N, K, M): each call followed by a smaller one on the same scratch
+        (2048, 3840, 512),    # GEMM, K split over workgroups: group sums + partial planes
+        (40, 384, 40),        # small GEMM
+        (3840, 15360, 2048),  # GEMM, the largest group-sum table of the configs
+        (2048, 3840, 1),      # decode: no scratch
+        (130, 1088, 300),     # GEMM with a ragged last octet
+        (48, 576, 33),
+    ]
+    for i, (n, k, m) in enumerate(cases):
+        tri = random_triple(n, k, seed=9100 + i)
+        x = A.make_activations(m, k, seed=9200 + i, outliers=True)
+        lin = gpu_lib.QuantizedLinear(*dev_triple(*tri))
+        ref, got = _both(lin, dev_x(x), dtype)
+        rows = np.unique(np.linspace(0, m - 1, min(m, 12)).astype(np.int64))
+        _compare(ref, got, x, tri, rows, f"n={n} k={k} m={m} {dtype_name}")
+        lin.close()
+
+
+def test_noalloc_eight_bit_and_its_limit(gpu_lib):
+    import torch
+
+    # 8-bit: [x | x] in the static scratch, then the GEMM's workspace after it
+    rng = np.random.default_rng(91)
+    w = A.round_to_bf16((rng.standard_normal((96, 3840)) * 0.02).astype(np.float32))
+    tri = C.quantize(w, bits=8)
+    for m in (64, 5):  # GEMM, then decode
+        x = A.make_activations(m, 3840, seed=92 + m)
+        lin = gpu_lib.QuantizedLinear(*dev_triple(*tri), bits=8)
+        ref, got = _both(lin, dev_x(x), torch.float32)
+        _compare(ref, got, x, tri, np.arange(m), f"8-bit m={m}", bits=8)
+        lin.close()
+    # [x | x] of 2048 rows at K = 15360 needs 126 MB: refused before any launch
+    small = C.quantize(A.round_to_bf16((rng.standard_normal((16, 15360)) * 0.02).astype(np.float32)), bits=8)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*small), bits=8)
+    x = torch.zeros((2048, 15360), dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros((2048, 16), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(gpu_lib.Gemma4Error) as e:
+        lin.forward_noalloc(x, y)
+    assert e.value.status == gpu_lib.Status.UNSUPPORTED_CONFIG and "scratch" in e.value.message
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(y).item() == 0
+    # the allocating entry point still serves it
+    lin.forward(x[:64], out=y[:64])
+    torch.cuda.synchronize()
+    lin.close()
+
+
+def test_noalloc_through_raw_c_abi(gpu_lib):
+    """The entry point called with raw pointers and the current stream, as a C caller
+    would: status 0 and the forward's bits."""
+    import torch
+
+    lib = gpu_lib.load_library()
+    tri = random_triple(256, 640, seed=93)
+    x = dev_x(A.make_activations(300, 640, seed=94))
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*tri))
+    y = torch.empty((300, 256), dtype=torch.bfloat16, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.gemma4_qlinear_forward_noalloc(lin._handle, st, ctypes.c_void_p(x.data_ptr()), 300,
+                                            ctypes.c_void_p(y.data_ptr()), gpu_lib.DTYPE_BF16)
+    assert rc == 0, gpu_lib.last_error()
+    ref = lin.forward(x)
+    torch.cuda.synchronize()
+    assert torch.equal(ref, y)
+    assert np.isfinite(A.bf16_bits_to_f32(host_bits(y))).all()
+    lin.close()

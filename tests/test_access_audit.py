@@ -1,0 +1,297 @@
+"""CPU audit of the gfx950 kernels' memory accesses (no GPU needed).
+
+The index arithmetic of the GEMM (q4_gemm.hip) and the decode kernels
+(q4_decode.hip) is restated here in numpy and checked against the buffers the host
+allocates, for the benchmark's shapes and the awkward ones the GPU tests use:
+
+* raw buffer loads: an in-range offset (below the resource's num_records) must read
+  inside the real buffer, num_records never exceeds the buffer, and offsets meant to
+  read zeros sit at or past num_records (the class of bug that once put a 2 GiB
+  offset in range: a resource of 0xFFFFFFFF records made kOutOfRange valid);
+* LDS reads and writes stay inside their arrays and the layout fits 160 KiB;
+* every output tile, row block and split is visited exactly once, and stores stay
+  inside y.
+
+It restates the kernels' formulas rather than executing them, so a change to an
+index expression in the .hip sources must be mirrored here."""
+
+import numpy as np
+import pytest
+
+OOB = 0x80000000
+LDS_BYTES = 160 * 1024
+
+
+def chk_buf(name, off, size, num_records, real_bytes):
+    off = np.asarray(off, dtype=np.int64)
+    assert num_records <= real_bytes, (name, num_records, real_bytes)
+    assert num_records <= 2 ** 31, (name, num_records)
+    inr = off < num_records
+    bad = inr & ((off < 0) | (off + size > num_records))
+    assert not bad.any(), (name, off[bad][:5], num_records)
+
+
+def layout(n, k):
+    g = k // 64
+    nb = (n + 15) // 16
+    gp = (g + 1) // 2
+    return dict(n=n, k=k, g=g, nb=nb, gp=gp, tile_bytes=nb * gp * 1024, sb_bytes=nb * gp * 128)
+
+
+# ------------------------------------------------------------------------- GEMM
+
+def tile_of(bid, nwg, mtiles, ntiles):
+    tile = bid
+    if nwg % 8 == 0:
+        tile = (bid % 8) * (nwg // 8) + bid // 8
+    band = tile // (2 * ntiles)
+    r = tile - band * 2 * ntiles
+    bm = min(2, mtiles - band * 2)
+    return band * 2 + r % bm, r // bm
+
+
+def audit_gemm(m, n, k, BM, splits):
+    L = layout(n, k)
+    BN, RB, WAVES = 256, 16, 8
+    WM = BM // 2
+    XP = BM * 8 // 512     # x DMA parts per wave per group
+    XA = BM // 128         # bias A-operand DMA parts per wave per octet
+    KWP, KSP = RB * 64, RB * 16 // 2  # uint4 units of one weight slot
+    BIAS_SLOT = 16 * 64 + RB * 4 * 16 // 2  # uint4 units: A operands, then the octet's scale/bias words
+    G = L["g"]
+    octets = (G + 7) // 8
+    mtiles = (m + BM - 1) // BM
+    ntiles = (n + BN - 1) // BN
+    nblocks = (n + 15) // 16
+    xbytes = m * k * 2
+    ws_bytes = mtiles * (BM // 16) * octets * 1024
+    per = (octets + splits - 1) // splits
+    assert (octets + per - 1) // per == splits
+    g_split = per * 8
+    nwg = mtiles * ntiles
+    seen = set()
+    lane = np.arange(64)
+    l16 = lane & 15
+    for bid in range(nwg):
+        mt, nt = tile_of(bid, nwg, mtiles, ntiles)
+        assert 0 <= mt < mtiles and 0 <= nt < ntiles
+        seen.add((mt, nt))
+        rbw = nt * RB
+        for wave in range(WAVES):
+            wm, wn = wave & 1, wave >> 1
+            # DMA offsets: per-lane constants + a scalar step offset (group, pair, octet)
+            for part in range(XP):
+                q = (8 * part + wave) * 64 + lane
+                rr = q >> 3
+                c = (q & 7) ^ ((rr >> 1) & 7)
+                row = mt * BM + rr
+                assert ((8 * part + wave) * 64 + 64) <= BM * 8
+                xv = np.where(row < m, (row * k + 8 * c) * 2, OOB)
+                for g in (0, G - 1):  # a per-lane constant plus g * 128: the extremes bound every step
+                    chk_buf("gemm x", np.where(xv == OOB, OOB, xv + g * 128), 16, xbytes, xbytes)
+            for part in range(2):
+                rb = rbw + 2 * wave + part
+                wv = np.where(rb < nblocks, (rb * L["gp"] * 64 + lane) * 16, OOB)
+                for p in (0, L["gp"] - 1):
+                    chk_buf("gemm w", np.where(wv == OOB, OOB, wv + p * 1024), 16, L["tile_bytes"], L["tile_bytes"])
+            if wave < 2:
+                rb = rbw + 8 * wave + (lane >> 3)
+                sv = np.where(rb < nblocks, rb * L["gp"] * 128 + (lane & 7) * 16, OOB)
+                for p in (0, L["gp"] - 1):
+                    chk_buf("gemm s", np.where(sv == OOB, OOB, sv + p * 128), 16, L["sb_bytes"], L["sb_bytes"])
+            for o in sorted({0, octets - 1}):
+                for u in range(XA):
+                    m16 = XA * wave + u
+                    assert m16 * 64 + 64 <= 1024
+                    off = ((mt * (BM // 16) + m16) * octets + o) * 1024 + lane * 16
+                    chk_buf("gemm xa", off, 16, ws_bytes, ws_bytes)
+                rb = rbw + 2 * wave + (lane >> 5)
+                chunk = lane & 31
+                ok = (rb < nblocks) & (4 * o + (chunk >> 3) < L["gp"])
+                raw = (rb * L["gp"] + 4 * o) * 128 + chunk * 16
+                chk_buf("gemm bias words", np.where(ok, raw, OOB), 16, L["sb_bytes"], L["sb_bytes"])
+                assert 16 * 64 + wave * 64 + 63 < BIAS_SLOT  # the scale/bias part of the bias slot
+            # LDS operand reads of the 16x16x32 product stream
+            kq = lane >> 4
+            for j in range(4):  # the wave's four row blocks
+                rbl = wn * 4 + j
+                assert rbl * 64 + 64 <= KWP and ((rbl * 16 + l16) < KSP * 2).all()
+                assert ((((wn * 4 + j) * 4 + kq) * 16 + l16) < 1024).all()  # bias words, uint2
+            for i in range(WM // 16):
+                r = wm * WM + 16 * i + l16
+                for c in (kq, 4 + kq):
+                    idx = r * 8 + (c ^ ((r >> 1) & 7))
+                    assert (idx >= 0).all() and (idx < BM * 8).all()
+                assert (wm * (WM // 16) + i) * 64 + 64 <= 1024  # bias A operands
+            # stores: rows 4*kq + e of each 16-row tile, column l16 of the row block
+            for i in range(WM // 16):
+                for e in range(4):
+                    mrow = mt * BM + wm * WM + 16 * i + 4 * kq + e
+                    assert (mrow < mtiles * BM).all()
+    assert len(seen) == nwg
+    # split-K: each split starts on an octet and the planes fit the partial buffer
+    for sp in range(splits):
+        gb = sp * g_split
+        ge = min(G, gb + g_split)
+        assert gb < ge and gb % 8 == 0
+    # LDS: three x slots, two weight slots, the bias slot
+    assert 3 * 256 * 8 * 16 + 2 * (KWP + KSP) * 16 + BIAS_SLOT * 16 <= LDS_BYTES
+
+
+GEMM_SHAPES = [(33, 40, 384), (300, 256, 640), (257, 130, 320), (64, 512, 3840), (512, 2048, 3840),
+               (512, 3840, 4096), (2048, 15360, 3840), (2048, 3840, 15360), (33, 16, 64), (40, 48, 576),
+               (300, 130, 1088), (256, 512, 3840), (2048, 8192, 3840), (2048, 3840, 8192)]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+@pytest.mark.parametrize("bm", [256, 128])
+def test_gemm_accesses(m, n, k, bm):
+    octets = (k // 64 + 7) // 8
+    for s in sorted({1, 2, min(8, octets), octets}):
+        per = (octets + s - 1) // s
+        if (octets + per - 1) // per == s:
+            audit_gemm(m, n, k, bm, s)
+
+
+# ----------------------------------------------------------------------- decode
+
+def _chunk_reads(first, n_in, tile_bytes, sb_bytes):
+    """A chunk's weight loads: lane offsets lane*16 + i*1024 (i < 4) against a resource
+    of n_in pairs starting at pair `first`, and the scale words (one 8-byte load per
+    lane over the chunk's 512 bytes).  Vectorized over chunks: the largest in-range
+    offset of each chunk must end inside the real buffer."""
+    first = np.asarray(first, np.int64)
+    n_in = np.asarray(n_in, np.int64)
+    assert (n_in >= 0).all() and (n_in <= 4).all()
+    live = n_in > 0
+    # largest lane offset below n_in * 1024 is (n_in - 1) * 1024 + 63 * 16; it ends 16 bytes later
+    assert ((first * 1024 + n_in * 1024)[live] <= tile_bytes).all()
+    assert ((first * 128 + n_in * 128)[live] <= sb_bytes).all()
+    assert (n_in * 1024 <= 2 ** 31).all()
+
+
+def audit_decode_stream(m_total, n, k, cus=256):
+    """decode_stream_kernel: persistent workgroups over row blocks, K split over waves,
+    16-row slabs along grid y; x staged in LDS with zero padding and a -X table."""
+    L = layout(n, k)
+    GPW = 4
+    MT = 1 if m_total == 1 else 2 if m_total == 2 else 4 if m_total <= 4 else 16
+    R = min(MT, 4)
+    ms = min(m_total, 16)
+    static_lds = 2 * 8 * R * 64 * 4
+    lds_bytes = ms * (k + GPW * 128) * 2 + (L["gp"] + GPW) * 2 * 16 * 4
+    stream_lds = lds_bytes + ms * 16
+    if stream_lds + static_lds > LDS_BYTES:
+        return False
+    waves = min(8, (L["gp"] + GPW - 1) // GPW, L["gp"])
+    per_cu = max(1, 20 // waves)
+    per_cu = min(per_cu, LDS_BYTES // (stream_lds + static_lds))
+    cap = cus * per_cu
+    per_wg = (L["nb"] + cap - 1) // cap
+    grid = (L["nb"] + per_wg - 1) // per_wg
+    nbuf = 4 if per_cu == 1 and per_wg >= 16 else 2
+    lane = np.arange(64)
+    col, kq = lane & 15, lane >> 4
+    bid = np.arange(grid)
+    my_blocks = (L["nb"] - bid + grid - 1) // grid
+    seen = np.zeros(L["nb"], np.int64)
+    for wave in range(waves):
+        gp0 = wave * L["gp"] // waves
+        cnt = (wave + 1) * L["gp"] // waves - gp0
+        assert cnt >= 1
+        passes = (cnt + GPW - 1) // GPW
+        # every chunk a workgroup's wave issues, nbuf past its last included (empty ranges)
+        c = np.arange(int(my_blocks.max()) * passes + nbuf)
+        B, C = np.meshgrid(bid, c, indexing="ij")
+        chunks = (my_blocks * passes)[:, None]
+        live = C < chunks
+        rb = np.where(live, B + (C // passes) * grid, 0)
+        assert (rb < L["nb"]).all()
+        pas = C % passes
+        n_in = np.where(live, np.minimum(cnt - pas * GPW, GPW), 0)
+        _chunk_reads(rb * L["gp"] + gp0 + pas * GPW, n_in, L["tile_bytes"], L["sb_bytes"])
+        if wave == 0:
+            np.add.at(seen, rb[live & (pas == passes - 1)], 1)
+    assert (seen == 1).all()
+    for slab in range((m_total + 15) // 16):
+        m_rows = min(16, m_total - 16 * slab)
+        row16 = ((k + GPW * 128) >> 3) + 1
+        negx_base = m_rows * row16
+        tab = 2 * (L["gp"] + GPW) * 16
+        assert negx_base * 16 + tab * 4 <= stream_lds
+        arow = np.minimum(col, m_rows - 1)
+        for wave in range(waves):
+            gp0 = wave * L["gp"] // waves
+            cnt = (wave + 1) * L["gp"] // waves - gp0
+            for pas in range((cnt + GPW - 1) // GPW):
+                gpb = gp0 + pas * GPW
+                xp = arow * row16 + kq + gpb * 16
+                for i in range(GPW):
+                    for gi in range(2):
+                        for h in (0, 4):
+                            idx = xp + i * 16 + gi * 8 + h
+                            assert (idx >= 0).all() and (idx < negx_base).all()
+                        nidx = gpb * 32 + 4 * kq + i * 32 + gi * 16
+                        assert (nidx + 4 <= tab).all()
+        xchunks = (m_rows * k) >> 3
+        rowc = k >> 3
+        c = np.arange(xchunks)
+        row = c // rowc
+        cr = c - row * rowc
+        assert (row * row16 + cr < negx_base).all() and ((cr >> 3) * 16 + row < tab).all()
+        chk_buf("dec x", c * 16, 16, m_rows * k * 2, m_rows * k * 2)
+        pad = (GPW * 128) >> 3
+        c = np.arange(m_rows * pad)
+        assert ((c // pad) * row16 + rowc + (c % pad) < negx_base).all()
+    return True
+
+
+def audit_decode_rows(m, n, k, cus=256, GPW=4, NBUF=2, waves=4, per_cu=2):
+    """decode_rows_kernel (M = 1): one wave per row block, NBUF chunks in flight."""
+    L = layout(n, k)
+    nb, gp = L["nb"], L["gp"]
+    grid = min((nb + waves - 1) // waves, cus * per_cu)
+    nw = grid * waves
+    passes = (gp + GPW - 1) // GPW
+    row16 = (k + GPW * 128) >> 3
+    lds_bytes = m * (k + GPW * 128) * 2 + (gp + GPW) * 2 * 16 * 4
+    assert lds_bytes <= LDS_BYTES
+    negx_base = m * row16
+    gw = np.arange(nw)
+    my = np.where(gw < nb, (nb - gw + nw - 1) // nw, 0)
+    c = np.arange(int(my.max()) * passes + NBUF)
+    W, C = np.meshgrid(gw, c, indexing="ij")
+    chunks = (my * passes)[:, None]
+    live = C < chunks
+    rb = np.where(live, W + (C // passes) * nw, 0)
+    assert (rb < nb).all()
+    gpb = (C % passes) * GPW
+    n_in = np.where(live, np.minimum(GPW, gp - gpb), 0)
+    _chunk_reads(rb * gp + gpb, n_in, L["tile_bytes"], L["sb_bytes"])
+    seen = np.zeros(nb, np.int64)
+    np.add.at(seen, rb[live & (C % passes == passes - 1)], 1)
+    assert (seen == 1).all()
+    kq = np.arange(64) >> 4
+    for p in range(passes):
+        gpb = p * GPW
+        for i in range(GPW):
+            for gi in range(2):
+                idx = (m - 1) * row16 + kq + (gpb + i) * 16 + gi * 8 + 4
+                assert (idx < negx_base).all()
+                t = (gpb + i) * 32 + gi * 16 + 4 * kq + 3
+                assert (t < 2 * (gp + GPW) * 16).all()
+
+
+DECODE_SHAPES = [(40, 384), (64, 320), (16, 64), (4096, 3840), (2048, 3840), (3840, 4096), (15360, 3840),
+                 (3840, 15360), (262144, 3840), (131072 + 48, 128), (33, 640), (70000, 3840), (76800 + 40, 3840)]
+
+
+@pytest.mark.parametrize("n,k", DECODE_SHAPES)
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 9, 16, 17, 31])
+def test_decode_stream_accesses(m, n, k):
+    audit_decode_stream(m, n, k)
+
+
+@pytest.mark.parametrize("n,k", [(15360, 3840), (30720, 3840), (8192 + 48, 128), (8192, 640), (16 * 512, 3840)])
+def test_decode_rows_accesses(n, k):
+    audit_decode_rows(1, n, k)

@@ -383,6 +383,35 @@ def test_gemm_prefill_projections(gpu_lib, proj, m):
     assert torch.all(diff <= y_f.abs() * 2**-8 + 1e-6).item()
 
 
+# the real Gemma 4 12B's full-attention layers (native_model.cc:795-798, :820-827): q
+# 3840 -> 8192, k 3840 -> 512 (k doubles as v, no v_proj), o 8192 -> 3840
+FULL_ATTENTION = {"full_q_proj": (8192, 3840), "full_k_proj": (512, 3840), "full_o_proj": (3840, 8192)}
+
+
+@pytest.mark.parametrize("proj", sorted(FULL_ATTENTION))
+@pytest.mark.parametrize("m", [1, 4, 8, 256, 2048])
+def test_full_attention_projections(gpu_lib, proj, m):
+    """The full-attention shapes at decode (every output against the oracle) and at the
+    long-context chunk M = 256 and the prefill chunk M = 2048 (sampled rows)."""
+    import torch
+
+    n, k = FULL_ATTENTION[proj]
+    triple = A.make_weights(n, k, seed=20260630 + 6000 + sorted(FULL_ATTENTION).index(proj))
+    x = A.make_activations(m, k, seed=6100 + m, outliers=m > 8)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*triple))
+    xd = dev_x(x)
+    y_bf = lin.forward(xd)
+    y_f = lin.forward(xd, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rows = np.arange(m) if m <= 8 else np.sort(np.random.default_rng(m).choice(m, 24, replace=False))
+    rt = torch.from_numpy(rows).cuda()
+    y_exact = C.qmm_f64(np.ascontiguousarray(x[rows]), *triple)
+    assert_close(y_bf[rt], y_exact, f"{proj} m={m} bf16")
+    assert_rounded(y_bf[rt], y_exact, f"{proj} m={m} bf16", literal=m <= 8)
+    assert assert_close(y_f[rt], y_exact, f"{proj} m={m} f32") < (ACC_REL if m <= 8 else 5e-4)
+    lin.close()
+
+
 def test_gemm_prefill_chain_m2048_geglu(gpu_lib):
     """Chunked-prefill chain at M=2048: gate and up, GeGLU on the host (identical bf16
     bytes to both sides), then down_proj; sampled rows against the oracle."""

@@ -341,6 +341,14 @@ def summarize_profiles(stats_dir: str, fetch_dir: str, write_dir: str, line_file
     w_cpy, n_wc = per_dispatch(write_rows, "WRITE_SIZE", is_copy)
     f_scale = line["copy_bytes"] / (f_cpy * 1024)
     w_scale = line["copy_bytes"] / (w_cpy * 1024)
+    # a second, independent calibration of the read counter: the read-only probe
+    # kernel reads exactly read_probe_bytes per dispatch and writes 4 bytes per wave
+    is_probe = lambda n: "hbm_read_kernel" in n  # noqa: E731
+    try:
+        f_prb, n_fp = per_dispatch(fetch_rows, "FETCH_SIZE", is_probe)
+        f_scale_probe = line["read_probe_bytes"] / (f_prb * 1024)
+    except (SystemExit, KeyError):
+        f_prb, n_fp, f_scale_probe = None, 0, None
     fetch_b = f_dom * 1024 * f_scale
     write_b = w_dom * 1024 * w_scale
     dom_stats = [r for r in stats if is_dom(r["Name"])]
@@ -358,7 +366,10 @@ def summarize_profiles(stats_dir: str, fetch_dir: str, write_dir: str, line_file
         "copy_write_kib": round(w_cpy, 1),
         "fetch_scale": round(f_scale, 5),
         "write_scale": round(w_scale, 5),
-        "dispatches": {"fetch": n_fd, "write": n_wd, "copy_fetch": n_fc, "copy_write": n_wc},
+        "fetch_scale_read_probe": round(f_scale_probe, 5) if f_scale_probe else None,
+        "read_probe_fetch_kib": round(f_prb, 1) if f_prb else None,
+        "fetch_bytes_per_launch_by_probe_scale": int(round(f_dom * 1024 * f_scale_probe)) if f_scale_probe else None,
+        "dispatches": {"fetch": n_fd, "write": n_wd, "copy_fetch": n_fc, "copy_write": n_wc, "probe_fetch": n_fp},
         "rocprof_avg_launch_us": round(avg_ns / 1e3, 3) if avg_ns else None,
         "bench_avg_launch_us": line["avg_launch_us"],
         "source": "rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE over bench.py --roofline-only",
@@ -375,7 +386,8 @@ def summarize_profiles(stats_dir: str, fetch_dir: str, write_dir: str, line_file
     for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))[:8]:
         md.append(f"| {short(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
                   f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} |")
-    md += ["", "HBM traffic per launch (FETCH_SIZE, WRITE_SIZE in KiB per dispatch, scaled by the 1 GiB copy):", "",
+    md += ["", "HBM traffic per launch (FETCH_SIZE, WRITE_SIZE in KiB per dispatch, scaled by the 1 GiB copy; "
+           "the read-only probe over 1 GiB gives a second, independent scale for FETCH_SIZE):", "",
            "```", json.dumps(traffic, indent=1), "```", ""]
     with open(os.path.join(ROOT, "profiles", "gate_up_decode_m1.md"), "w") as f:
         f.write("\n".join(md))
@@ -391,6 +403,52 @@ def prefill_sweep_names(ms=PREFILL_MS):
     for m in ms:
         names += [f"{n}_m{m}" for n, _, _ in list(LAYER) + list(FULL_ATTENTION)] + [f"{PAIR}_m{m}"]
     return names
+
+
+def variants_run(torch, Q, host) -> dict:
+    """The 8-bit affine variant and a LoRA adapter on the gate_proj shape (N = 15360,
+    K = 3840): decode at M = 1 (HBM rate over the variant's own algorithmic bytes:
+    8-bit codes are 1 byte per weight plus the bf16 scales and biases) and prefill at
+    M = 2048 (TFLOPS), and the LoRA forward (rank 16, delta added to the bf16 output)
+    against the plain forward on the same handle."""
+    import torch as _t
+    from helios_amd.quantize import quantize
+
+    n, k = 15360, HIDDEN
+    rng = np.random.Generator(np.random.PCG64(SEED_BASE + 7000))
+    w = _t.from_numpy(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).cuda().bfloat16()
+    wq8, s8, b8 = quantize(w, bits=8)
+    del w
+    out = {}
+    x1 = torch.from_numpy(synthetic_activations(1, k, seed=SEED_BASE + 11).view(np.int16)).view(torch.bfloat16).cuda()
+    x2 = torch.from_numpy(synthetic_activations(2048, k, seed=SEED_BASE + 12, outliers=True).view(np.int16)) \
+        .view(torch.bfloat16).cuda()
+    w8bytes = n * k + 4 * n * (k // 64)
+    us = kernel_us(torch, lambda: Q.QuantizedLinear(wq8, s8, b8, bits=8), 1, k, n, x1, w8bytes)
+    b1 = w8bytes + 2 * k + 2 * n
+    out["q8_gate_m1"] = {"us": round(us, 2), "GBps": round(b1 / (us * 1e-6) / 1e9, 1),
+                         "algo_bytes": b1, "resident_bytes_per_weight": 1.125}
+    lin8 = Q.QuantizedLinear(wq8, s8, b8, bits=8)
+    y2 = torch.empty((2048, n), dtype=torch.bfloat16, device="cuda")
+    ms = graph_ms_steady(torch, lambda: lin8.forward(x2, out=y2))
+    out["q8_gate_m2048"] = {"us": round(ms * 1e3, 1),
+                            "TFLOPS": round(algo_flops(2048, n, k) / (ms * 1e-3) / 1e12, 1)}
+    lin8.close()
+    # LoRA: rank 16, scale 2 (alpha 32), A [16, K], B [N, 16]
+    r = 16
+    a = (rng.standard_normal((r, k)) * 0.02).astype(np.float32)
+    bm = (rng.standard_normal((n, r)) * 0.02).astype(np.float32)
+    lora = Q.LoraAdapter(a, bm, 2.0)
+    lin = Q.QuantizedLinear(*host["gate_proj"])
+    for m, x in ((1, x1), (2048, x2)):
+        y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        t_plain = graph_ms_steady(torch, lambda: lin.forward(x, out=y)) * 1e3
+        t_lora = graph_ms_steady(torch, lambda: lin.forward_lora(x, lora, out=y)) * 1e3
+        out[f"lora_r16_gate_m{m}"] = {"us_plain": round(t_plain, 2), "us_lora": round(t_lora, 2),
+                                      "overhead_us": round(t_lora - t_plain, 2)}
+    lin.close()
+    lora.close()
+    return out
 
 
 def summarize_trace(db_path: str, out_md: str, command: str) -> None:
@@ -748,9 +806,11 @@ def main() -> int:
     if args.roofline_only:
         us_gu = pair_us(1)
         cgbs = copy_gbs(torch)
+        rd = read_gbs(torch, reps=10)
         print(json.dumps({"kernel": gu_kernel, "algo_bytes_per_launch": gu_bytes, "avg_launch_us": round(us_gu, 3),
                           "achieved_GBps": round(gu_bytes / (us_gu * 1e-6) / 1e9, 1),
-                          "copy_bytes": COPY_BYTES, "copy_GBps": round(cgbs, 1)}), flush=True)
+                          "copy_bytes": COPY_BYTES, "copy_GBps": round(cgbs, 1),
+                          "read_probe_bytes": rd["bytes"], "read_probe_GBps": rd["GBps"]}), flush=True)
         return 0
 
     layer_w_bytes = sum(wbytes_of.values())
@@ -859,6 +919,14 @@ def main() -> int:
                      "gemv_config1_frac_of_read": round(gbs1 / rd["GBps"], 4),
                      "gemm_frac_of_dense": round(head["TFLOPS"] / dense, 4)}
 
+    variants = None
+    if not args.quick:
+        log("8-bit and LoRA variants on the gate_proj shape")
+        try:
+            variants = variants_run(torch, Q, host)
+        except Exception as e:  # memory or build problems should not hide the headline
+            variants = {"error": str(e)}
+
     model = None
     if not args.quick:
         log("48-layer decoder: 16K prefill + 128 decode steps (quantized matmuls only)")
@@ -901,6 +969,7 @@ def main() -> int:
         "decode_per_projection": per_proj,
         "lm_head": lm,
         "prefill_gemm": gemm,
+        "variants_8bit_lora": variants,
         "model_48_layers": model,
         "practical_peaks": peaks,
     }

@@ -12,7 +12,10 @@
 //
 // Tiling: a 512-thread workgroup computes a 256 (M) x 256 (N) tile as 2 x 4 waves
 // of 128 x 64 (two waves per SIMD, so one's MFMA and LDS latencies are covered by
-// the other's work).  Everything streams through LDS by direct-to-LDS buffer loads
+// the other's work); or 128 x 256 (2 x 4 waves of 64 x 64).  The kernel is written
+// for tiles of BN = 128 too (four waves, 78 KiB of LDS: two workgroups per CU); a
+// forced-plan sweep over the benchmark's shapes measured it within 6% of the two
+// tiles above where it helped at all, so the plan does not use it.  Everything streams through LDS by direct-to-LDS buffer loads
 // (no staging registers): per 64-wide group the x tile (rows swizzled so the MFMA
 // operand reads are bank-conflict free), the group's weight words and scale words;
 // the bias operands once per 8 groups.  The rings have three slots, so each load has
@@ -23,13 +26,8 @@
 namespace q4 {
 namespace {
 
-constexpr int kBM = 256;              // workgroup tile rows (M), the taller of the two tile shapes
-constexpr int kBN = 256;              // workgroup tile columns (N)
-constexpr int kWaves = 8;             // 2 (M) x 4 (N) waves, two per SIMD
-constexpr int kRB = kBN / 16;         // 16-row weight blocks per workgroup tile
 constexpr int kWN = 64;               // wave tile columns
 constexpr int kNT = kWN / 16;         // 16x16 tiles per wave along N
-constexpr int kXChunks = kBM * 8;     // 16-byte chunks of one x group tile (256 rows x 64 bf16)
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -111,41 +109,49 @@ __device__ __forceinline__ void tile_of(int id, int nwg, int mtiles, int ntiles,
     nt = r / bm;
 }
 
-// LDS rings.  x: three slots of one group each (group g in slot g % 3; the loads for
-// g+2 are in flight while g is multiplied).  Weights: two slots of one group pair
-// each (pair p in slot p % 2, loaded with the x of its first group), holding the
-// tiled words of the workgroup's 16 row blocks [row block][lane] (16 KiB) followed
-// by their scale/bias words [row block][row] as uint2 (2 KiB).  Every load is a
-// 16-byte-per-lane DMA: 4-byte LDS DMAs cost the load pipe about twice the cycles
-// for a quarter of the bytes.  Each slot is its own object so the compiler can tell
-// a DMA into one slot from reads of another (a shared array would make it wait for
-// every DMA before every read); it tells apart at most eight such objects.
-constexpr int kWPair = kRB * 64;          // uint4: tiled words of the pair
-constexpr int kSPair = kRB * 16 / 2;      // uint4: scale/bias words of the pair
-__shared__ uint4 g_xs0[kXChunks];          // x group tile, 256 rows x 64 (32 KiB)
-__shared__ uint4 g_xs1[kXChunks];
-__shared__ uint4 g_xs2[kXChunks];
-__shared__ uint4 g_wp0[kWPair + kSPair];   // 18 KiB
-__shared__ uint4 g_wp1[kWPair + kSPair];
-// one octet's bias operands: A side for the 256 rows [m16][lane] (16 KiB), then the
-// scale/bias words as uint2 [row block][pair][column] (8 KiB)
-__shared__ uint4 g_xab[16 * 64 + kRB * 4 * 16 / 2];
+// LDS rings (declared per instantiation inside the kernel, sized by its tile).
+// x: three slots of one group each (group g in slot g % 3; the loads for g+2 are in
+// flight while g is multiplied).  Weights: two slots of one group pair each (pair p
+// in slot p % 2, loaded with the x of its first group), holding the tiled words of
+// the workgroup's row blocks [row block][lane] followed by their scale/bias words
+// [row block][row] as uint2.  Every load is a 16-byte-per-lane DMA: 4-byte LDS DMAs
+// cost the load pipe about twice the cycles for a quarter of the bytes.  Each slot is
+// its own object so the compiler can tell a DMA into one slot from reads of another
+// (a shared array would make it wait for every DMA before every read); it tells apart
+// at most eight such objects.
 
-
-template <int OUT, int BM>
-__global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ tiles, const uint2* __restrict__ sb,
+template <int OUT, int BM, int BN>
+__global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ tiles, const uint2* __restrict__ sb,
                                                    const uint16_t* __restrict__ x, const uint4* __restrict__ xaug,
                                                    void* __restrict__ y, int m_rows, int n_rows, int k, int groups,
                                                    int gpairs, int mtiles, int ntiles, int octets, uint32_t tile_bytes,
                                                    uint32_t sb_bytes, int g_split, long split_stride, int n_out,
                                                    const uint16_t* __restrict__ gelu_table) {
     // BM = 256: 2 x 4 waves of 128 x 64; BM = 128: 2 x 4 waves of 64 x 64 (more
-    // workgroups for small M without splitting K)
+    // workgroups for small M without splitting K); BN = 128: 2 x 2 waves
     static_assert(BM == 256 || BM == 128, "tile rows");
+    static_assert(BN == 256 || BN == 128, "tile columns");
+    constexpr int kWaves = 2 * (BN / kWN);        // 2 (M) x BN/64 (N) waves
+    constexpr int kRB = BN / 16;                  // 16-row weight blocks per workgroup tile
+    constexpr int kXChunks = BM * 8;              // 16-byte chunks of one x group tile (BM rows x 64 bf16)
+    constexpr int kWPair = kRB * 64;              // uint4: tiled words of the pair
+    constexpr int kSPair = kRB * 16 / 2;          // uint4: scale/bias words of the pair
+    constexpr int kXaA = BM / 16 * 64;            // uint4: the bias A operands of the tile's rows
     constexpr int kWM = BM / 2;                   // wave tile rows
     constexpr int kMT = kWM / 16;                 // 16x16 tiles per wave along M
     constexpr int kXParts = BM * 8 / (64 * kWaves);  // 16-byte x loads per wave per group
-    constexpr int kXaParts = BM / 128;            // bias A-operand loads per wave per octet
+    constexpr int kXaParts = BM / 16 / kWaves;    // bias A-operand loads per wave per octet
+    constexpr int kSWaves = kRB / 8;              // waves that load a pair's scale words (1 KiB each)
+    static_assert(kRB == 2 * kWaves, "two row blocks of tiled words per wave per pair");
+    static_assert(kXParts >= 1 && kXaParts >= 1, "every wave loads x and bias operands");
+    __shared__ uint4 g_xs0[kXChunks];             // x group tiles (BM rows x 64: 16 or 32 KiB)
+    __shared__ uint4 g_xs1[kXChunks];
+    __shared__ uint4 g_xs2[kXChunks];
+    __shared__ uint4 g_wp0[kWPair + kSPair];      // a pair's weights: 9 or 18 KiB
+    __shared__ uint4 g_wp1[kWPair + kSPair];
+    // one octet's bias operands: A side for the tile's rows [m16][lane], then the
+    // scale/bias words as uint2 [row block][pair][column]
+    __shared__ uint4 g_xab[kXaA + kRB * 4 * 16 / 2];
     int mt, nt;
     tile_of((int)blockIdx.x, (int)gridDim.x, mtiles, ntiles, mt, nt);
     // split of K: groups [g_begin, g_end), whole octets; with several splits each
@@ -183,7 +189,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
                            // LDS row (swizzle: conflict-free MFMA operand reads)
 #pragma unroll
     for (int u = 0; u < kXParts; ++u) {
-        const int q = (8 * u + wave) * 64 + lane;
+        const int q = (kWaves * u + wave) * 64 + lane;
         const int r = q >> 3;
         const int c = (q & 7) ^ ((r >> 1) & 7);
         const int row = mt * BM + r;
@@ -195,13 +201,13 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         const int rb = rbw + 2 * wave + t;
         wv[t] = rb < nblocks ? ((uint32_t)rb * (uint32_t)gpairs * 64u + (uint32_t)lane) * 16u : kOutOfRange;
     }
-    uint32_t sv;  // scale words of a pair (waves 0, 1): row block 8w + l/8, chunk l%8 of its 128 bytes
+    uint32_t sv;  // scale words of a pair (waves w < kSWaves): row block 8w + l/8, chunk l%8 of its 128 bytes
     {
         const int rb = rbw + 8 * wave + (lane >> 3);
         sv = rb < nblocks ? (uint32_t)rb * (uint32_t)gpairs * 128u + (uint32_t)(lane & 7) * 16u : kOutOfRange;
     }
     auto dma_x = [&](int g, int part, uint4* xdst) {
-        dma16(g < g_end ? xrs : zrs, xdst + (8 * part + wave) * 64, xv[part], (uint32_t)g * 128u);
+        dma16(g < g_end ? xrs : zrs, xdst + (kWaves * part + wave) * 64, xv[part], (uint32_t)g * 128u);
     };
     auto dma_w = [&](int p, int part, uint4* wdst) {
         dma16(p < p_end ? trs : zrs, wdst + (2 * wave + part) * 64, wv[part], (uint32_t)p * 1024u);
@@ -225,7 +231,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         const int chunk = ln & 31;
         const bool ok = (rb < nblocks) & (4 * o + (chunk >> 3) < gpairs);
         const uint32_t raw = ((uint32_t)rb * (uint32_t)gpairs + 4u * (uint32_t)o) * 128u + (uint32_t)chunk * 16u;
-        dma16(srs, g_xab + (16 * 64 + wave * 64), ok ? raw : kOutOfRange);
+        dma16(srs, g_xab + (kXaA + wave * 64), ok ? raw : kOutOfRange);
     };
 
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -307,7 +313,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     auto bias = [&]() {
         bf16x8 bb[kNT];
 #pragma unroll
-        for (int j = 0; j < kNT; ++j) bb[j] = bias_operand(reinterpret_cast<const uint2*>(g_xab + 16 * 64)[((wn * kNT + j) * 4 + kq) * 16 + col]);
+        for (int j = 0; j < kNT; ++j) bb[j] = bias_operand(reinterpret_cast<const uint2*>(g_xab + kXaA)[((wn * kNT + j) * 4 + kq) * 16 + col]);
 #pragma unroll
         for (int i = 0; i < kMT; ++i) {
             const bf16x8 aa = __builtin_bit_cast(bf16x8, g_xab[(wm * kMT + i) * 64 + lane]);
@@ -328,7 +334,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     // (past the end they read zeros), so the counts are fixed.
     auto issues_xa = [&](int g) { return (g & 7) == 1 && g > g_begin + 1; };
     auto issued = [&](int g) {  // loads this wave issues at step g
-        return kXParts + ((g & 1) == 0 ? 2 + (wave < 2 ? 1 : 0) : 0) + (issues_xa(g) ? kXaParts + 1 : 0);
+        return kXParts + ((g & 1) == 0 ? 2 + (wave < kSWaves ? 1 : 0) : 0) + (issues_xa(g) ? kXaParts + 1 : 0);
     };
     auto step = [&](int g, const uint4* xs, const uint4* wp, uint4* xs2, uint4* wp2) {
         if (g == g_begin) {
@@ -336,12 +342,15 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         } else {
             switch (issued(g - 1)) {
                 case 2: wait_vm_lds<2>(); break;
+                case 3: wait_vm_lds<3>(); break;
                 case 4: wait_vm_lds<4>(); break;
                 case 5: wait_vm_lds<5>(); break;
                 case 6: wait_vm_lds<6>(); break;
                 case 7: wait_vm_lds<7>(); break;
+                case 8: wait_vm_lds<8>(); break;
                 case 9: wait_vm_lds<9>(); break;
                 case 10: wait_vm_lds<10>(); break;
+                case 11: wait_vm_lds<11>(); break;
                 default: wait_vm_lds<0>(); break;  // (not reached) safe fallback
             }
         }
@@ -350,7 +359,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
         if (issues_xa(g)) dma_xa(g >> 3);
         // the pair's scale words (waves 0, 1), issued here rather than inside the
         // product stream, which then has no branch
-        if ((g & 1) == 0 && wave < 2) dma_s((g + 2) >> 1, wp2);
+        if ((g & 1) == 0 && wave < kSWaves) dma_s((g + 2) >> 1, wp2);
         const bool pair = (g & 1) == 0;
         compute(xs, wp, g & 1, [&](int t) {
             if ((t & 1) && (t >> 1) < kXParts) dma_x(g + 2, t >> 1, xs2);
@@ -367,7 +376,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     }
     dma_w(g_begin >> 1, 0, g_wp0);
     dma_w(g_begin >> 1, 1, g_wp0);
-    if (wave < 2) dma_s(g_begin >> 1, g_wp0);
+    if (wave < kSWaves) dma_s(g_begin >> 1, g_wp0);
     dma_xa(g_begin >> 3);
     wait_vm<0>();
 
@@ -411,11 +420,11 @@ __global__ __launch_bounds__(512) void gemm_kernel(const uint4* __restrict__ til
     const uint16_t* gtab = reinterpret_cast<const uint16_t*>(g_xs0);
     if constexpr (OUT == kOutGegluBf16) {
         constexpr int kTabChunks = kGeluTable * 2 / 16;
-        static_assert(kTabChunks <= 64 * kWaves && kTabChunks <= kXChunks, "one 16-byte chunk per thread");
+        static_assert(kTabChunks <= kXChunks, "the table fits one x slot");
         wait_lds();  // this wave's operand reads have returned
         lds_barrier();
-        const int t = wave * 64 + slane;
-        if (t < kTabChunks) g_xs0[t] = reinterpret_cast<const uint4*>(gelu_table)[t];
+        for (int t = wave * 64 + slane; t < kTabChunks; t += 64 * kWaves)
+            g_xs0[t] = reinterpret_cast<const uint4*>(gelu_table)[t];
         __syncthreads();
     }
 #pragma unroll
@@ -555,19 +564,27 @@ __global__ void split_geglu_kernel(const float* __restrict__ part, void* __restr
 
 }  // namespace
 
-// Tile shape and split of K.  For each tile height (256 rows, or 128 rows with half
-// the products per group step) and split count (whole octets per split), the cost is
+// Tile shape and split of K.  For each tile shape (256 x 256 or 128 x 256) and split
+// count (whole octets per split), the cost is
 // rounds-of-workgroups x octets-per-split x the measured step time, plus the partial
 // sums' extra traffic; the cheapest wins.
+namespace {
+struct TileShape {
+    int bm, bn, per_cu;
+    double step_us;  // one 64-wide group step of a workgroup at that occupancy (measured)
+};
+constexpr TileShape kTileShapes[] = {{256, 256, 1, 2.0}, {128, 256, 1, 1.15}};
+}  // namespace
+
 GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
     GemmPlan p;
     const int octets = (l.g + 7) / 8;
     const long cus = device_cus();
     const double bytes_per_us = 6.0e6;  // partial sums written and read back, largely through the caches
     double best = -1.0;
-    for (int bm : {256, 128}) {
-        const double step_us = bm == 256 ? 2.0 : 1.15;  // one 64-wide group step (measured)
-        const long tiles = (long)((m + bm - 1) / bm) * ((l.n + kBN - 1) / kBN);
+    for (const TileShape& ts : kTileShapes) {
+        const int bm = ts.bm, bn = ts.bn;
+        const long tiles = (long)((m + bm - 1) / bm) * ((l.n + bn - 1) / bn);
         for (int s = 1; s <= octets && s <= kMaxSplits; ++s) {
             const int per = (octets + s - 1) / s;
             const int used = (octets + per - 1) / per;  // splits that get work
@@ -576,11 +593,12 @@ GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
             if (part > kMaxPartialBytes) break;
             const size_t m16 = ((size_t)m + bm - 1) / bm * (bm / 16);
             if (m16 * octets * 64 * 16 + part > max_workspace) break;  // (more splits need more)
-            const double rounds = (double)((tiles * s + cus - 1) / cus);
-            const double t = rounds * per * 8 * step_us + (s > 1 ? 3.0 + part / bytes_per_us : 0.0);
+            const double rounds = (double)((tiles * s + cus * ts.per_cu - 1) / (cus * ts.per_cu));
+            const double t = rounds * per * 8 * ts.step_us + (s > 1 ? 3.0 + part / bytes_per_us : 0.0);
             if (best < 0.0 || t < best) {
                 best = t;
                 p.bm = bm;
+                p.bn = bn;
                 p.splits = s;
                 p.g_split = per * 8;
                 p.part_bytes = part;
@@ -609,7 +627,7 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     if (plan.xaug_bytes + plan.part_bytes > workspace_bytes) return hipErrorInvalidValue;
     const int octets = (l.g + 7) / 8;
     const int mtiles = (m + plan.bm - 1) / plan.bm;
-    const int ntiles = (l.n + kBN - 1) / kBN;
+    const int ntiles = (l.n + plan.bn - 1) / plan.bn;
     uint4* xaug = static_cast<uint4*>(workspace);
     float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.xaug_bytes);
     if (l.tile_bytes() > kMaxBufferBytes || l.sb_bytes() > kMaxBufferBytes ||
@@ -621,18 +639,23 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    const dim3 grid((unsigned)(mtiles * ntiles), (unsigned)plan.splits), block(64 * kWaves);
+    const dim3 grid((unsigned)(mtiles * ntiles), (unsigned)plan.splits), block(2 * plan.bn);
     const uint32_t tb = (uint32_t)l.tile_bytes(), sbb = (uint32_t)l.sb_bytes();
     const long elems = (long)m * l.n;
+    // one instantiation per (output mode, tile shape)
+#define Q4_GEMM_LAUNCH(MODE, YPTR, STRIDE)                                                                       \
+    do {                                                                                                         \
+        if (plan.bm == 256)                                                                                      \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,  \
+                               l.n, l.k, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, STRIDE, n_out,  \
+                               gelu_table);                                                                      \
+        else                                                                                                     \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 128, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,  \
+                               l.n, l.k, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, STRIDE, n_out,  \
+                               gelu_table);                                                                      \
+    } while (0)
     if (plan.splits > 1) {
-        if (plan.bm == 128)
-            hipLaunchKernelGGL((gemm_kernel<kOutF32, 128>), grid, block, 0, stream, tiles, sb, x, xaug, (void*)part, m,
-                               l.n, l.k, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, elems, n_out,
-                               gelu_table);
-        else
-            hipLaunchKernelGGL((gemm_kernel<kOutF32, 256>), grid, block, 0, stream, tiles, sb, x, xaug, (void*)part, m,
-                               l.n, l.k, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, elems, n_out,
-                               gelu_table);
+        Q4_GEMM_LAUNCH(kOutF32, (void*)part, elems);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const int rblock = 256;
@@ -655,20 +678,11 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
                                plan.splits);
         return hipGetLastError();
     }
-#define Q4_GEMM_LAUNCH(MODE)                                                                                    \
-    do {                                                                                                        \
-        if (plan.bm == 128)                                                                                     \
-            hipLaunchKernelGGL((gemm_kernel<MODE, 128>), grid, block, 0, stream, tiles, sb, x, xaug, y, m, l.n, l.k, \
-                               l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L, n_out, gelu_table);   \
-        else                                                                                                    \
-            hipLaunchKernelGGL((gemm_kernel<MODE, 256>), grid, block, 0, stream, tiles, sb, x, xaug, y, m, l.n, l.k, \
-                               l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, 0L, n_out, gelu_table);   \
-    } while (0)
     switch (out_mode) {
-        case kOutF32: Q4_GEMM_LAUNCH(kOutF32); break;
-        case kOutGegluBf16: Q4_GEMM_LAUNCH(kOutGegluBf16); break;
-        case kOutGegluF32: Q4_GEMM_LAUNCH(kOutGegluF32); break;
-        default: Q4_GEMM_LAUNCH(kOutBf16); break;
+        case kOutF32: Q4_GEMM_LAUNCH(kOutF32, y, 0L); break;
+        case kOutGegluBf16: Q4_GEMM_LAUNCH(kOutGegluBf16, y, 0L); break;
+        case kOutGegluF32: Q4_GEMM_LAUNCH(kOutGegluF32, y, 0L); break;
+        default: Q4_GEMM_LAUNCH(kOutBf16, y, 0L); break;
     }
 #undef Q4_GEMM_LAUNCH
     return hipGetLastError();

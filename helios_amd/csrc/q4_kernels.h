@@ -79,6 +79,7 @@ hipError_t launch_greedy_reduce(const unsigned long long* part, int nb, int rows
 // needs, and with that much the launch runs the unconstrained plan.
 struct GemmPlan {
     int bm = 256;            // output tile rows: 256, or 128 for small M
+    int bn = 256;            // output tile columns
     int splits = 1;          // workgroups along K per output tile
     int g_split = 0;         // groups per split (whole octets)
     size_t xaug_bytes = 0;   // group sums of x

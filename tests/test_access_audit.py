@@ -50,14 +50,18 @@ def tile_of(bid, nwg, mtiles, ntiles):
     return band * 2 + r % bm, r // bm
 
 
-def audit_gemm(m, n, k, BM, splits):
+def audit_gemm(m, n, k, BM, splits, BN=256):
     L = layout(n, k)
-    BN, RB, WAVES = 256, 16, 8
+    WAVES = 2 * BN // 64   # 2 (M) x BN/64 (N)
+    RB = BN // 16
     WM = BM // 2
-    XP = BM * 8 // 512     # x DMA parts per wave per group
-    XA = BM // 128         # bias A-operand DMA parts per wave per octet
+    XP = BM * 8 // (64 * WAVES)   # x DMA parts per wave per group
+    XA = BM // 16 // WAVES        # bias A-operand DMA parts per wave per octet
+    SW = RB // 8                  # waves loading a pair's scale words
+    assert RB == 2 * WAVES and XP >= 1 and XA >= 1
     KWP, KSP = RB * 64, RB * 16 // 2  # uint4 units of one weight slot
-    BIAS_SLOT = 16 * 64 + RB * 4 * 16 // 2  # uint4 units: A operands, then the octet's scale/bias words
+    XAA = BM // 16 * 64               # uint4 units of the bias A operands
+    BIAS_SLOT = XAA + RB * 4 * 16 // 2  # uint4 units: A operands, then the octet's scale/bias words
     G = L["g"]
     octets = (G + 7) // 8
     mtiles = (m + BM - 1) // BM
@@ -76,16 +80,20 @@ def audit_gemm(m, n, k, BM, splits):
         mt, nt = tile_of(bid, nwg, mtiles, ntiles)
         assert 0 <= mt < mtiles and 0 <= nt < ntiles
         seen.add((mt, nt))
+        # interior tiles repeat the first one's pattern shifted inside the buffers: the
+        # edge tiles (first and last along M and N) bound every access
+        if mt not in (0, mtiles - 1) and nt not in (0, ntiles - 1):
+            continue
         rbw = nt * RB
         for wave in range(WAVES):
             wm, wn = wave & 1, wave >> 1
             # DMA offsets: per-lane constants + a scalar step offset (group, pair, octet)
             for part in range(XP):
-                q = (8 * part + wave) * 64 + lane
+                q = (WAVES * part + wave) * 64 + lane
                 rr = q >> 3
                 c = (q & 7) ^ ((rr >> 1) & 7)
                 row = mt * BM + rr
-                assert ((8 * part + wave) * 64 + 64) <= BM * 8
+                assert ((WAVES * part + wave) * 64 + 64) <= BM * 8
                 xv = np.where(row < m, (row * k + 8 * c) * 2, OOB)
                 for g in (0, G - 1):  # a per-lane constant plus g * 128: the extremes bound every step
                     chk_buf("gemm x", np.where(xv == OOB, OOB, xv + g * 128), 16, xbytes, xbytes)
@@ -94,7 +102,7 @@ def audit_gemm(m, n, k, BM, splits):
                 wv = np.where(rb < nblocks, (rb * L["gp"] * 64 + lane) * 16, OOB)
                 for p in (0, L["gp"] - 1):
                     chk_buf("gemm w", np.where(wv == OOB, OOB, wv + p * 1024), 16, L["tile_bytes"], L["tile_bytes"])
-            if wave < 2:
+            if wave < SW:
                 rb = rbw + 8 * wave + (lane >> 3)
                 sv = np.where(rb < nblocks, rb * L["gp"] * 128 + (lane & 7) * 16, OOB)
                 for p in (0, L["gp"] - 1):
@@ -102,7 +110,7 @@ def audit_gemm(m, n, k, BM, splits):
             for o in sorted({0, octets - 1}):
                 for u in range(XA):
                     m16 = XA * wave + u
-                    assert m16 * 64 + 64 <= 1024
+                    assert m16 * 64 + 64 <= XAA
                     off = ((mt * (BM // 16) + m16) * octets + o) * 1024 + lane * 16
                     chk_buf("gemm xa", off, 16, ws_bytes, ws_bytes)
                 rb = rbw + 2 * wave + (lane >> 5)
@@ -110,7 +118,7 @@ def audit_gemm(m, n, k, BM, splits):
                 ok = (rb < nblocks) & (4 * o + (chunk >> 3) < L["gp"])
                 raw = (rb * L["gp"] + 4 * o) * 128 + chunk * 16
                 chk_buf("gemm bias words", np.where(ok, raw, OOB), 16, L["sb_bytes"], L["sb_bytes"])
-                assert 16 * 64 + wave * 64 + 63 < BIAS_SLOT  # the scale/bias part of the bias slot
+                assert XAA + wave * 64 + 63 < BIAS_SLOT  # the scale/bias part of the bias slot
             # LDS operand reads of the 16x16x32 product stream
             kq = lane >> 4
             for j in range(4):  # the wave's four row blocks
@@ -122,7 +130,7 @@ def audit_gemm(m, n, k, BM, splits):
                 for c in (kq, 4 + kq):
                     idx = r * 8 + (c ^ ((r >> 1) & 7))
                     assert (idx >= 0).all() and (idx < BM * 8).all()
-                assert (wm * (WM // 16) + i) * 64 + 64 <= 1024  # bias A operands
+                assert (wm * (WM // 16) + i) * 64 + 64 <= XAA  # bias A operands
             # stores: rows 4*kq + e of each 16-row tile, column l16 of the row block
             for i in range(WM // 16):
                 for e in range(4):
@@ -134,8 +142,9 @@ def audit_gemm(m, n, k, BM, splits):
         gb = sp * g_split
         ge = min(G, gb + g_split)
         assert gb < ge and gb % 8 == 0
-    # LDS: three x slots, two weight slots, the bias slot
-    assert 3 * 256 * 8 * 16 + 2 * (KWP + KSP) * 16 + BIAS_SLOT * 16 <= LDS_BYTES
+    # LDS: three x slots, two weight slots, the bias slot; two 128 x 128 workgroups per CU
+    lds = 3 * BM * 8 * 16 + 2 * (KWP + KSP) * 16 + BIAS_SLOT * 16
+    assert lds <= (LDS_BYTES if BN == 256 else LDS_BYTES // 2)
 
 
 GEMM_SHAPES = [(33, 40, 384), (300, 256, 640), (257, 130, 320), (64, 512, 3840), (512, 2048, 3840),
@@ -144,13 +153,13 @@ GEMM_SHAPES = [(33, 40, 384), (300, 256, 640), (257, 130, 320), (64, 512, 3840),
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
-@pytest.mark.parametrize("bm", [256, 128])
-def test_gemm_accesses(m, n, k, bm):
+@pytest.mark.parametrize("bm,bn", [(256, 256), (128, 256)])
+def test_gemm_accesses(m, n, k, bm, bn):
     octets = (k // 64 + 7) // 8
     for s in sorted({1, 2, min(8, octets), octets}):
         per = (octets + s - 1) // s
         if (octets + per - 1) // per == s:
-            audit_gemm(m, n, k, bm, s)
+            audit_gemm(m, n, k, bm, s, bn)
 
 
 # ----------------------------------------------------------------------- decode

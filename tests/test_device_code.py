@@ -43,7 +43,7 @@ def gemm_asm():
 
 def test_lds_dma_sgpr_hazards_covered(gemm_asm):
     kernels = list(_kernels(gemm_asm))
-    assert len(kernels) == 8  # bf16 / fp32 outputs, bf16 / fp32 GeGLU pairs; 256- and 128-row tiles
+    assert len(kernels) == 8  # bf16 / fp32 outputs, bf16 / fp32 GeGLU pairs; 256x256 and 128x256 tiles
     for name, lines in kernels:
         dmas = 0
         for i, line in enumerate(lines):
@@ -72,6 +72,11 @@ def test_no_spills_and_lds_budget(gemm_asm):
         assert vals and max(vals) == 0, (field, vals)
     lds = [int(v) for v in re.findall(r"\.group_segment_fixed_size:\s+(\d+)", gemm_asm)]
     assert max(lds) <= 160 * 1024
+    # the 128 x 128 tile runs two workgroups per CU (the plan's occupancy assumption)
+    for m in re.finditer(r"\.group_segment_fixed_size:\s+(\d+).*?\.name:\s+(\S+).*?\.vgpr_count:\s+(\d+)",
+                         gemm_asm, re.S):
+        if "gemm_kernelILi" in m.group(2) and "ELi128ELi128E" in m.group(2):
+            assert int(m.group(1)) <= 80 * 1024 and int(m.group(3)) <= 256, m.group(2)
 
 
 def _kernel_meta(asm: str):

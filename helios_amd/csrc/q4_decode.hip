@@ -1,4 +1,5 @@
-// Decode-shape affine-Q4 matmul on gfx950: y[M,N] = x[M,K] . W^T for M < 32, in
+// Decode-shape affine-Q4 matmul on gfx950: y[M,N] = x[M,K] . W^T for M < 32 (and
+// beyond, for weights small enough that slabs beat the GEMM's fixed costs), in
 // 16-row slabs (one launch; slab = blockIdx.y).
 //
 // Bandwidth-bound: every weight byte is read once from HBM with 16-byte coalesced
@@ -598,16 +599,24 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
     // variant below is ahead of streaming (12.0 vs 12.6 us at M = 3, 12.5 vs 13.7 at 4;
     // behind at M = 2)
     const bool one_pass = MT >= 4 && l.gp % 8 == 0 && l.gp / 8 <= 16 && l.gp / 4 > 16;
-    if (!one_pass && stream_lds + static_lds <= kLdsPerCu) {
-        // persistent streaming kernel: 4 pairs per chunk, up to 8 waves per workgroup
-        int waves = (l.gp + GPW - 1) / GPW;
-        if (waves > 8) waves = 8;
-        if (waves > l.gp) waves = l.gp;
-        int per_cu = 20 / waves > 0 ? 20 / waves : 1;
-        const int lds_fit = (int)(kLdsPerCu / (stream_lds + static_lds));
-        if (per_cu > lds_fit) per_cu = lds_fit;
-        const int capacity = device_cus() * per_cu;
-        const int per_wg = (l.nb + capacity - 1) / capacity;
+    // persistent streaming kernel: 4 pairs per chunk, up to 8 waves per workgroup
+    int waves = (l.gp + GPW - 1) / GPW;
+    if (waves > 8) waves = 8;
+    if (waves > l.gp) waves = l.gp;
+    int per_cu = 20 / waves > 0 ? 20 / waves : 1;
+    const int lds_fit = (int)(kLdsPerCu / (stream_lds + static_lds));
+    if (per_cu > lds_fit) per_cu = lds_fit;
+    const int capacity = device_cus() * (per_cu > 0 ? per_cu : 1);
+    const int per_wg = (l.nb + capacity - 1) / capacity;
+    // Slabs of 5-16 rows with one or two row blocks per workgroup: staging x (up to
+    // 16 rows of K) costs each workgroup more than its weights, and the per-block
+    // kernel below, reading x straight from L2, is ahead: q_proj 4096x3840 at M = 16
+    // 7.7 vs 9.0 us, at M = 64 20.4 vs 31.6; k_proj 2048x3840 at M = 128 19.4 vs
+    // 30.7; the fused qkv 8192x3840 (two blocks per workgroup) 20.9 vs 22.1 at M = 32
+    // (behind at one slab, 12.3 vs 12.0).  gate 15360x3840 (four per workgroup) stays
+    // streaming: 15.4 vs 20.7 at M = 16.
+    const bool few_blocks = MT == 16 && (per_wg == 1 || (per_wg == 2 && slabs > 1));
+    if (!one_pass && !few_blocks && lds_fit > 0) {
         const int grid = (l.nb + per_wg - 1) / per_wg;
         // one workgroup per CU and a long walk (the lm_head at M = 8: 126 vs 135 us):
         // four chunks per wave in flight.  Not for short walks (down and the gate|up

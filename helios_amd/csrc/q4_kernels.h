@@ -111,7 +111,19 @@ int lora_slices(int k);
 hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float* part, void* y, int m, int n, int k,
                        int rank, float scale, bool out_f32, hipStream_t stream);
 
-// Rows at or above which forward uses the GEMM path.
+// Forward path choice (automatic mode): the decode kernels below kGemmMinRows rows,
+// and beyond that while rows x N x K stays at most kDecodeMaxWork.  Measured per
+// shape as whole forwards (graph replays) at 33-256 rows: the decode kernels' cost
+// grows by one weight pass per 16-row slab (~4 us per 16M weights), the GEMM's is
+// ~30 us of fixed cost (group sums of x, split-K reduction, tile prologue) plus its
+// MFMA time.  Ties: 4096x3840 at ~128 rows (2.0e9), 2048x3840 at ~224 (1.8e9),
+// 8192x3840 and 3840x8192 at ~50 (1.6e9), 15360x3840 at ~40 (2.4e9); 3840x15360
+// (K of 120 pairs) is ahead on the GEMM from 32 rows (1.9e9).
 constexpr int kGemmMinRows = 32;
+constexpr double kDecodeMaxWork = 1.6e9;
+inline bool use_decode(long rows, const Layout& l, int gemm_min_rows) {
+    if (gemm_min_rows > 0) return rows < gemm_min_rows;
+    return rows < kGemmMinRows || (double)rows * (double)l.n * (double)l.k <= kDecodeMaxWork;
+}
 
 }  // namespace q4

@@ -7,6 +7,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <climits>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -22,6 +24,8 @@ constexpr uint64_t kQLinearMagic = 0x47454d3451344c4eULL;  // "GEM4Q4LN"
 constexpr int kGreedyMaxRows = 16;  // rows per greedy-head call (decode and verify blocks)
 constexpr uint64_t kLoraMagic = 0x47454d344c4f5241ULL;  // "GEM4LORA"
 thread_local char g_last_error[512] = "";
+// forward path choice: 0 = automatic (q4::use_decode), r > 0 = the GEMM from r rows on
+std::atomic<uint32_t> g_gemm_min_rows{0};
 
 // Records the message (truncated to the buffer) and returns status.  The const char*
 // forms build no std::string, so they cannot throw: catch blocks use them.
@@ -386,7 +390,7 @@ Gemma4Status dispatch_forward(const Gemma4QLinear* linear, const uint16_t* x_dev
     Gemma4Status pst = prepare_x(linear, x_dev, rows, sc, name, &x_dev);
     if (pst != GEMMA4_OK) return pst;
     hipError_t e;
-    if ((int)rows < q4::kGemmMinRows) {
+    if (q4::use_decode(rows, linear->layout, (int)g_gemm_min_rows.load(std::memory_order_relaxed))) {
         const q4::OutParams op{y_dev, nullptr, mode, n_out, 0, 0.0f};
         e = q4::launch_decode(linear->tiles, linear->sb, x_dev, op, (int)rows, linear->layout, sc.stream);
         if (e != hipSuccess) return hip_fail((name + ": decode launch").c_str(), e);
@@ -484,6 +488,10 @@ Gemma4Status gemma4_qmm_get_last_error(char* buffer, size_t buffer_len) {
     } catch (...) {
         return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qmm_get_last_error: unexpected native exception");
     }
+}
+
+uint32_t gemma4_qmm_set_gemm_min_rows(uint32_t rows) {
+    return g_gemm_min_rows.exchange(rows > (uint32_t)INT_MAX ? (uint32_t)INT_MAX : rows);
 }
 
 Gemma4Status gemma4_qlinear_create(const Gemma4QLinearDesc* desc, const uint32_t* weight,

@@ -22,6 +22,7 @@ fallback: without the built library every call raises.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import enum
 import os
@@ -92,6 +93,7 @@ def load_library(path: str | None = None):
     sig = {
         "gemma4_qmm_runtime_version": [ctypes.POINTER(_Version)],
         "gemma4_qmm_get_last_error": [ctypes.c_char_p, ctypes.c_size_t],
+        "gemma4_qmm_set_gemm_min_rows": [ctypes.c_uint32],
         "gemma4_qlinear_create": [ctypes.POINTER(_Desc), vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qlinear_create_device": [ctypes.POINTER(_Desc), vp, vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qlinear_free": [vp],
@@ -112,7 +114,7 @@ def load_library(path: str | None = None):
     for name, args in sig.items():
         fn = getattr(lib, name)
         fn.argtypes = args
-        fn.restype = st
+        fn.restype = ctypes.c_uint32 if name == "gemma4_qmm_set_gemm_min_rows" else st
     _lib = lib
     return lib
 
@@ -136,6 +138,25 @@ def runtime_version() -> dict:
     check(lib.gemma4_qmm_runtime_version(ctypes.byref(v)), lib)
     return {"abi_version": v.abi_version, "backend_name": v.backend_name.decode(),
             "backend_version": v.backend_version.decode()}
+
+
+def set_gemm_min_rows(rows: int) -> int:
+    """Pins the forward path for this process: 0 (the default) chooses by shape; r > 0
+    runs the GEMM from r rows on and the decode kernels below.  Returns the previous
+    setting."""
+    if not 0 <= int(rows) < 2 ** 32:
+        raise ValueError(f"rows must be in [0, 2**32), got {rows}")
+    return int(load_library().gemma4_qmm_set_gemm_min_rows(int(rows)))
+
+
+@contextlib.contextmanager
+def gemm_min_rows(rows: int):
+    """set_gemm_min_rows for the duration of a with-block."""
+    prev = set_gemm_min_rows(rows)
+    try:
+        yield
+    finally:
+        set_gemm_min_rows(prev)
 
 
 def _stream_ptr(stream):

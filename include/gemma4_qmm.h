@@ -110,6 +110,20 @@ Gemma4Status gemma4_qmm_runtime_version(Gemma4QmmVersionInfo* out);
  * error message (empty after a success) into buffer, NUL-terminated. */
 Gemma4Status gemma4_qmm_get_last_error(char* buffer, size_t buffer_len);
 
+/* Path choice of the forward calls in this process.  No counterpart in the
+ * reference (MLX picks its own kernels); for tests and benchmarks that pin a path.
+ *   0 (the default): automatic.  The decode kernels (16-row slabs, weights read
+ *     once) below 32 rows, and beyond that while rows * N * K <= 1.6e9 (rows * K'
+ *     * N with K' = 2K for 8-bit handles), the GEMM otherwise: for the Gemma 4
+ *     shapes the decode kernels are ahead of the GEMM's fixed costs up to ~100 rows
+ *     for 4096x3840, ~200 for 2048x3840, ~50 for 8192x3840, at every row count up
+ *     to 800 for 512x3840, and below 32 rows for the MLP projections.
+ *   r > 0: the GEMM from r rows on, the decode kernels below.
+ * Both paths meet the same accuracy contract; they sum in different orders, so the
+ * last bits of some outputs differ between them.  Returns the previous setting.
+ * Takes effect for calls issued after it returns (a process-wide atomic). */
+uint32_t gemma4_qmm_set_gemm_min_rows(uint32_t rows);
+
 /* Load one projection's weight triple from HOST memory in MLX layout onto the
  * current HIP device (the per-prefix tensors the reference keeps in Impl::tensors,
  * native_model.cc:84-104, :3550-3566).  The host arrays may be freed on return. */
@@ -143,7 +157,8 @@ Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, c
  * 64 MiB device array that the library holds on each GPU it runs on until the
  * process ends.  No counterpart in the reference (its MLX ops allocate per call).
  * It calls no hipMalloc, hipFree or allocating library routine.  Scratch needs:
- * none for 4-bit rows < 32; for rows >= 32 the GEMM's group sums of x (rows * K / 8
+ * none for 4-bit calls on the decode path (gemma4_qmm_set_gemm_min_rows); on the
+ * GEMM path the group sums of x (rows * K / 8
  * bytes, rounded up to 128- or 256-row tiles), and split-K partial sums only as far
  * as the array has room (fewer splits than gemma4_qlinear_forward may choose, so the
  * fp32 summation order, and with it the last bits of some outputs, can differ from

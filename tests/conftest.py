@@ -23,3 +23,11 @@ def gpu_lib():
 
     qmm.load_library()
     return qmm
+
+
+@pytest.fixture
+def gemm_from_32(gpu_lib):
+    """Pins the GEMM path from 32 rows on for tests aimed at the GEMM: the automatic
+    choice runs small weights on the decode kernels up to hundreds of rows."""
+    with gpu_lib.gemm_min_rows(32):
+        yield

@@ -84,7 +84,7 @@ def test_gpu_dequantize_golden(gpu_lib):
 @pytest.mark.parametrize("case", CASES)
 @pytest.mark.parametrize("rows", [3, 40])
 @pytest.mark.parametrize("out_dtype", ["bf16", "f32"])
-def test_gpu_forward_golden(gpu_lib, case, rows, out_dtype):
+def test_gpu_forward_golden(gpu_lib, gemm_from_32, case, rows, out_dtype):
     import torch
 
     from test_gpu_parity import BF16_REL, F32_REL, dev_triple, dev_x, host_bits

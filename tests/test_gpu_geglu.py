@@ -80,7 +80,7 @@ def _check(h_dev, g, u, what):
 @pytest.mark.parametrize("f,k,m", [(40, 192, 1), (40, 192, 3), (13, 64, 2), (300, 640, 17), (72, 128, 8),
                                    (13, 64, 33), (300, 640, 40), (136, 1088, 300)])
 @pytest.mark.parametrize("f32", [False, True])
-def test_geglu_small_shapes(gpu_lib, f, k, m, f32):
+def test_geglu_small_shapes(gpu_lib, gemm_from_32, f, k, m, f32):
     import torch
 
     gate, up = _pair(f, k, 500 + f + k)

@@ -30,7 +30,7 @@ def check_bf16_two_roundings(y_bits, want):
 @pytest.mark.parametrize("n,k,m,r", [(4096, 3840, 1, 16), (2048, 3840, 4, 8), (3840, 15360, 8, 16),
                                      (300, 640, 17, 4), (256, 640, 64, 16), (512, 3840, 300, 32)])
 @pytest.mark.parametrize("f32", [False, True])
-def test_lora_forward(gpu_lib, n, k, m, r, f32):
+def test_lora_forward(gpu_lib, gemm_from_32, n, k, m, r, f32):
     import torch
 
     tri = random_triple(n, k, n + k + r)

@@ -144,7 +144,7 @@ def test_dequantize_host_create_edge_groups(gpu_lib):
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 12, 16, 17, 40])
 @pytest.mark.parametrize("f32", [False, True])
-def test_forward_small_shapes(gpu_lib, m, f32):
+def test_forward_small_shapes(gpu_lib, gemm_from_32, m, f32):
     import torch
 
     n, k = 40, 384  # N not a multiple of 16, 6 groups
@@ -275,7 +275,7 @@ def test_forward_rejects_misaligned_x(gpu_lib):
 
 @pytest.mark.parametrize("m", [0, 1, 4, 33])
 @pytest.mark.parametrize("n,k", [(1, 64), (15, 192), (17, 64)])
-def test_forward_empty_rows_and_partial_row_blocks(gpu_lib, m, n, k):
+def test_forward_empty_rows_and_partial_row_blocks(gpu_lib, gemm_from_32, m, n, k):
     """M = 0 returns an empty result without a launch; N of 1, 15 and 17 leave a row
     block mostly or partly empty, on the decode (M = 1, 4) and GEMM (M = 33) paths."""
     import torch
@@ -337,7 +337,7 @@ def test_forward_decode_x_beyond_lds(gpu_lib, m, n, k, f32):
 @pytest.mark.parametrize("n,k,m", [(40, 384, 33), (256, 640, 300), (130, 320, 257), (512, 3840, 64), (16, 64, 33),
                                    (48, 576, 40), (130, 1088, 300)])
 @pytest.mark.parametrize("f32", [False, True])
-def test_gemm_small_shapes(gpu_lib, n, k, m, f32):
+def test_gemm_small_shapes(gpu_lib, gemm_from_32, n, k, m, f32):
     """GEMM path (M >= 32): ragged M and N, odd group counts, outlier activations."""
     import torch
 
@@ -409,6 +409,43 @@ def test_full_attention_projections(gpu_lib, proj, m):
     assert_close(y_bf[rt], y_exact, f"{proj} m={m} bf16")
     assert_rounded(y_bf[rt], y_exact, f"{proj} m={m} bf16", literal=m <= 8)
     assert assert_close(y_f[rt], y_exact, f"{proj} m={m} f32") < (ACC_REL if m <= 8 else 5e-4)
+    lin.close()
+
+
+# (projection, rows) the automatic path choice runs on the decode kernels past 32 rows
+# (rows x N x K <= 1.6e9): 16-row slabs with one workgroup per row block and slab, the
+# ragged last slab included; 9 and 15 rows are single slabs of the same kernel.
+SLAB_CASES = [("q_proj", 9), ("q_proj", 15), ("q_proj", 48), ("q_proj", 101), ("k_proj", 33), ("k_proj", 203),
+              ("o_proj", 96), ("full_q_proj", 50), ("full_k_proj", 256), ("full_k_proj", 800)]
+
+
+@pytest.mark.parametrize("proj,m", SLAB_CASES)
+def test_forward_decode_slabs_past_32_rows(gpu_lib, proj, m):
+    """Sampled rows of every slab against the oracle, bf16 and fp32 outputs, with the
+    tighter accumulation bars of the decode path; the same rows through the GEMM
+    (pinned from 32 rows on) meet the same bars."""
+    import torch
+
+    shapes = {**PROJ, **FULL_ATTENTION}
+    n, k = shapes[proj]
+    seed = (20260630 + 1000 + sorted(PROJ).index(proj) if proj in PROJ
+            else 20260630 + 6000 + sorted(FULL_ATTENTION).index(proj))
+    triple = A.make_weights(n, k, seed=seed)
+    x = A.make_activations(m, k, seed=6300 + m, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*triple))
+    xd = dev_x(x)
+    y_bf = lin.forward(xd)
+    y_f = lin.forward(xd, out_dtype=torch.float32)
+    with gpu_lib.gemm_min_rows(32):
+        y_gemm = lin.forward(xd, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.linspace(0, m - 1, 24).astype(np.int64), [m - 1]]))
+    rt = torch.from_numpy(rows).cuda()
+    y_exact = C.qmm_f64(np.ascontiguousarray(x[rows]), *triple)
+    assert_close(y_bf[rt], y_exact, f"{proj} m={m} bf16")
+    assert_rounded(y_bf[rt], y_exact, f"{proj} m={m} bf16")
+    assert assert_close(y_f[rt], y_exact, f"{proj} m={m} f32") < ACC_REL
+    assert assert_close(y_gemm[rt], y_exact, f"{proj} m={m} f32 (GEMM)") < 5e-4
     lin.close()
 
 

@@ -46,11 +46,13 @@ def _compare(ref, got, x_bits, tri, rows, what, bits=4):
 
 
 @pytest.mark.parametrize("dtype_name", ["bfloat16", "float32"])
-def test_noalloc_matches_forward_on_consecutive_calls(gpu_lib, dtype_name):
+@pytest.mark.parametrize("gemm_min", [32, 0])  # the GEMM from 32 rows on; the automatic choice
+def test_noalloc_matches_forward_on_consecutive_calls(gpu_lib, dtype_name, gemm_min):
     import torch
 
     dtype = getattr(torch, dtype_name)
-    cases = [  # (N, K, M): each call followed by a smaller one on the same scratch
+    cases = [  # (N, K, M), paths as with the GEMM from 32 rows on: each call followed
+               # by a smaller one on the same scratch
         (2048, 3840, 512),    # GEMM, K split over workgroups: group sums + partial planes
         (40, 384, 40),        # small GEMM
         (3840, 15360, 2048),  # GEMM, the largest group-sum table of the configs
@@ -58,17 +60,18 @@ def test_noalloc_matches_forward_on_consecutive_calls(gpu_lib, dtype_name):
         (130, 1088, 300),     # GEMM with a ragged last octet
         (48, 576, 33),
     ]
-    for i, (n, k, m) in enumerate(cases):
-        tri = random_triple(n, k, seed=9100 + i)
-        x = A.make_activations(m, k, seed=9200 + i, outliers=True)
-        lin = gpu_lib.QuantizedLinear(*dev_triple(*tri))
-        ref, got = _both(lin, dev_x(x), dtype)
-        rows = np.unique(np.linspace(0, m - 1, min(m, 12)).astype(np.int64))
-        _compare(ref, got, x, tri, rows, f"n={n} k={k} m={m} {dtype_name}")
-        lin.close()
+    with gpu_lib.gemm_min_rows(gemm_min):
+        for i, (n, k, m) in enumerate(cases):
+            tri = random_triple(n, k, seed=9100 + i)
+            x = A.make_activations(m, k, seed=9200 + i, outliers=True)
+            lin = gpu_lib.QuantizedLinear(*dev_triple(*tri))
+            ref, got = _both(lin, dev_x(x), dtype)
+            rows = np.unique(np.linspace(0, m - 1, min(m, 12)).astype(np.int64))
+            _compare(ref, got, x, tri, rows, f"n={n} k={k} m={m} {dtype_name} gemm_min={gemm_min}")
+            lin.close()
 
 
-def test_noalloc_eight_bit_and_its_limit(gpu_lib):
+def test_noalloc_eight_bit_and_its_limit(gpu_lib, gemm_from_32):
     import torch
 
     # 8-bit: [x | x] in the static scratch, then the GEMM's workspace after it
@@ -97,7 +100,7 @@ def test_noalloc_eight_bit_and_its_limit(gpu_lib):
     lin.close()
 
 
-def test_noalloc_through_raw_c_abi(gpu_lib):
+def test_noalloc_through_raw_c_abi(gpu_lib, gemm_from_32):
     """The entry point called with raw pointers and the current stream, as a C caller
     would: status 0 and the forward's bits."""
     import torch

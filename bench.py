@@ -80,6 +80,11 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_decode_m1_traffic.json")
 DOM_KERNEL = "decode_rows_kernel"
 
 
+def weight_bytes(n: int, k: int) -> int:
+    """Resident bytes of one 4-bit projection: codes plus bf16 scale and bias per group."""
+    return n * k // 2 + 4 * n * (k // 64)
+
+
 def algo_bytes(m: int, n: int, k: int, y_bytes: int = 2) -> int:
     """Packed W + bf16 scales and biases + bf16 x + y."""
     return n * k // 2 + 4 * n * (k // 64) + 2 * m * k + y_bytes * m * n
@@ -453,11 +458,12 @@ def variants_run(torch, Q, host) -> dict:
 
 def summarize_trace(db_path: str, out_md: str, command: str) -> None:
     """Per-shape kernel durations of `bench.py --prefill-only` from a rocprofv3
-    --kernel-trace database (rocpd SQLite).  Each shape's handle is created (one
-    repack launch) before its forwards, which split the trace into the sweep's shapes
-    in order; every forward launches xaug_kernel, the GEMM and (when K is split) the
-    split-K reduction.  Reported: the median duration of each kernel and of the whole
-    forward (first launch start to last launch end) over the shape's graph replays."""
+    --kernel-trace database (rocpd SQLite).  Each shape's handles are created (repack
+    launches) before its forwards, which split the trace into the sweep's shapes in
+    order; a GEMM-path forward launches xaug_kernel, the GEMM and (when K is split) the
+    split-K reduction, a decode-path forward one decode kernel.  Reported: the median
+    duration of each kernel and of the whole forward (first launch start to last
+    launch end) over the shape's forwards."""
     import re
     import sqlite3
 
@@ -476,15 +482,16 @@ def summarize_trace(db_path: str, out_md: str, command: str) -> None:
         if s.startswith("repack"):
             if not shapes or shapes[-1]:
                 shapes.append([])
-        elif s.startswith("xaug") and shapes:
+        elif (s.startswith("xaug") or s.startswith("decode")) and shapes:
             shapes[-1].append([r])
         elif shapes and shapes[-1]:
             shapes[-1][-1].append(r)
     names = prefill_sweep_names()
     md = ["# Prefill GEMM sweep: kernel durations per forward", "", "Command (from the repository root):", "",
           "```", command, "```", "",
-          "Per shape: the launches of one forward (kernel: workgroups x K splits) and their median durations over "
-          "the shape's graph replays; the forward's span runs from its first launch's start to its last launch's "
+          "Per shape: the launches of one forward (kernel: workgroups x K splits, or x 16-row slabs for the decode "
+          "kernels) and their median durations over the shape's forwards (back-to-back forwards over rotated weight "
+          "copies in a replayed graph); the forward's span runs from its first launch's start to its last launch's "
           "end.", "",
           "| shape | launches | forwards | median us per kernel | forward span us |", "|---|---|---:|---|---:|"]
     for name, fwds in zip(names, shapes):
@@ -689,8 +696,11 @@ FULL_ATTENTION = [("full_q_proj", 8192, 3840), ("full_k_proj", 512, 3840), ("ful
 
 def prefill_sweep(torch, Q, host, ms, shapes, pair: bool, full_attention: bool) -> dict:
     """Prefill GEMM lines: each projection of `shapes` (and, optionally, the gate|up
-    GeGLU pair and the full-attention shapes) at every M of ms, graph-replayed after a
-    wall-time settle; activations N(0, 1) with 1% outliers x20."""
+    GeGLU pair and the full-attention shapes) at every M of ms; activations N(0, 1)
+    with 1% outliers x20.  Timed as the decode lines are (kernel_us): back-to-back
+    forwards over rotated weight copies in one graph, replayed after a wall-time
+    settle, so a line is one forward's launches and the gaps between them, not the
+    launch of a one-forward graph (~7-10 us per replay)."""
     out = {}
     extra = {}
     if full_attention:
@@ -701,24 +711,18 @@ def prefill_sweep(torch, Q, host, ms, shapes, pair: bool, full_attention: bool) 
         xk = {k: torch.from_numpy(synthetic_activations(m, k, seed=SEED_BASE + 2 + k, outliers=True).view(np.int16))
               .view(torch.bfloat16).cuda() for k in {k for _, _, k in all_shapes}}
         for name, n, k in all_shapes:
-            ym = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-            lin = Q.QuantizedLinear(*(host[name] if name in host else extra[name]))
-            ms_ = graph_ms_steady(torch, lambda: lin.forward(xk[k], out=ym))
-            lin.close()
-            tflops = algo_flops(m, n, k) / (ms_ * 1e-3) / 1e12
-            out[f"{name}_m{m}"] = {"us": round(ms_ * 1e3, 1), "TFLOPS": round(tflops, 1),
+            tri = host[name] if name in host else extra[name]
+            us = kernel_us(torch, lambda: Q.QuantizedLinear(*tri), m, k, n, xk[k], weight_bytes(n, k))
+            tflops = algo_flops(m, n, k) / (us * 1e-6) / 1e12
+            out[f"{name}_m{m}"] = {"us": round(us, 1), "TFLOPS": round(tflops, 1),
                                    "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
-            del ym
         if pair:  # the GeGLU pair: gate and up in one GEMM, h = geglu(gate, up)
             f, k = 15360, HIDDEN
-            hm = torch.empty((m, f), dtype=torch.bfloat16, device="cuda")
-            pr = Q.QuantizedGeGLU(host["gate_proj"], host["up_proj"])
-            ms_ = graph_ms_steady(torch, lambda: pr.forward(xk[k], out=hm))
-            pr.close()
-            tflops = algo_flops(m, 2 * f, k) / (ms_ * 1e-3) / 1e12
-            out[f"{PAIR}_m{m}"] = {"us": round(ms_ * 1e3, 1), "TFLOPS": round(tflops, 1),
+            us = kernel_us(torch, lambda: Q.QuantizedGeGLU(host["gate_proj"], host["up_proj"]), m, k, f, xk[k],
+                           2 * weight_bytes(f, k))
+            tflops = algo_flops(m, 2 * f, k) / (us * 1e-6) / 1e12
+            out[f"{PAIR}_m{m}"] = {"us": round(us, 1), "TFLOPS": round(tflops, 1),
                                    "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
-            del hm
         del xk
     return out
 

@@ -103,11 +103,11 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
 hipError_t launch_gelu_table(uint16_t* table, hipStream_t stream);
 
 // LoRA delta added in place to a projection output y [m, n] (bf16 or fp32) already
-// holding the base product: part is fp32 scratch of lora_slices(k) x m x rank floats
+// holding the base product: part is fp32 scratch of lora_slices(k, m) x m x rank floats
 // (x . A^T summed over slices of K), a [rank, k] and b [n, rank] fp32 on the device
 // (q4_lora.hip).
 constexpr int kLoraSlices = 8;
-int lora_slices(int k);
+int lora_slices(int k, int m);
 hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float* part, void* y, int m, int n, int k,
                        int rank, float scale, bool out_f32, hipStream_t stream);
 

@@ -8,15 +8,19 @@
 // In bf16 the scale is bf16 (model_scalar) and delta is rounded to bf16 before the
 // bf16 add, as the reference's array ops round.
 //
-// lora_down: K is cut into kSlices slices; a 256-thread workgroup per (4 rows of x,
-// 16 ranks, slice) has wave w take ranks 4w..4w+3 and lane l an 8-column chunk of the
-// slice per step (one 16-byte x load per row, two 16-byte A loads per rank, all in
-// flight together), then each wave sums its 4 x 4 partials by shuffles and writes
-// them to part[slice][m][r].  No atomics: lora_up adds the slices in a fixed order.
-// lora_up: a 256-thread workgroup per (256 columns, 16 or 64 rows); t[m, r] (the
-// slices summed in order) and the workgroup's rows of B are staged in LDS 16 ranks at
-// a time (B with coalesced loads), each thread takes its column's B values into
-// registers and updates its rows of y.  B is read once per 16 or 64 rows, y once.
+// lora_down: K is cut into lora_slices(k, m) slices (up to 8; fewer when the rows
+// alone give enough workgroups); a 256-thread workgroup per (4 rows of x, 16 ranks,
+// slice) has wave w take ranks 4w..4w+3 and lane l an 8-column chunk of the slice per
+// step (one 16-byte x load per row, two 16-byte A loads per rank, all in flight
+// together), then each wave sums its 4 x 4 partials by shuffles and writes them to
+// part[slice][m][r].  No atomics: lora_up adds the slices in a fixed order.
+// lora_up: a 256-thread workgroup per (256 columns, 16 or 32 rows); t[m, r] (the
+// slices summed in order, all of them requested at once) and the workgroup's rows of
+// B are staged in LDS 16 ranks at a time (B with coalesced loads), and each thread
+// takes its column's B values into registers and forms its rows' deltas.  With 32
+// rows (M > 16) the deltas go through LDS and y is read and written in 16-byte pieces
+// by consecutive threads (when N and y allow it); with 16 each thread updates its own
+// column.  B is read once per 16 or 32 rows, y once.
 #include "q4_common.h"
 #include "q4_kernels.h"
 
@@ -90,33 +94,76 @@ __global__ __launch_bounds__(256) void lora_up_kernel(const float* __restrict__ 
                                                       void* __restrict__ y, int m_rows, int n_rows, int rank,
                                                       int slices, float scale) {
 #pragma clang fp contract(off)
+    constexpr bool kStaged = ROWS > kUpRows;   // large M: y updated in 16-byte pieces
+    constexpr int kPer = F32 ? 4 : 8;           // outputs per 16 bytes
+    constexpr int kChunks = 256 / kPer;         // 16-byte pieces per tile row
+    constexpr int kPieces = kStaged ? ROWS * kChunks / 256 : 1;  // y pieces per thread
+    constexpr int kEntries = ROWS * kRankBlock / 256;          // t entries staged per thread
+    static_assert(ROWS * kRankBlock % 256 == 0 && ROWS * kChunks % 256 == 0, "whole pieces per thread");
     const int n0 = (int)blockIdx.x * 256;
     const int n = n0 + (int)threadIdx.x;
     const int m0 = (int)blockIdx.y * ROWS;
     const int rows = m_rows - m0 < ROWS ? m_rows - m0 : ROWS;
+    const bool vec = kStaged && n_rows % kPer == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
     __shared__ float ts[ROWS][kRankBlock];
     __shared__ float bs[256][kRankBlock + 1];  // +1: thread n reads row n without bank conflicts
+    __shared__ float dt[kStaged ? ROWS : 1][kStaged ? 256 + 4 : 1];  // the tile's deltas
     float d[ROWS];
 #pragma unroll
     for (int i = 0; i < ROWS; ++i) d[i] = 0.f;
+    // small M: y's current values, requested after the first rank block's operands
+    // (loads return in order) so that they arrive while the deltas are formed; large
+    // M reads them after the deltas (holding them across the math costs occupancy)
+    float base[ROWS];
     for (int r0 = 0; r0 < rank; r0 += kRankBlock) {
         const int rb = rank - r0 < kRankBlock ? rank - r0 : kRankBlock;
-        __syncthreads();  // the previous block's values have been read
-        for (int e = (int)threadIdx.x; e < ROWS * kRankBlock; e += 256) {
+        // this block's operands into registers: t (every slice of each entry at once)
+        // and the workgroup's 256 rows of B (consecutive threads read consecutive ranks
+        // of a row: contiguous when rank == 16)
+        float pv[kEntries][kLoraSlices];
+#pragma unroll
+        for (int u = 0; u < kEntries; ++u) {
+            const int e = u * 256 + (int)threadIdx.x;
             const int i = e / kRankBlock, r = e % kRankBlock;
-            float v = 0.f;
-            if (i < rows && r < rb)
-                for (int sl = 0; sl < slices; ++sl) v += part[((long)sl * m_rows + m0 + i) * rank + r0 + r];
-            ts[i][r] = v;
+            const bool live = i < rows && r < rb;
+#pragma unroll
+            for (int sl = 0; sl < kLoraSlices; ++sl)
+                pv[u][sl] = live && sl < slices ? part[((long)sl * m_rows + m0 + i) * rank + r0 + r] : 0.f;
         }
-        // the workgroup's 256 rows of B, ranks r0 .. r0 + rb: consecutive threads read
-        // consecutive ranks of a row (contiguous when rank == 16)
+        float bl[kRankBlock];
 #pragma unroll
         for (int j = 0; j < kRankBlock; ++j) {
             const int e = j * 256 + (int)threadIdx.x;
             const int row = e / kRankBlock, r = e % kRankBlock;
             const int nn = n0 + row < n_rows ? n0 + row : n_rows - 1;  // rows of B past N: never used
-            bs[row][r] = r < rb ? b[(long)nn * rank + r0 + r] : 0.f;
+            bl[j] = r < rb ? b[(long)nn * rank + r0 + r] : 0.f;
+        }
+        if (r0 == 0) {
+            if constexpr (!kStaged) {
+#pragma unroll
+                for (int i = 0; i < ROWS; ++i) {
+                    const long o = (long)(m0 + i) * n_rows + n;
+                    base[i] = i < rows && n < n_rows
+                                  ? (F32 ? static_cast<const float*>(y)[o]
+                                         : __uint_as_float((uint32_t)static_cast<const uint16_t*>(y)[o] << 16))
+                                  : 0.f;
+                }
+            }
+        }
+        __syncthreads();  // the previous block's values have been read
+#pragma unroll
+        for (int u = 0; u < kEntries; ++u) {
+            const int e = u * 256 + (int)threadIdx.x;
+            float v = pv[u][0];  // summed in slice order
+#pragma unroll
+            for (int sl = 1; sl < kLoraSlices; ++sl)
+                if (sl < slices) v += pv[u][sl];
+            ts[e / kRankBlock][e % kRankBlock] = v;
+        }
+#pragma unroll
+        for (int j = 0; j < kRankBlock; ++j) {
+            const int e = j * 256 + (int)threadIdx.x;
+            bs[e / kRankBlock][e % kRankBlock] = bl[j];
         }
         __syncthreads();
         float bv[kRankBlock];
@@ -127,15 +174,64 @@ __global__ __launch_bounds__(256) void lora_up_kernel(const float* __restrict__ 
 #pragma unroll
             for (int r = 0; r < kRankBlock; ++r) d[i] = __builtin_fmaf(ts[i][r], bv[r], d[i]);
     }
-    if (n >= n_rows) return;
-    // every row's base value first (independent loads, one round trip), then the stores
-    float base[ROWS];
+    if constexpr (kStaged) {
+        if (vec) {
 #pragma unroll
-    for (int i = 0; i < ROWS; ++i) {
-        const long o = (long)(m0 + i) * n_rows + n;
-        if (i < rows)
-            base[i] = F32 ? static_cast<const float*>(y)[o]
-                          : __uint_as_float((uint32_t)static_cast<const uint16_t*>(y)[o] << 16);
+            for (int i = 0; i < ROWS; ++i) dt[i][threadIdx.x] = d[i];
+            // consecutive threads take consecutive 16-byte pieces of a row; a piece lies
+            // wholly inside or outside the row (N is a multiple of the piece); all of a
+            // thread's pieces are requested before the first store
+            uint4 ypre[kPieces];
+#pragma unroll
+            for (int u = 0; u < kPieces; ++u) {
+                const int q = u * 256 + (int)threadIdx.x;
+                const int i = q / kChunks, nn = n0 + (q % kChunks) * kPer;
+                ypre[u] = i < rows && nn < n_rows
+                              ? *reinterpret_cast<const uint4*>(static_cast<const char*>(y) +
+                                                                ((long)(m0 + i) * n_rows + nn) * (F32 ? 4 : 2))
+                              : make_uint4(0, 0, 0, 0);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < kPieces; ++u) {
+                const int q = u * 256 + (int)threadIdx.x;
+                const int i = q / kChunks, j = q % kChunks;
+                const int nn = n0 + j * kPer;
+                if (i >= rows || nn >= n_rows) continue;
+                const long o = (long)(m0 + i) * n_rows + nn;
+                const float* dv = &dt[i][j * kPer];
+                if constexpr (F32) {
+                    float4 v = __builtin_bit_cast(float4, ypre[u]);
+                    v.x = v.x + dv[0] * scale;
+                    v.y = v.y + dv[1] * scale;
+                    v.z = v.z + dv[2] * scale;
+                    v.w = v.w + dv[3] * scale;
+                    *reinterpret_cast<float4*>(static_cast<float*>(y) + o) = v;
+                } else {
+                    const uint32_t w[4] = {ypre[u].x, ypre[u].y, ypre[u].z, ypre[u].w};
+                    const float sc = round_bf16(scale);
+                    uint32_t out[4];
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) {
+                        const uint32_t lo = f32_to_bf16(bf16_lo(w[h]) + round_bf16(dv[2 * h] * sc));
+                        const uint32_t hi = f32_to_bf16(bf16_hi(w[h]) + round_bf16(dv[2 * h + 1] * sc));
+                        out[h] = lo | (hi << 16);
+                    }
+                    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(y) + o) = make_uint4(out[0], out[1], out[2], out[3]);
+                }
+            }
+            return;
+        }
+    }
+    if (n >= n_rows) return;
+    if constexpr (kStaged) {  // N or y not 16-byte friendly: every row's value now, then the stores
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i) {
+            const long o = (long)(m0 + i) * n_rows + n;
+            base[i] = i < rows ? (F32 ? static_cast<const float*>(y)[o]
+                                      : __uint_as_float((uint32_t)static_cast<const uint16_t*>(y)[o] << 16))
+                               : 0.f;
+        }
     }
 #pragma unroll
     for (int i = 0; i < ROWS; ++i) {
@@ -151,15 +247,20 @@ __global__ __launch_bounds__(256) void lora_up_kernel(const float* __restrict__ 
 
 }  // namespace
 
-int lora_slices(int k) {
+int lora_slices(int k, int m) {
     const int chunks = k / 8;
-    return chunks >= kLoraSlices * 64 ? kLoraSlices : (chunks + 63) / 64;
+    int s = chunks >= kLoraSlices * 64 ? kLoraSlices : (chunks + 63) / 64;
+    // the rows alone give enough workgroups: fewer slices (fewer shuffle reductions and
+    // partial planes; M = 2048 at K = 3840 runs 2 slices of 1024 workgroups)
+    const int wgs = (m + kDownRows - 1) / kDownRows;
+    while (s > 1 && wgs * (s / 2) >= 1024) s /= 2;
+    return s;
 }
 
 hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float* part, void* y, int m, int n, int k,
                        int rank, float scale, bool out_f32, hipStream_t stream) {
     static_assert(kWaveRanks * 4 == kRankBlock, "four waves per lora_down workgroup");
-    const int slices = lora_slices(k);
+    const int slices = lora_slices(k, m);
     const int slice_chunks = (k / 8 + slices - 1) / slices;
     const dim3 dgrid((unsigned)((m + kDownRows - 1) / kDownRows), (unsigned)((rank + kRankBlock - 1) / kRankBlock),
                      (unsigned)slices);

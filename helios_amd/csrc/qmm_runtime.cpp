@@ -763,7 +763,7 @@ Gemma4Status gemma4_qlinear_forward_lora(const Gemma4QLinear* linear, const Gemm
         hipMemPool_t pool = nullptr;
         e = scratch_pool(linear->device, &pool);
         void* t = nullptr;
-        const size_t t_bytes = (size_t)q4::lora_slices((int)linear->desc.in_features) * rows * lora->rank * 4;
+        const size_t t_bytes = (size_t)q4::lora_slices((int)linear->desc.in_features, (int)rows) * rows * lora->rank * 4;
         if (e == hipSuccess) e = hipMallocFromPoolAsync(&t, t_bytes, pool, sh);
         if (e != hipSuccess)
             return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));

@@ -76,6 +76,15 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// The same with a wave-uniform part of the offset in the instruction's scalar offset
+// (soff: an SGPR, no VGPR spent on it).  In-range lanes keep off + soff inside the
+// buffer; lanes at kOutOfRange read zero.
+template <int AUX = 0>
+__device__ __forceinline__ uint4 buffer_load16s(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, AUX);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 template <int AUX = 0>
 __device__ __forceinline__ uint2 buffer_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, AUX);
@@ -141,6 +150,17 @@ struct OutParams {
     int nb;                    // greedy modes: row blocks (the stride of part)
     float cap;                 // greedy modes: the softcap (0: none)
 };
+
+// Byte offset in x of 16-byte unit c of x' (rows of k elements), for x rows of kx
+// elements: kx = k, or k / 2 for a two-plane 8-bit handle, whose x' = [x | x] repeats
+// each row (column c of x' is column c mod kx of x).
+__device__ __forceinline__ uint32_t xprime_offset(int c, int k, int kx) {
+    if (kx == k) return (uint32_t)c * 16u;
+    const int rowc = k >> 3, rowcx = kx >> 3;
+    const int row = c / rowc;
+    const int cr = c - row * rowc;
+    return (uint32_t)(row * rowcx + (cr >= rowcx ? cr - rowcx : cr)) * 16u;
+}
 
 // Output parameters of the 16-row slab `slab` of a launch: y (or h, or the logits)
 // and the greedy keys advance by 16 rows.  Decode kernels launched over M > 16 rows

@@ -39,13 +39,13 @@ namespace {
 template <int MT, int GPW, bool XLDS>
 __global__ __launch_bounds__(1024) void decode_kernel(
     const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x_in,
-    OutParams op_in, int m_total, int n_rows, int k, int gpairs, int waves) {
+    OutParams op_in, int m_total, int n_rows, int k, int kx, int gpairs, int waves) {
     constexpr int R = MT < 4 ? MT : 4;
     extern __shared__ uint4 xs_lds[];  // XLDS: x[M][K] as bf16, 16 B per entry
     // this workgroup's 16-row slab (blockIdx.y) of the launch's m_total rows
     const int slab = (int)blockIdx.y;
     const int m_rows = m_total - 16 * slab < 16 ? m_total - 16 * slab : 16;
-    const uint16_t* __restrict__ x = x_in + (size_t)slab * 16 * k;
+    const uint16_t* __restrict__ x = x_in + (size_t)slab * 16 * kx;
     const OutParams op = slab_params(op_in, slab, n_rows);
     const int rb = blockIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -54,9 +54,10 @@ __global__ __launch_bounds__(1024) void decode_kernel(
     const int kq = lane >> 4;
     const int gp0 = (wave * gpairs) / waves;
     const int cnt = ((wave + 1) * gpairs) / waves - gp0;
-    const uint32_t xbytes = (uint32_t)m_rows * (uint32_t)k * 2u;
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, xbytes);
+    const uint32_t xbytes = (uint32_t)m_rows * (uint32_t)k * 2u;  // of x' (rows of k)
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)kx * 2u);
     const int arow = col < m_rows ? col : m_rows - 1;  // any valid row for A rows >= M
+    const uint32_t lane_x = (uint32_t)(arow * kx + 8 * kq) * 2u;  // XLDS = false: this lane's x bytes
 
     if constexpr (XLDS) {
         // cooperative copy x -> LDS; these loads are issued first so that waiting for
@@ -68,7 +69,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = c0 + u * nthr + (int)threadIdx.x;
-                tmp[u] = buffer_load16(xrs, c < chunks ? (uint32_t)c * 16u : kOutOfRange);
+                tmp[u] = buffer_load16(xrs, c < chunks ? xprime_offset(c, k, kx) : kOutOfRange);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(
         const long first = (long)rb * gpairs + gpb;
         const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * 64, (uint32_t)left * 1024u);
         const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * 16, (uint32_t)left * 128u);
-        // element offset of this lane's x operand at pair i, group 0, half 0
+        // element offset of this lane's x operand at pair i, group 0, half 0 (x in LDS)
         const int xel = arow * k + 8 * kq + gpb * 128;
         const int kleft = k - gpb * 128;
 
@@ -118,7 +119,11 @@ __global__ __launch_bounds__(1024) void decode_kernel(
                 if constexpr (XLDS) {
                     dst[q] = ok ? xs_lds[(xel + kb) >> 3] : make_uint4(0, 0, 0, 0);
                 } else {
-                    dst[q] = buffer_load16(xrs, ok ? (uint32_t)(xel + kb) * 2u : kOutOfRange);
+                    // a per-lane offset plus the operand's wave-uniform column (in the
+                    // scalar offset): column cu of x' is column cu mod kx of x
+                    const int cu = gpb * 128 + kb;
+                    const int cm = cu >= kx ? cu - kx : cu;
+                    dst[q] = buffer_load16s(xrs, ok ? lane_x : kOutOfRange, (uint32_t)cm * 2u);
                 }
             }
         };
@@ -192,14 +197,14 @@ __device__ __forceinline__ uint32_t scale_word(uint2 sv, int pair, int gi, int c
 template <int MT, int GPW, int NBUF>
 __global__ __launch_bounds__(512) void decode_stream_kernel(
     const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x_in,
-    OutParams op_in, int m_total, int n_rows, int k, int gpairs, int nblocks, int waves) {
+    OutParams op_in, int m_total, int n_rows, int k, int kx, int gpairs, int nblocks, int waves) {
     constexpr int R = MT < 4 ? MT : 4;
     constexpr int kPad = GPW * 128;  // zero columns after each x row
     extern __shared__ uint4 lds[];
     // this workgroup's 16-row slab (blockIdx.y) of the launch's m_total rows
     const int slab = (int)blockIdx.y;
     const int m_rows = m_total - 16 * slab < 16 ? m_total - 16 * slab : 16;
-    const uint16_t* __restrict__ x = x_in + (size_t)slab * 16 * k;
+    const uint16_t* __restrict__ x = x_in + (size_t)slab * 16 * kx;
     const OutParams op = slab_params(op_in, slab, n_rows);
     // layout: x rows [m_rows][k + kPad + 8] bf16, then -X table [2*(gpairs+GPW)][16] fp32
     __shared__ float red[2][8][R * 64];
@@ -248,13 +253,13 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
         const int xchunks = (m_rows * k) >> 3;
         const int rowc = k >> 3;
         const int nthr = waves * 64;
-        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)k * 2u);
+        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)kx * 2u);
         uint4 tmp[4];
         auto load_x = [&](int c0) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = c0 + u * nthr + (int)threadIdx.x;
-                tmp[u] = buffer_load16(xrs, c < xchunks ? (uint32_t)c * 16u : kOutOfRange);
+                tmp[u] = buffer_load16(xrs, c < xchunks ? xprime_offset(c, k, kx) : kOutOfRange);
             }
         };
         auto store_x = [&](int c0) {
@@ -372,7 +377,7 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
 template <int MT, int GPW, int NBUF>
 __global__ __launch_bounds__(256) void decode_rows_kernel(
     const uint4* __restrict__ tiles, const uint2* __restrict__ sb, const uint16_t* __restrict__ x,
-    OutParams op, int m_rows, int n_rows, int k, int gpairs, int nblocks) {
+    OutParams op, int m_rows, int n_rows, int k, int kx, int gpairs, int nblocks) {
     static_assert(GPW == 4, "one 8-byte load per lane covers a chunk's scale words");
     constexpr int R = MT < 4 ? MT : 4;
     constexpr int kPad = GPW * 128;  // zero columns after each x row
@@ -418,13 +423,13 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(
         const int xchunks = (m_rows * k) >> 3;
         const int rowc = k >> 3;
         const int nthr = waves * 64;
-        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)k * 2u);
+        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)kx * 2u);
         uint4 tmp[4];
         auto load_x = [&](int c0) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = c0 + u * nthr + (int)threadIdx.x;
-                tmp[u] = buffer_load16(xrs, c < xchunks ? (uint32_t)c * 16u : kOutOfRange);
+                tmp[u] = buffer_load16(xrs, c < xchunks ? xprime_offset(c, k, kx) : kOutOfRange);
             }
         };
         // each thread sums its eight values; eight consecutive lanes hold one group
@@ -583,7 +588,7 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
             const int cap = device_cus() * kRowsPerCu;
             if (grid > cap) grid = cap;
             hipLaunchKernelGGL((decode_rows_kernel<MT, GPW, 2>), dim3(grid), dim3(64 * kRowsWaves), lds_bytes, stream,
-                               tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb);
+                               tiles, sb, x, op, m, l.n, l.k, l.kx, l.gp, l.nb);
             return hipGetLastError();
         }
     }
@@ -591,7 +596,7 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
     if (l.gp <= kXLdsMaxPairs && x_bytes <= kXLdsMaxBytes && l.nb <= kXLdsMaxBlocks * (MT > 1 ? 2 : 1)) {
         const int waves = (l.gp + GPW - 1) / GPW;  // <= 8, each wave one pass of <= 4 pairs
         hipLaunchKernelGGL((decode_kernel<MT, GPW, true>), dim3(l.nb, slabs), dim3(64 * waves), x_bytes, stream, tiles,
-                           sb, x, op, m, l.n, l.k, l.gp, waves);
+                           sb, x, op, m, l.n, l.k, l.kx, l.gp, waves);
         return hipGetLastError();
     }
     const size_t stream_lds = lds_bytes + (size_t)ms * 16;  // x rows one 16-byte unit longer
@@ -623,20 +628,20 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
         // pair at M = 2-16 were 5-15% slower: the deeper prefetch delays x staging).
         if (per_cu == 1 && per_wg >= 16)
             hipLaunchKernelGGL((decode_stream_kernel<MT, GPW, 4>), dim3(grid, slabs), dim3(64 * waves), stream_lds,
-                               stream, tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb, waves);
+                               stream, tiles, sb, x, op, m, l.n, l.k, l.kx, l.gp, l.nb, waves);
         else
             hipLaunchKernelGGL((decode_stream_kernel<MT, GPW, 2>), dim3(grid, slabs), dim3(64 * waves), stream_lds,
-                               stream, tiles, sb, x, op, m, l.n, l.k, l.gp, l.nb, waves);
+                               stream, tiles, sb, x, op, m, l.n, l.k, l.kx, l.gp, l.nb, waves);
         return hipGetLastError();
     }
     const Split sp = choose_split(l.gp, MT);
     const dim3 grid(l.nb, slabs), block(64 * sp.waves);
     if (sp.gpw == 8)
-        hipLaunchKernelGGL((decode_kernel<MT, 8, false>), grid, block, 0, stream, tiles, sb, x, op, m, l.n, l.k, l.gp, sp.waves);
+        hipLaunchKernelGGL((decode_kernel<MT, 8, false>), grid, block, 0, stream, tiles, sb, x, op, m, l.n, l.k, l.kx, l.gp, sp.waves);
     else if (sp.gpw == 6)
-        hipLaunchKernelGGL((decode_kernel<MT, 6, false>), grid, block, 0, stream, tiles, sb, x, op, m, l.n, l.k, l.gp, sp.waves);
+        hipLaunchKernelGGL((decode_kernel<MT, 6, false>), grid, block, 0, stream, tiles, sb, x, op, m, l.n, l.k, l.kx, l.gp, sp.waves);
     else
-        hipLaunchKernelGGL((decode_kernel<MT, 4, false>), grid, block, 0, stream, tiles, sb, x, op, m, l.n, l.k, l.gp, sp.waves);
+        hipLaunchKernelGGL((decode_kernel<MT, 4, false>), grid, block, 0, stream, tiles, sb, x, op, m, l.n, l.k, l.kx, l.gp, sp.waves);
     return hipGetLastError();
 }
 

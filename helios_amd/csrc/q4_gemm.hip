@@ -41,7 +41,10 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // (row, group) from its 128 contiguous bytes, two rounds cover the 16 x 8 pairs, the
 // sums meet in LDS and one wave packs the block.
 __global__ __launch_bounds__(512) void xaug_kernel(const uint16_t* __restrict__ x, uint4* __restrict__ xaug,
-                                                   int m_rows, int k, int groups, int octets) {
+                                                   int m_rows, int kx, int groups, int octets) {
+    // x rows are kx long; group g >= kx / 64 (the low plane of a two-plane handle) is
+    // group g - kx / 64 of x
+    const int gx = kx >> 6;
     __shared__ float gsum[8][16];  // [group within the octet][row within the block]
     const int unit = (int)blockIdx.x;  // 16-row block * octets + octet
     const int o = unit % octets;
@@ -54,8 +57,9 @@ __global__ __launch_bounds__(512) void xaug_kernel(const uint16_t* __restrict__ 
         const int p = (t >> 3) + 64 * r;
         const long m = mb * 16 + (p & 15);
         const int g = 8 * o + (p >> 4);
-        v[r] = (m < m_rows && g < groups) ? *reinterpret_cast<const uint4*>(x + m * k + 64 * g + 8 * c)
-                                          : make_uint4(0, 0, 0, 0);
+        v[r] = (m < m_rows && g < groups)
+                   ? *reinterpret_cast<const uint4*>(x + m * kx + 64 * (g >= gx ? g - gx : g) + 8 * c)
+                   : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -123,7 +127,7 @@ __device__ __forceinline__ void tile_of(int id, int nwg, int mtiles, int ntiles,
 template <int OUT, int BM, int BN>
 __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ tiles, const uint2* __restrict__ sb,
                                                    const uint16_t* __restrict__ x, const uint4* __restrict__ xaug,
-                                                   void* __restrict__ y, int m_rows, int n_rows, int k, int groups,
+                                                   void* __restrict__ y, int m_rows, int n_rows, int kx, int groups,
                                                    int gpairs, int mtiles, int ntiles, int octets, uint32_t tile_bytes,
                                                    uint32_t sb_bytes, int g_split, long split_stride, int n_out,
                                                    const uint16_t* __restrict__ gelu_table) {
@@ -172,7 +176,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
 
     // sized to the buffers (<= 2^31 bytes, checked by the host) so that kOutOfRange is
     // outside every range and reads as zero
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)k * 2u);
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)kx * 2u);
     const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles, tile_bytes);
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, sb_bytes);
     const __amdgpu_buffer_rsrc_t ars = make_rsrc(xaug, (uint32_t)(mtiles * (BM / 16) * octets) * 1024u);
@@ -193,7 +197,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         const int r = q >> 3;
         const int c = (q & 7) ^ ((r >> 1) & 7);
         const int row = mt * BM + r;
-        xv[u] = row < m_rows ? ((uint32_t)row * (uint32_t)k + (uint32_t)(8 * c)) * 2u : kOutOfRange;
+        xv[u] = row < m_rows ? ((uint32_t)row * (uint32_t)kx + (uint32_t)(8 * c)) * 2u : kOutOfRange;
     }
     uint32_t wv[2];  // tiled words of a pair, part t: row block 2w + t, one 16-byte word per lane
 #pragma unroll
@@ -206,8 +210,12 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         const int rb = rbw + 8 * wave + (lane >> 3);
         sv = rb < nblocks ? (uint32_t)rb * (uint32_t)gpairs * 128u + (uint32_t)(lane & 7) * 16u : kOutOfRange;
     }
+    // x rows are kx long: group g >= kx / 64 (the low plane of a two-plane handle) reads
+    // group g - kx / 64 of x (a scalar select)
+    const int gx = kx >> 6;
     auto dma_x = [&](int g, int part, uint4* xdst) {
-        dma16(g < g_end ? xrs : zrs, xdst + (kWaves * part + wave) * 64, xv[part], (uint32_t)g * 128u);
+        dma16(g < g_end ? xrs : zrs, xdst + (kWaves * part + wave) * 64, xv[part],
+              (uint32_t)(g >= gx ? g - gx : g) * 128u);
     };
     auto dma_w = [&](int p, int part, uint4* wdst) {
         dma16(p < p_end ? trs : zrs, wdst + (2 * wave + part) * 64, wv[part], (uint32_t)p * 1024u);
@@ -631,11 +639,11 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     uint4* xaug = static_cast<uint4*>(workspace);
     float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.xaug_bytes);
     if (l.tile_bytes() > kMaxBufferBytes || l.sb_bytes() > kMaxBufferBytes ||
-        (size_t)m * l.k * 2 > kMaxBufferBytes || plan.xaug_bytes > kMaxBufferBytes)
+        (size_t)m * l.kx * 2 > kMaxBufferBytes || plan.xaug_bytes > kMaxBufferBytes)
         return hipErrorInvalidValue;
     {
         const long units = (long)mtiles * (plan.bm / 16) * octets;  // 1 KiB blocks
-        hipLaunchKernelGGL(xaug_kernel, dim3((unsigned)units), dim3(512), 0, stream, x, xaug, m, l.k, l.g, octets);
+        hipLaunchKernelGGL(xaug_kernel, dim3((unsigned)units), dim3(512), 0, stream, x, xaug, m, l.kx, l.g, octets);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -647,11 +655,11 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     do {                                                                                                         \
         if (plan.bm == 256)                                                                                      \
             hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,  \
-                               l.n, l.k, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, STRIDE, n_out,  \
+                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, STRIDE, n_out,  \
                                gelu_table);                                                                      \
         else                                                                                                     \
             hipLaunchKernelGGL((gemm_kernel<MODE, 128, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,  \
-                               l.n, l.k, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, STRIDE, n_out,  \
+                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, STRIDE, n_out,  \
                                gelu_table);                                                                      \
     } while (0)
     if (plan.splits > 1) {

@@ -9,7 +9,9 @@ namespace q4 {
 
 struct Layout {
     int n = 0;   // output features
-    int k = 0;   // input features
+    int k = 0;   // input features of the tiled weight (2K for two-plane 8-bit handles)
+    int kx = 0;  // row length of x: k, or K = k / 2 for two-plane handles, whose kernels
+                 // read column c of x' = [x | x] as column c mod K of x
     int g = 0;   // groups per row (k / 64)
     int nb = 0;  // 16-row blocks
     int gp = 0;  // group pairs (ceil(g / 2))
@@ -21,6 +23,7 @@ inline Layout make_layout(int n, int k) {
     Layout l;
     l.n = n;
     l.k = k;
+    l.kx = k;
     l.g = k / 64;
     l.nb = (n + 15) / 16;
     l.gp = (l.g + 1) / 2;
@@ -42,8 +45,8 @@ hipError_t launch_dequantize(const uint4* tiles, const uint2* sb, float* out, co
                              hipStream_t stream);
 
 // 8-bit affine weights as two 4-bit planes over K' = 2K (q4_layout.hip): the layout l
-// of such a handle is make_layout(N, 2K) (pair_layout(F, 2K) for a pair); its kernels
-// take x' = [x | x] from launch_duplicate_x (x 16-byte aligned, K a multiple of 64).
+// of such a handle is make_layout(N, 2K) (pair_layout(F, 2K) for a pair) with kx = K;
+// its kernels read x [M, K] as x' = [x | x] (column c of x' is column c mod K of x).
 hipError_t launch_repack8(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint32_t* w_up,
                           const uint16_t* s_up, const uint16_t* b_up, uint4* tiles, uint2* sb, const Layout& l,
                           int pair_rows, hipStream_t stream);
@@ -51,7 +54,6 @@ hipError_t launch_dequantize8(const uint4* tiles, const uint2* sb, float* out, c
                               hipStream_t stream);
 hipError_t launch_embed8(const uint4* tiles, const uint2* sb, const int32_t* ids, int count, void* out, bool out_f32,
                          const Layout& l, hipStream_t stream);
-hipError_t launch_duplicate_x(const uint16_t* x, uint16_t* xp, int m, int k, hipStream_t stream);
 
 // out[t, :] = dequantized row ids[t] of a projection (fp32, or bf16 rounded once), t <
 // count; ids outside [0, N) give zero rows.  out is 16-byte aligned, [count, K].

@@ -328,17 +328,6 @@ __global__ void embed8_kernel(const uint4* __restrict__ tiles, const uint2* __re
     }
 }
 
-// x' [M, 2K] = [x | x] for a two-plane handle; one thread per 16 bytes of x
-__global__ void duplicate_x_kernel(const uint4* __restrict__ x, uint4* __restrict__ xp, int k16, long total) {
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= total) return;
-    const long m = i / k16;
-    const int c = (int)(i - m * k16);
-    const uint4 v = x[i];
-    xp[m * 2 * k16 + c] = v;
-    xp[m * 2 * k16 + k16 + c] = v;
-}
-
 }  // namespace
 
 hipError_t launch_repack8(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint32_t* w_up,
@@ -369,16 +358,6 @@ hipError_t launch_embed8(const uint4* tiles, const uint2* sb, const int32_t* ids
     const long grid = (total + block - 1) / block;
     hipLaunchKernelGGL(embed8_kernel, dim3((unsigned)grid), dim3(block), 0, stream, tiles, sb, ids, out,
                        out_f32 ? 1 : 0, l.n, l.k / 2, l.g / 2, l.gp, total);
-    return hipGetLastError();
-}
-
-hipError_t launch_duplicate_x(const uint16_t* x, uint16_t* xp, int m, int k, hipStream_t stream) {
-    const int k16 = k / 8;
-    const long total = (long)m * k16;
-    const int block = 256;
-    const long grid = (total + block - 1) / block;
-    hipLaunchKernelGGL(duplicate_x_kernel, dim3((unsigned)grid), dim3(block), 0, stream,
-                       reinterpret_cast<const uint4*>(x), reinterpret_cast<uint4*>(xp), k16, total);
     return hipGetLastError();
 }
 

@@ -133,8 +133,8 @@ hipError_t static_scratch(int device, char** out) {
     return hipSuccess;
 }
 
-// Device memory one forward call borrows for its kernels' scratch (8-bit handles'
-// [x | x], the GEMM's group sums and split-K partials): stream-ordered allocations
+// Device memory one forward call borrows for its kernels' scratch (the GEMM's group
+// sums and split-K partials, the greedy head's keys): stream-ordered allocations
 // from the private pool, released on the same stream after the launches; or, for the
 // allocation-free entry point, consecutive 256-byte-aligned pieces of `scratch`.
 struct Scratch {
@@ -225,7 +225,9 @@ namespace {
 // planes over 2K; a gate|up pair interleaves its two projections 8 rows at a time.
 q4::Layout handle_layout(const Gemma4QLinearDesc& d, bool pair) {
     const int k = (int)d.in_features * (d.bits == 8 ? 2 : 1);
-    return pair ? q4::pair_layout((int)d.out_features, k) : q4::make_layout((int)d.out_features, k);
+    q4::Layout l = pair ? q4::pair_layout((int)d.out_features, k) : q4::make_layout((int)d.out_features, k);
+    l.kx = (int)d.in_features;  // two-plane handles read x [M, K] as [x | x]
+    return l;
 }
 
 Gemma4Status check_desc(const Gemma4QLinearDesc* desc, bool pair, const char* fn) {
@@ -256,31 +258,6 @@ void release(Gemma4QLinear* h) {
 }
 
 bool valid_handle(const Gemma4QLinear* h) { return h != nullptr && h->magic == kQLinearMagic; }
-
-// The x the kernels read: x itself, or for an 8-bit handle x' = [x | x] (rows x 2K) in
-// the call's scratch.
-Gemma4Status prepare_x(const Gemma4QLinear* h, const uint16_t* x, uint32_t rows, Scratch& sc, const std::string& name,
-                       const uint16_t** xk) {
-    *xk = x;
-    if (h->desc.bits != 8) return GEMMA4_OK;
-    const size_t k = h->desc.in_features;
-    const size_t bytes = (size_t)rows * 2 * k * 2;
-    if (bytes > q4::kMaxBufferBytes)
-        return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, name + ": x exceeds 1 GiB for an 8-bit projection (split the rows)");
-    if (bytes > sc.room())
-        return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
-                    name + ": [x | x] of an 8-bit projection needs " + std::to_string(bytes) +
-                        " bytes of scratch, more than the " + std::to_string(kStaticScratchBytes) +
-                        "-byte static scratch holds (split the rows)");
-    void* xs = nullptr;
-    hipError_t e = sc.take(bytes, &xs);
-    if (e != hipSuccess)
-        return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": x workspace allocation failed: " + hipGetErrorString(e));
-    e = q4::launch_duplicate_x(x, static_cast<uint16_t*>(xs), (int)rows, (int)k, sc.stream);
-    if (e != hipSuccess) return hip_fail((name + ": x duplicate").c_str(), e);
-    *xk = static_cast<const uint16_t*>(xs);
-    return GEMMA4_OK;
-}
 
 // One weight triple in MLX layout (device pointers).
 struct Triple {
@@ -387,8 +364,6 @@ Gemma4Status dispatch_forward(const Gemma4QLinear* linear, const uint16_t* x_dev
     const bool f32 = y_dtype == GEMMA4_QMM_F32;
     const int mode = geglu ? (f32 ? q4::kOutGegluF32 : q4::kOutGegluBf16) : (f32 ? q4::kOutF32 : q4::kOutBf16);
     const int n_out = linear->pair_rows;
-    Gemma4Status pst = prepare_x(linear, x_dev, rows, sc, name, &x_dev);
-    if (pst != GEMMA4_OK) return pst;
     hipError_t e;
     if (q4::use_decode(rows, linear->layout, (int)g_gemm_min_rows.load(std::memory_order_relaxed))) {
         const q4::OutParams op{y_dev, nullptr, mode, n_out, 0, 0.0f};
@@ -669,14 +644,12 @@ Gemma4Status gemma4_qlinear_forward_greedy(const Gemma4QLinear* linear, void* st
             return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
         const int mode = dtype == GEMMA4_QMM_F32 ? q4::kOutGreedyF32 : q4::kOutGreedyBf16;
         const q4::OutParams op{logits_dev, static_cast<unsigned long long*>(part), mode, 0, nb, softcap};
-        Gemma4Status pst = prepare_x(linear, x_dev, rows, sc, name, &x_dev);
-        if (pst == GEMMA4_OK) {
-            e = q4::launch_decode(linear->tiles, linear->sb, x_dev, op, (int)rows, linear->layout, sc.stream);
-            if (e == hipSuccess)
-                e = q4::launch_greedy_reduce(static_cast<const unsigned long long*>(part), nb, (int)rows, token_dev,
-                                             value_dev, sc.stream);
-            if (e != hipSuccess) pst = hip_fail((name + ": launch").c_str(), e);
-        }
+        Gemma4Status pst = GEMMA4_OK;
+        e = q4::launch_decode(linear->tiles, linear->sb, x_dev, op, (int)rows, linear->layout, sc.stream);
+        if (e == hipSuccess)
+            e = q4::launch_greedy_reduce(static_cast<const unsigned long long*>(part), nb, (int)rows, token_dev,
+                                         value_dev, sc.stream);
+        if (e != hipSuccess) pst = hip_fail((name + ": launch").c_str(), e);
         const hipError_t ef = sc.release();
         if (pst != GEMMA4_OK) return pst;
         if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);

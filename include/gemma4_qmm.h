@@ -35,7 +35,7 @@
  * Gemma 4 12B artifact and the only overrides its loader allows (model_manifest.cc:148).
  * With bits = 8 the weight is uint32 [N, K/4], code k in byte k%4 of word k/4, lowest
  * byte first; it is held as two 4-bit planes (q = 16*qh + ql) and runs on the same
- * kernels over 2K, reading [x | x].
+ * kernels over 2K, which read x in place as [x | x].
  *
  * Streams are hipStream_t values passed as void* (NULL = the null stream).  All
  * device work is asynchronous on that stream.  A handle is immutable after
@@ -157,12 +157,12 @@ Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, c
  * 64 MiB device array that the library holds on each GPU it runs on until the
  * process ends.  No counterpart in the reference (its MLX ops allocate per call).
  * It calls no hipMalloc, hipFree or allocating library routine.  Scratch needs:
- * none for 4-bit calls on the decode path (gemma4_qmm_set_gemm_min_rows); on the
- * GEMM path the group sums of x (rows * K / 8
- * bytes, rounded up to 128- or 256-row tiles), and split-K partial sums only as far
- * as the array has room (fewer splits than gemma4_qlinear_forward may choose, so the
- * fp32 summation order, and with it the last bits of some outputs, can differ from
- * that call's); 8-bit handles add [x | x], rows * 4K bytes.  A call needing more
+ * none on the decode path (gemma4_qmm_set_gemm_min_rows); on the GEMM path the
+ * group sums of x (rows * K / 8 bytes, rows * K / 4 for 8-bit handles, rounded up to
+ * 128- or 256-row tiles), and split-K partial sums only as far as the array has room
+ * (fewer splits than gemma4_qlinear_forward may choose, so the fp32 summation order,
+ * and with it the last bits of some outputs, can differ from that call's).  A call
+ * needing more
  * than 64 MiB fails with GEMMA4_ERR_UNSUPPORTED_CONFIG (split the rows).  Every call
  * on a GPU shares that GPU's array: calls that overlap in time on one GPU (other
  * streams, other threads) race and must be serialized by the caller. */

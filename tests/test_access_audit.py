@@ -50,7 +50,19 @@ def tile_of(bid, nwg, mtiles, ntiles):
     return band * 2 + r % bm, r // bm
 
 
-def audit_gemm(m, n, k, BM, splits, BN=256):
+def xprime_offset(c, k, kx):
+    """Byte offset in x (rows of kx) of 16-byte unit c of x' (rows of k): column c of a
+    two-plane handle's x' = [x | x] is column c mod kx of x."""
+    c = np.asarray(c, np.int64)
+    if kx == k:
+        return c * 16
+    row, cr = c // (k // 8), c % (k // 8)
+    return (row * (kx // 8) + np.where(cr >= kx // 8, cr - kx // 8, cr)) * 16
+
+
+def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
+    """kx: the row length of x (k, or k / 2 for a two-plane 8-bit handle)."""
+    kx = kx or k
     L = layout(n, k)
     WAVES = 2 * BN // 64   # 2 (M) x BN/64 (N)
     RB = BN // 16
@@ -67,7 +79,8 @@ def audit_gemm(m, n, k, BM, splits, BN=256):
     mtiles = (m + BM - 1) // BM
     ntiles = (n + BN - 1) // BN
     nblocks = (n + 15) // 16
-    xbytes = m * k * 2
+    xbytes = m * kx * 2
+    gx = kx // 64
     ws_bytes = mtiles * (BM // 16) * octets * 1024
     per = (octets + splits - 1) // splits
     assert (octets + per - 1) // per == splits
@@ -94,9 +107,12 @@ def audit_gemm(m, n, k, BM, splits, BN=256):
                 c = (q & 7) ^ ((rr >> 1) & 7)
                 row = mt * BM + rr
                 assert ((WAVES * part + wave) * 64 + 64) <= BM * 8
-                xv = np.where(row < m, (row * k + 8 * c) * 2, OOB)
-                for g in (0, G - 1):  # a per-lane constant plus g * 128: the extremes bound every step
-                    chk_buf("gemm x", np.where(xv == OOB, OOB, xv + g * 128), 16, xbytes, xbytes)
+                xv = np.where(row < m, (row * kx + 8 * c) * 2, OOB)
+                # a per-lane constant plus (g mod gx) * 128: the extremes bound every step
+                for g in sorted({0, G - 1, min(G, gx) - 1, gx % G}):
+                    gm = g - gx if g >= gx else g
+                    assert 0 <= gm < gx
+                    chk_buf("gemm x", np.where(xv == OOB, OOB, xv + gm * 128), 16, xbytes, xbytes)
             for part in range(2):
                 rb = rbw + 2 * wave + part
                 wv = np.where(rb < nblocks, (rb * L["gp"] * 64 + lane) * 16, OOB)
@@ -161,6 +177,16 @@ def test_gemm_accesses(m, n, k, bm, bn):
         if (octets + per - 1) // per == s:
             audit_gemm(m, n, k, bm, s, bn)
 
+# two-plane 8-bit handles: the tiled K' = 2K, x rows of K
+@pytest.mark.parametrize("m,n,k", [(2048, 15360, 3840), (300, 130, 1088), (33, 48, 576), (64, 96, 3840)])
+@pytest.mark.parametrize("bm,bn", [(256, 256), (128, 256)])
+def test_gemm_accesses_two_plane(m, n, k, bm, bn):
+    octets = (2 * k // 64 + 7) // 8
+    for s in sorted({1, 2, min(8, octets), octets}):
+        per = (octets + s - 1) // s
+        if (octets + per - 1) // per == s:
+            audit_gemm(m, n, 2 * k, bm, s, bn, kx=k)
+
 
 # ----------------------------------------------------------------------- decode
 
@@ -179,9 +205,11 @@ def _chunk_reads(first, n_in, tile_bytes, sb_bytes):
     assert (n_in * 1024 <= 2 ** 31).all()
 
 
-def audit_decode_stream(m_total, n, k, cus=256):
+def audit_decode_stream(m_total, n, k, cus=256, kx=None):
     """decode_stream_kernel: persistent workgroups over row blocks, K split over waves,
-    16-row slabs along grid y; x staged in LDS with zero padding and a -X table."""
+    16-row slabs along grid y; x staged in LDS with zero padding and a -X table; x rows
+    are kx long (k, or k / 2 for a two-plane handle's x' = [x | x])."""
+    kx = kx or k
     L = layout(n, k)
     GPW = 4
     MT = 1 if m_total == 1 else 2 if m_total == 2 else 4 if m_total <= 4 else 16
@@ -248,7 +276,7 @@ def audit_decode_stream(m_total, n, k, cus=256):
         row = c // rowc
         cr = c - row * rowc
         assert (row * row16 + cr < negx_base).all() and ((cr >> 3) * 16 + row < tab).all()
-        chk_buf("dec x", c * 16, 16, m_rows * k * 2, m_rows * k * 2)
+        chk_buf("dec x", xprime_offset(c, k, kx), 16, m_rows * kx * 2, m_rows * kx * 2)
         pad = (GPW * 128) >> 3
         c = np.arange(m_rows * pad)
         assert ((c // pad) * row16 + rowc + (c % pad) < negx_base).all()
@@ -299,6 +327,13 @@ DECODE_SHAPES = [(40, 384), (64, 320), (16, 64), (4096, 3840), (2048, 3840), (38
 @pytest.mark.parametrize("m", [1, 2, 4, 8, 9, 16, 17, 31])
 def test_decode_stream_accesses(m, n, k):
     audit_decode_stream(m, n, k)
+
+
+# two-plane 8-bit handles (K' = 2K, x rows of K)
+@pytest.mark.parametrize("n,k", [(15360, 3840), (48, 576), (130, 1088), (4096, 3840), (262144, 3840)])
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 9, 16, 17, 31])
+def test_decode_stream_accesses_two_plane(m, n, k):
+    audit_decode_stream(m, n, 2 * k, kx=k)
 
 
 @pytest.mark.parametrize("n,k", [(15360, 3840), (30720, 3840), (8192 + 48, 128), (8192, 640), (16 * 512, 3840)])

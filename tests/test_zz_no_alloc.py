@@ -74,7 +74,7 @@ def test_noalloc_matches_forward_on_consecutive_calls(gpu_lib, dtype_name, gemm_
 def test_noalloc_eight_bit_and_its_limit(gpu_lib, gemm_from_32):
     import torch
 
-    # 8-bit: [x | x] in the static scratch, then the GEMM's workspace after it
+    # 8-bit: the GEMM's workspace over K' = 2K (x itself is read in place)
     rng = np.random.default_rng(91)
     w = A.round_to_bf16((rng.standard_normal((96, 3840)) * 0.02).astype(np.float32))
     tri = C.quantize(w, bits=8)
@@ -84,11 +84,12 @@ def test_noalloc_eight_bit_and_its_limit(gpu_lib, gemm_from_32):
         ref, got = _both(lin, dev_x(x), torch.float32)
         _compare(ref, got, x, tri, np.arange(m), f"8-bit m={m}", bits=8)
         lin.close()
-    # [x | x] of 2048 rows at K = 15360 needs 126 MB: refused before any launch
+    # the GEMM's group sums of 18000 rows over K' = 30720 need 70 MB: refused before any
+    # launch
     small = C.quantize(A.round_to_bf16((rng.standard_normal((16, 15360)) * 0.02).astype(np.float32)), bits=8)
     lin = gpu_lib.QuantizedLinear(*dev_triple(*small), bits=8)
-    x = torch.zeros((2048, 15360), dtype=torch.bfloat16, device="cuda")
-    y = torch.zeros((2048, 16), dtype=torch.bfloat16, device="cuda")
+    x = torch.zeros((18000, 15360), dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros((18000, 16), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(gpu_lib.Gemma4Error) as e:
         lin.forward_noalloc(x, y)
     assert e.value.status == gpu_lib.Status.UNSUPPORTED_CONFIG and "scratch" in e.value.message

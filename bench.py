@@ -456,6 +456,69 @@ def variants_run(torch, Q, host) -> dict:
     return out
 
 
+def summarize_gemm(stats_dir: str, pmc_dir: str, line_file: str, command: str) -> None:
+    """Turns rocprofv3 output over `bench.py --gemm-only` into the headline GEMM's
+    committed summary (profiles/gate_prefill_m2048.md): the kernel-trace statistics
+    (the GEMM kernel's average duration and the TFLOPS it implies), and the counters of
+    one --pmc pass per dispatch of the GEMM kernel (median over dispatches), with the
+    matrix cores' busy share: SQ_VALU_MFMA_BUSY_CYCLES per SIMD over the kernel's
+    cycles (GRBM_GUI_ACTIVE counts once per XCD)."""
+    import statistics
+
+    with open(line_file) as f:
+        line = json.loads([l for l in f if l.startswith("{")][-1])
+    stats = _csv_rows(stats_dir, "kernel_stats.csv")
+    rows = _csv_rows(pmc_dir, "counter_collection.csv")
+
+    def short(name: str) -> str:
+        return name.replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0][:90]
+
+    is_gemm = lambda n: "gemm_kernel" in n  # noqa: E731
+    per = {}
+    for r in rows:
+        if is_gemm(r["Kernel_Name"]):
+            per.setdefault(r["Counter_Name"], {}).setdefault(r["Dispatch_Id"], 0.0)
+            per[r["Counter_Name"]][r["Dispatch_Id"]] += float(r["Counter_Value"])
+    med = {c: statistics.median(v.values()) for c, v in per.items()}
+    g = [r for r in stats if is_gemm(r["Name"])]
+    avg_us = float(g[0]["AverageNs"]) / 1e3 if g else None
+    m, n, k = 2048, 15360, HIDDEN
+    md = [f"# Prefill GEMM: {short(g[0]['Name']) if g else 'gemm_kernel'} gate_proj M=2048 N=15360 K=3840 (bf16 out)", "",
+          "Command (from the repository root):", "", "```", command, "```", "",
+          f"Unprofiled line (`bench.py --gemm-only`): {json.dumps(line)}", "",
+          "rocprofv3 --kernel-trace --stats (kernel_stats.csv):", "",
+          "| kernel | calls | avg us | min us | max us |", "|---|---:|---:|---:|---:|"]
+    for r in sorted((r for r in stats if "q4::" in r["Name"]), key=lambda r: -float(r["TotalDurationNs"]))[:6]:
+        md.append(f"| {short(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                  f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} |")
+    if avg_us:
+        tf = algo_flops(m, n, k) / (avg_us * 1e-6) / 1e12
+        md += ["", f"GEMM kernel alone: {tf:.0f} TFLOPS at the rocprof average ({avg_us:.1f} us), "
+                   f"{tf / BF16_PEAK_TFLOPS:.1%} of {BF16_PEAK_TFLOPS / 1e3:.1f} PF dense bf16."]
+    md += ["", "Counters per dispatch of the GEMM kernel (median over dispatches; SQ counters summed over the chip):",
+           "", "| counter | value |", "|---|---:|"]
+    for c in sorted(med):
+        md.append(f"| {c} | {med[c]:.0f} |")
+    if {"SQ_INSTS_MFMA", "SQ_INSTS_VALU"} <= med.keys():
+        mf, va = med["SQ_INSTS_MFMA"], med["SQ_INSTS_VALU"]
+        md += ["", f"- MFMA instructions {mf / 1e6:.2f} M; other VALU instructions (SQ_INSTS_VALU counts the MFMAs "
+                   f"too) {(va - mf) / 1e6:.2f} M, {(va - mf) / mf:.2f} per MFMA."]
+    if {"SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE"} <= med.keys():
+        simds = 4 * device_cus_hint()
+        busy = med["SQ_VALU_MFMA_BUSY_CYCLES"] / simds
+        cyc = med["GRBM_GUI_ACTIVE"] / 8
+        md.append(f"- Matrix-core busy cycles per SIMD: {busy / 1e3:.0f} K of {cyc / 1e3:.0f} K kernel cycles "
+                  f"(GRBM_GUI_ACTIVE / 8 XCDs): {busy / cyc:.0%} busy.")
+    with open(os.path.join(ROOT, "profiles", "gate_prefill_m2048.md"), "w") as f:
+        f.write("\n".join(md) + "\n")
+    print("\n".join(md))
+
+
+def device_cus_hint() -> int:
+    """Compute units of the part the counters came from (MI355X: 256)."""
+    return 256
+
+
 def summarize_trace(db_path: str, out_md: str, command: str) -> None:
     """Per-shape kernel durations of `bench.py --prefill-only` from a rocprofv3
     --kernel-trace database (rocpd SQLite).  Each shape's handles are created (repack
@@ -746,6 +809,8 @@ def main() -> int:
                     help="time only the dominant kernel and a 1 GiB copy (the program rocprofv3 passes run)")
     ap.add_argument("--summarize-profiles", nargs=5, metavar=("STATS_DIR", "FETCH_DIR", "WRITE_DIR", "LINE", "CMD"),
                     help="write the profiles/ summaries from rocprofv3 output over --roofline-only (no GPU)")
+    ap.add_argument("--summarize-gemm", nargs=4, metavar=("STATS_DIR", "PMC_DIR", "LINE", "CMD"),
+                    help="write profiles/gate_prefill_m2048.md from rocprofv3 output over --gemm-only")
     ap.add_argument("--summarize-trace", nargs=3, metavar=("RESULTS_DB", "OUT_MD", "CMD"),
                     help="write a per-shape summary of a rocprofv3 kernel trace of --prefill-only (no GPU)")
     args = ap.parse_args()
@@ -754,6 +819,9 @@ def main() -> int:
         return 0
     if args.summarize_trace:
         summarize_trace(*args.summarize_trace)
+        return 0
+    if args.summarize_gemm:
+        summarize_gemm(*args.summarize_gemm)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)

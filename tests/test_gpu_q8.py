@@ -1,5 +1,5 @@
 """GPU parity at bits = 8 (the QAT override, model_manifest.cc:148) through the C ABI:
-the handle holds two 4-bit planes over 2K and reads [x | x], so every 4-bit path
+the handle holds two 4-bit planes over 2K and reads x in place as [x | x], so every 4-bit path
 (decode, GEMM, GeGLU pair, greedy head, embedding) is checked again at 8 bits against
 the oracle's 8-bit dequantize / qmm, with the bars of test_gpu_parity.py (bit-exact
 dequantize, bf16 output max|err| <= 1e-2 RMS + ulp/2, fp32 <= 2e-3 RMS)."""
@@ -49,6 +49,25 @@ def test_q8_forward(gpu_lib, gemm_from_32, n, k, m, f32):
     rows = np.arange(m) if m <= 64 else np.sort(np.random.default_rng(m).choice(m, 16, replace=False))
     want = C.qmm_f64(np.ascontiguousarray(x[rows]), *tri, bits=8)
     assert_close(y[torch.from_numpy(rows).cuda()], want, f"q8 N={n} K={k} M={m} f32={f32}")
+
+
+# the automatic path choice at 8 bits: rows x N x 2K <= 1.6e9 run on the decode kernels
+# past 32 rows (16-row slabs reading x in place as [x | x]; the global-x kernel for
+# K = 3840 and 640 x 1088, slabs of one and of several row blocks)
+@pytest.mark.parametrize("n,k,m", [(2048, 3840, 64), (512, 3840, 200), (640, 1088, 100), (4096, 3840, 9)])
+@pytest.mark.parametrize("f32", [False, True])
+def test_q8_decode_slabs_past_32_rows(gpu_lib, n, k, m, f32):
+    import torch
+
+    tri = triple8(n, k, 11 * n + k)
+    x = A.make_activations(m, k, seed=3 * m + n, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*tri), bits=8)
+    y = lin.forward(dev_x(x), out_dtype=torch.float32 if f32 else torch.bfloat16)
+    torch.cuda.synchronize()
+    lin.close()
+    rows = np.unique(np.concatenate([np.linspace(0, m - 1, 20).astype(np.int64), [m - 1]]))
+    want = C.qmm_f64(np.ascontiguousarray(x[rows]), *tri, bits=8)
+    assert_close(y[torch.from_numpy(rows).cuda()], want, f"q8 slabs N={n} K={k} M={m} f32={f32}")
 
 
 def test_q8_pair_greedy_and_embed(gpu_lib):

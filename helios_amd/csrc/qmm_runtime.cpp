@@ -416,7 +416,7 @@ Gemma4Status run_forward(const Gemma4QLinear* linear, void* stream, const uint16
     if ((reinterpret_cast<uintptr_t>(y_dev) & yalign) != 0)
         return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": the output is misaligned for its dtype");
     if (rows > (1u << 24)) return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, name + ": rows exceeds 2^24");
-    if ((size_t)rows * linear->layout.k * 2 > q4::kMaxBufferBytes)
+    if ((size_t)rows * linear->layout.kx * 2 > q4::kMaxBufferBytes)
         return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, name + ": x exceeds 2 GiB (split the rows into several calls)");
     DeviceGuard guard;
     hipError_t e = guard.enter(linear->device);

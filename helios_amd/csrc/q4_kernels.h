@@ -110,6 +110,8 @@ hipError_t launch_gelu_table(uint16_t* table, hipStream_t stream);
 // (q4_lora.hip).
 constexpr int kLoraSlices = 8;
 int lora_slices(int k, int m);
+// Small M and rank: one fused launch that needs no part scratch (part may be null).
+bool lora_fused(int m, int rank);
 hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float* part, void* y, int m, int n, int k,
                        int rank, float scale, bool out_f32, hipStream_t stream);
 

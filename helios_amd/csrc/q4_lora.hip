@@ -20,7 +20,8 @@
 // takes its column's B values into registers and forms its rows' deltas.  With 32
 // rows (M > 16) the deltas go through LDS and y is read and written in 16-byte pieces
 // by consecutive threads (when N and y allow it); with 16 each thread updates its own
-// column.  B is read once per 16 or 32 rows, y once.
+// column.  B is read once per 16 or 32 rows, y once.  Up to 4 rows with rank up to
+// 64, lora_fused_kernel_f does both steps in one launch (below).
 #include "q4_common.h"
 #include "q4_kernels.h"
 
@@ -32,6 +33,8 @@ constexpr int kWaveRanks = 4;   // ranks per lora_down wave
 constexpr int kRankBlock = 16;  // ranks per lora_down workgroup / per lora_up register block
 constexpr int kUpRows = 16;     // rows of y per lora_up workgroup (M <= 16)
 constexpr int kUpRowsLarge = 32;  // rows of y per lora_up workgroup (M > 16)
+constexpr int kFusedRows = 4;      // M up to this with rank up to kFusedMaxRank: one fused launch
+constexpr int kFusedMaxRank = 64;
 
 __global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restrict__ x, const float* __restrict__ a,
                                                         float* __restrict__ part, int m_rows, int rank, int k,
@@ -245,6 +248,91 @@ __global__ __launch_bounds__(256) void lora_up_kernel(const float* __restrict__ 
     }
 }
 
+
+// Small M (lora_fused(m, rank)): the whole delta in one launch, with no scratch.  A
+// 1024-thread workgroup per 256 columns of y:
+//   (1) t = x . A^T for all rows and ranks, computed by every workgroup (x and A come
+//       from L2 after the first): the 16 waves take 16 ranks of a block, a wave's
+//       lanes interleave K's 8-column chunks, and each wave sums its lanes by
+//       shuffles (a fixed order) into LDS;
+//   (2) each column's delta from t and its row of B, four threads per column with a
+//       contiguous quarter of the ranks each, the quarters added in a fixed order in
+//       LDS, then y updated as lora_up does.
+__global__ __launch_bounds__(1024) void lora_fused_kernel_f(const uint16_t* __restrict__ x, const float* __restrict__ a,
+                                                            const float* __restrict__ b, void* __restrict__ y,
+                                                            int m_rows, int n_rows, int k, int rank, float scale,
+                                                            int out_f32) {
+#pragma clang fp contract(off)
+    __shared__ float ts[kFusedRows][kFusedMaxRank];
+    __shared__ float dq[4][kFusedRows][256];
+    const int tid = (int)threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int chunks = k >> 3;
+    for (int r0 = 0; r0 < rank; r0 += 16) {
+        const int r = r0 + wave;
+        float acc[kFusedRows];
+#pragma unroll
+        for (int i = 0; i < kFusedRows; ++i) acc[i] = 0.f;
+        if (r < rank) {
+            const float* ar = a + (long)r * k;
+#pragma unroll 2
+            for (int c = lane; c < chunks; c += 64) {
+                const float4 a0 = *reinterpret_cast<const float4*>(ar + 8 * c);
+                const float4 a1 = *reinterpret_cast<const float4*>(ar + 8 * c + 4);
+                const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+                for (int i = 0; i < kFusedRows; ++i) {
+                    if (i < m_rows) {
+                        const uint4 xu = *reinterpret_cast<const uint4*>(x + (long)i * k + 8 * c);
+                        const uint32_t w[4] = {xu.x, xu.y, xu.z, xu.w};
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            acc[i] = __builtin_fmaf(bf16_lo(w[j]), av[2 * j], acc[i]);
+                            acc[i] = __builtin_fmaf(bf16_hi(w[j]), av[2 * j + 1], acc[i]);
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kFusedRows; ++i) {
+            float v = acc[i];
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+            if (lane == 0 && r < rank) ts[i][r] = v;
+        }
+    }
+    __syncthreads();
+    const int col = tid & 255, q = tid >> 8;
+    const int n = (int)blockIdx.x * 256 + col;
+    const int r_lo = q * rank / 4, r_hi = (q + 1) * rank / 4;
+    float d[kFusedRows];
+#pragma unroll
+    for (int i = 0; i < kFusedRows; ++i) d[i] = 0.f;
+    if (n < n_rows) {
+        const float* br = b + (long)n * rank;
+        for (int r = r_lo; r < r_hi; ++r) {
+            const float bv = br[r];
+#pragma unroll
+            for (int i = 0; i < kFusedRows; ++i) d[i] = __builtin_fmaf(ts[i][r], bv, d[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kFusedRows; ++i) dq[q][i][col] = d[i];
+    __syncthreads();
+    if (q != 0 || n >= n_rows) return;
+    for (int i = 0; i < m_rows; ++i) {
+        const float v = ((dq[0][i][col] + dq[1][i][col]) + dq[2][i][col]) + dq[3][i][col];
+        const long o = (long)i * n_rows + n;
+        if (out_f32) {
+            static_cast<float*>(y)[o] = static_cast<const float*>(y)[o] + v * scale;
+        } else {
+            const float base = __uint_as_float((uint32_t)static_cast<const uint16_t*>(y)[o] << 16);
+            static_cast<uint16_t*>(y)[o] = f32_to_bf16(base + round_bf16(v * round_bf16(scale)));
+        }
+    }
+}
+
 }  // namespace
 
 int lora_slices(int k, int m) {
@@ -257,9 +345,16 @@ int lora_slices(int k, int m) {
     return s;
 }
 
+bool lora_fused(int m, int rank) { return m <= kFusedRows && rank <= kFusedMaxRank; }
+
 hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float* part, void* y, int m, int n, int k,
                        int rank, float scale, bool out_f32, hipStream_t stream) {
     static_assert(kWaveRanks * 4 == kRankBlock, "four waves per lora_down workgroup");
+    if (lora_fused(m, rank)) {
+        hipLaunchKernelGGL(lora_fused_kernel_f, dim3((unsigned)((n + 255) / 256)), dim3(1024), 0, stream, x, a, b, y, m,
+                           n, k, rank, scale, out_f32 ? 1 : 0);
+        return hipGetLastError();
+    }
     const int slices = lora_slices(k, m);
     const int slice_chunks = (k / 8 + slices - 1) / slices;
     const dim3 dgrid((unsigned)((m + kDownRows - 1) / kDownRows), (unsigned)((rank + kRankBlock - 1) / kRankBlock),

@@ -733,17 +733,22 @@ Gemma4Status gemma4_qlinear_forward_lora(const Gemma4QLinear* linear, const Gemm
         hipError_t e = guard.enter(linear->device);
         if (e != hipSuccess) return hip_fail((name + ": hipSetDevice").c_str(), e);
         hipStream_t sh = static_cast<hipStream_t>(stream);
+        // the fused small-M launch needs no scratch
+        const bool fused = q4::lora_fused((int)rows, (int)lora->rank);
         hipMemPool_t pool = nullptr;
-        e = scratch_pool(linear->device, &pool);
         void* t = nullptr;
-        const size_t t_bytes = (size_t)q4::lora_slices((int)linear->desc.in_features, (int)rows) * rows * lora->rank * 4;
-        if (e == hipSuccess) e = hipMallocFromPoolAsync(&t, t_bytes, pool, sh);
-        if (e != hipSuccess)
-            return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
+        if (!fused) {
+            e = scratch_pool(linear->device, &pool);
+            const size_t t_bytes =
+                (size_t)q4::lora_slices((int)linear->desc.in_features, (int)rows) * rows * lora->rank * 4;
+            if (e == hipSuccess) e = hipMallocFromPoolAsync(&t, t_bytes, pool, sh);
+            if (e != hipSuccess)
+                return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
+        }
         e = q4::launch_lora(x_dev, lora->a, lora->b, static_cast<float*>(t), y_dev, (int)rows,
                             (int)linear->desc.out_features, (int)linear->desc.in_features, (int)lora->rank, lora->scale,
                             y_dtype == GEMMA4_QMM_F32, sh);
-        const hipError_t ef = hipFreeAsync(t, sh);
+        const hipError_t ef = fused ? hipSuccess : hipFreeAsync(t, sh);
         if (e != hipSuccess) return hip_fail((name + ": launch").c_str(), e);
         if (ef != hipSuccess) return hip_fail((name + ": workspace release").c_str(), ef);
         return ok();

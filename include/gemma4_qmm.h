@@ -190,9 +190,10 @@ Gemma4Status gemma4_qlora_create(const float* a, const float* b, uint32_t rank, 
 Gemma4Status gemma4_qlora_free(Gemma4QLora* lora);
 
 /* gemma4_qlinear_forward plus the adapter's delta; lora NULL is the plain forward.
- * The adapter must match the projection's K and N and live on its device.  Uses a
- * stream-ordered scratch of at most 8 * rows * rank * 4 bytes (x . A^T summed over up
- * to eight slices of K). */
+ * The adapter must match the projection's K and N and live on its device.  Up to 4
+ * rows with rank up to 64: one fused launch and no scratch; otherwise a stream-ordered
+ * scratch of at most 8 * rows * rank * 4 bytes (x . A^T summed over up to eight
+ * slices of K). */
 Gemma4Status gemma4_qlinear_forward_lora(const Gemma4QLinear* linear, const Gemma4QLora* lora, void* stream,
                                          const uint16_t* x_dev, uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype);
 

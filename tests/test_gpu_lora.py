@@ -27,8 +27,11 @@ def check_bf16_two_roundings(y_bits, want):
     return worst <= BF16_REL, worst
 
 
+# M <= 4 with rank <= 64 runs the fused one-launch kernel (rank 64 at M = 3 its edge;
+# rank 65 at M = 1 and M = 8 the two-kernel path)
 @pytest.mark.parametrize("n,k,m,r", [(4096, 3840, 1, 16), (2048, 3840, 4, 8), (3840, 15360, 8, 16),
-                                     (300, 640, 17, 4), (256, 640, 64, 16), (512, 3840, 300, 32)])
+                                     (300, 640, 17, 4), (256, 640, 64, 16), (512, 3840, 300, 32),
+                                     (1000, 640, 3, 64), (520, 384, 1, 65)])
 @pytest.mark.parametrize("f32", [False, True])
 def test_lora_forward(gpu_lib, gemm_from_32, n, k, m, r, f32):
     import torch

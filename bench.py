@@ -504,7 +504,9 @@ def summarize_gemm(stats_dir: str, pmc_dir: str, line_file: str, command: str) -
         md += ["", f"- MFMA instructions {mf / 1e6:.2f} M; other VALU instructions (SQ_INSTS_VALU counts the MFMAs "
                    f"too) {(va - mf) / 1e6:.2f} M, {(va - mf) / mf:.2f} per MFMA."]
     if {"SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE"} <= med.keys():
-        simds = 4 * device_cus_hint()
+        # the profiled GPU's SIMD count, from the agent description rocprofv3 writes
+        agents = [r for r in _csv_rows(pmc_dir, "agent_info.csv") if int(r.get("Simd_Count") or 0) > 0]
+        simds = int(agents[0]["Simd_Count"]) if agents else 1024
         busy = med["SQ_VALU_MFMA_BUSY_CYCLES"] / simds
         cyc = med["GRBM_GUI_ACTIVE"] / 8
         md.append(f"- Matrix-core busy cycles per SIMD: {busy / 1e3:.0f} K of {cyc / 1e3:.0f} K kernel cycles "
@@ -512,11 +514,6 @@ def summarize_gemm(stats_dir: str, pmc_dir: str, line_file: str, command: str) -
     with open(os.path.join(ROOT, "profiles", "gate_prefill_m2048.md"), "w") as f:
         f.write("\n".join(md) + "\n")
     print("\n".join(md))
-
-
-def device_cus_hint() -> int:
-    """Compute units of the part the counters came from (MI355X: 256)."""
-    return 256
 
 
 def summarize_trace(db_path: str, out_md: str, command: str) -> None:

@@ -399,7 +399,7 @@ def summarize_profiles(stats_dir: str, fetch_dir: str, write_dir: str, line_file
     print(json.dumps(traffic))
 
 
-PREFILL_MS = (256, 512, 2048)
+PREFILL_MS = (64, 256, 512, 2048)
 
 
 def prefill_sweep_names(ms=PREFILL_MS):
@@ -798,7 +798,7 @@ def main() -> int:
     ap.add_argument("--gemm-only", action="store_true",
                     help="the headline prefill GEMM (gate_proj, M=2048) only, one JSON line (for rocprofv3)")
     ap.add_argument("--prefill-only", action="store_true",
-                    help="the prefill GEMM sweep only (the seven projections at M = 256, 512, 2048 and the "
+                    help="the prefill GEMM sweep only (the seven projections at M = 64, 256, 512, 2048 and the "
                          "full-attention shapes), one JSON line (for rocprofv3 kernel traces)")
     ap.add_argument("--settle-ms", type=float, default=100.0,
                     help="untimed wall time of headline replays after the warm-up replays (the clock ramps)")
@@ -966,7 +966,7 @@ def main() -> int:
         except Exception as e:  # memory or build problems should not hide the headline
             lm = {"error": str(e)}
 
-    # --- prefill GEMM: the seven projections at M = 256, 512, 2048 (gate at M=2048 headlines) ---
+    # --- prefill GEMM: the seven projections at M = 64, 256, 512, 2048 (gate at M=2048 headlines) ---
     gemm = None
     peaks = None
     if not args.no_gemm:
@@ -974,7 +974,7 @@ def main() -> int:
             gemm = prefill_sweep(torch, Q, host, (2048,), [l for l in LAYER if l[0] == "gate_proj"], pair=False,
                                  full_attention=False)
         else:
-            gemm = prefill_sweep(torch, Q, host, (256, 512, 2048), LAYER, pair=True, full_attention=True)
+            gemm = prefill_sweep(torch, Q, host, PREFILL_MS, LAYER, pair=True, full_attention=True)
         head = gemm["gate_proj_m2048"]
         gemm["headline"] = {"shape": "gate_proj M=2048 N=15360 K=3840", **head}
         if not args.quick:

@@ -133,7 +133,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
                                                    const uint16_t* __restrict__ gelu_table) {
     // BM = 256: 2 x 4 waves of 128 x 64; BM = 128: 2 x 4 waves of 64 x 64 (more
     // workgroups for small M without splitting K); BN = 128: 2 x 2 waves
-    static_assert(BM == 256 || BM == 128, "tile rows");
+    static_assert(BM == 256 || BM == 128 || BM == 64, "tile rows");
     static_assert(BN == 256 || BN == 128, "tile columns");
     constexpr int kWaves = 2 * (BN / kWN);        // 2 (M) x BN/64 (N) waves
     constexpr int kRB = BN / 16;                  // 16-row weight blocks per workgroup tile
@@ -144,10 +144,14 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     constexpr int kWM = BM / 2;                   // wave tile rows
     constexpr int kMT = kWM / 16;                 // 16x16 tiles per wave along M
     constexpr int kXParts = BM * 8 / (64 * kWaves);  // 16-byte x loads per wave per group
-    constexpr int kXaParts = BM / 16 / kWaves;    // bias A-operand loads per wave per octet
+    // bias A-operand loads per wave per octet: BM / 16 row blocks over the waves (with
+    // BM = 64, waves 0-3 load one each and the rest none)
+    constexpr int kXaParts = BM / 16 >= kWaves ? BM / 16 / kWaves : 1;
+    constexpr int kXaWaves = BM / 16 >= kWaves ? kWaves : BM / 16;
     constexpr int kSWaves = kRB / 8;              // waves that load a pair's scale words (1 KiB each)
+    constexpr int kTW = kMT * kNT >= 12 ? 9 : 5;  // product-stream tile after which a pair's weights are issued
     static_assert(kRB == 2 * kWaves, "two row blocks of tiled words per wave per pair");
-    static_assert(kXParts >= 1 && kXaParts >= 1, "every wave loads x and bias operands");
+    static_assert(kXParts >= 1 && kXaParts * kXaWaves == BM / 16, "every wave loads x; the bias operands are covered");
     __shared__ uint4 g_xs0[kXChunks];             // x group tiles (BM rows x 64: 16 or 32 KiB)
     __shared__ uint4 g_xs1[kXChunks];
     __shared__ uint4 g_xs2[kXChunks];
@@ -233,8 +237,10 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     auto dma_xa = [&](int o) {
         int ln = threadIdx.x & 63;
         asm volatile("" : "+v"(ln));
+        if (kXaWaves == kWaves || wave < kXaWaves) {
 #pragma unroll
-        for (int u = 0; u < kXaParts; ++u) dma_xa_part(o, u);
+            for (int u = 0; u < kXaParts; ++u) dma_xa_part(o, u);
+        }
         const int rb = rbw + 2 * wave + (ln >> 5);
         const int chunk = ln & 31;
         const bool ok = (rb < nblocks) & (4 * o + (chunk >> 3) < gpairs);
@@ -342,13 +348,15 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     // (past the end they read zeros), so the counts are fixed.
     auto issues_xa = [&](int g) { return (g & 7) == 1 && g > g_begin + 1; };
     auto issued = [&](int g) {  // loads this wave issues at step g
-        return kXParts + ((g & 1) == 0 ? 2 + (wave < kSWaves ? 1 : 0) : 0) + (issues_xa(g) ? kXaParts + 1 : 0);
+        return kXParts + ((g & 1) == 0 ? 2 + (wave < kSWaves ? 1 : 0) : 0) +
+               (issues_xa(g) ? (wave < kXaWaves ? kXaParts : 0) + 1 : 0);
     };
     auto step = [&](int g, const uint4* xs, const uint4* wp, uint4* xs2, uint4* wp2) {
         if (g == g_begin) {
             wait_vm_lds<0>();
         } else {
             switch (issued(g - 1)) {
+                case 1: wait_vm_lds<1>(); break;
                 case 2: wait_vm_lds<2>(); break;
                 case 3: wait_vm_lds<3>(); break;
                 case 4: wait_vm_lds<4>(); break;
@@ -371,7 +379,9 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         const bool pair = (g & 1) == 0;
         compute(xs, wp, g & 1, [&](int t) {
             if ((t & 1) && (t >> 1) < kXParts) dma_x(g + 2, t >> 1, xs2);
-            if (pair && (t == 9 || t == 11)) dma_w((g + 2) >> 1, (t - 9) >> 1, wp2);
+            // the pair's two weight loads after tiles kTW and kTW + 2 (inside the stream
+            // of kMT x kNT tiles: 8 of them for 64-row tiles)
+            if (pair && (t == kTW || t == kTW + 2)) dma_w((g + 2) >> 1, (t - kTW) >> 1, wp2);
         });
     };
 
@@ -580,8 +590,14 @@ namespace {
 struct TileShape {
     int bm, bn, per_cu;
     double step_us;  // one 64-wide group step of a workgroup at that occupancy (measured)
+    int max_m;       // offered up to this many rows (0: any)
 };
-constexpr TileShape kTileShapes[] = {{256, 256, 1, 2.0}, {128, 256, 1, 1.15}};
+// The 64-row tile: for M <= 64, where the 128-row tile would pad half its rows
+// (measured at 33-64 rows against the 128-row plans: gate 15360x3840 32.6-35.3 vs
+// 38.7-41.1 us, down 3840x15360 35.8-36.7 vs 40.5-42.2, the gate|up pair 42.2-46.9 vs
+// 52.8-56.6; slower from 128 rows on).  Its step time is fitted at one workgroup per
+// CU (two fit, but then each runs at half the rate).
+constexpr TileShape kTileShapes[] = {{256, 256, 1, 2.0, 0}, {128, 256, 1, 1.15, 0}, {64, 256, 1, 0.8, 64}};
 }  // namespace
 
 GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
@@ -591,6 +607,7 @@ GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
     const double bytes_per_us = 6.0e6;  // partial sums written and read back, largely through the caches
     double best = -1.0;
     for (const TileShape& ts : kTileShapes) {
+        if (ts.max_m > 0 && m > ts.max_m) continue;
         const int bm = ts.bm, bn = ts.bn;
         const long tiles = (long)((m + bm - 1) / bm) * ((l.n + bn - 1) / bn);
         for (int s = 1; s <= octets && s <= kMaxSplits; ++s) {
@@ -653,7 +670,11 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     // one instantiation per (output mode, tile shape)
 #define Q4_GEMM_LAUNCH(MODE, YPTR, STRIDE)                                                                       \
     do {                                                                                                         \
-        if (plan.bm == 256)                                                                                      \
+        if (plan.bm == 64)                                                                                       \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 64, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,   \
+                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, STRIDE, n_out,  \
+                               gelu_table);                                                                      \
+        else if (plan.bm == 256)                                                                                 \
             hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,  \
                                l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, STRIDE, n_out,  \
                                gelu_table);                                                                      \

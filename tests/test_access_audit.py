@@ -68,9 +68,16 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
     RB = BN // 16
     WM = BM // 2
     XP = BM * 8 // (64 * WAVES)   # x DMA parts per wave per group
-    XA = BM // 16 // WAVES        # bias A-operand DMA parts per wave per octet
+    XA = max(1, BM // 16 // WAVES)   # bias A-operand DMA parts per loading wave per octet
+    XA_WAVES = min(WAVES, BM // 16)  # waves that load them (BM = 64: waves 0-3)
     SW = RB // 8                  # waves loading a pair's scale words
-    assert RB == 2 * WAVES and XP >= 1 and XA >= 1
+    assert RB == 2 * WAVES and XP >= 1 and XA * XA_WAVES == BM // 16
+    # the DMAs issued from inside the product stream (after tile t of the wave's
+    # (BM / 32) x 4 tiles): the x loads after tiles 1, 3, ..., the pair's weights after
+    # tiles TW and TW + 2 -- every one must fall inside the stream or it is never issued
+    TILES = (BM // 2 // 16) * 4
+    TW = 9 if TILES >= 12 else 5
+    assert 2 * XP - 1 < TILES and TW + 2 < TILES, (BM, TILES, TW)
     KWP, KSP = RB * 64, RB * 16 // 2  # uint4 units of one weight slot
     XAA = BM // 16 * 64               # uint4 units of the bias A operands
     BIAS_SLOT = XAA + RB * 4 * 16 // 2  # uint4 units: A operands, then the octet's scale/bias words
@@ -124,7 +131,7 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
                 for p in (0, L["gp"] - 1):
                     chk_buf("gemm s", np.where(sv == OOB, OOB, sv + p * 128), 16, L["sb_bytes"], L["sb_bytes"])
             for o in sorted({0, octets - 1}):
-                for u in range(XA):
+                for u in (range(XA) if wave < XA_WAVES else ()):
                     m16 = XA * wave + u
                     assert m16 * 64 + 64 <= XAA
                     off = ((mt * (BM // 16) + m16) * octets + o) * 1024 + lane * 16
@@ -169,7 +176,7 @@ GEMM_SHAPES = [(33, 40, 384), (300, 256, 640), (257, 130, 320), (64, 512, 3840),
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
-@pytest.mark.parametrize("bm,bn", [(256, 256), (128, 256)])
+@pytest.mark.parametrize("bm,bn", [(256, 256), (128, 256), (64, 256)])
 def test_gemm_accesses(m, n, k, bm, bn):
     octets = (k // 64 + 7) // 8
     for s in sorted({1, 2, min(8, octets), octets}):
@@ -179,7 +186,7 @@ def test_gemm_accesses(m, n, k, bm, bn):
 
 # two-plane 8-bit handles: the tiled K' = 2K, x rows of K
 @pytest.mark.parametrize("m,n,k", [(2048, 15360, 3840), (300, 130, 1088), (33, 48, 576), (64, 96, 3840)])
-@pytest.mark.parametrize("bm,bn", [(256, 256), (128, 256)])
+@pytest.mark.parametrize("bm,bn", [(256, 256), (128, 256), (64, 256)])
 def test_gemm_accesses_two_plane(m, n, k, bm, bn):
     octets = (2 * k // 64 + 7) // 8
     for s in sorted({1, 2, min(8, octets), octets}):

@@ -43,7 +43,7 @@ def gemm_asm():
 
 def test_lds_dma_sgpr_hazards_covered(gemm_asm):
     kernels = list(_kernels(gemm_asm))
-    assert len(kernels) == 8  # bf16 / fp32 outputs, bf16 / fp32 GeGLU pairs; 256x256 and 128x256 tiles
+    assert len(kernels) == 12  # bf16 / fp32 outputs, bf16 / fp32 GeGLU pairs; 256, 128 and 64 x 256 tiles
     for name, lines in kernels:
         dmas = 0
         for i, line in enumerate(lines):
@@ -77,6 +77,9 @@ def test_no_spills_and_lds_budget(gemm_asm):
                          gemm_asm, re.S):
         if "gemm_kernelILi" in m.group(2) and "ELi128ELi128E" in m.group(2):
             assert int(m.group(1)) <= 80 * 1024 and int(m.group(3)) <= 256, m.group(2)
+        # the 64 x 256 tile: two workgroups per CU as well
+        if "gemm_kernelILi" in m.group(2) and "ELi64ELi256E" in m.group(2):
+            assert int(m.group(1)) <= 80 * 1024 and int(m.group(3)) <= 128, m.group(2)
 
 
 def _kernel_meta(asm: str):

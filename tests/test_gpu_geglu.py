@@ -123,10 +123,11 @@ def test_geglu_decode_gate_up(gpu_lib, m):
         obj.close()
 
 
-@pytest.mark.parametrize("m", [512, 2048])
+@pytest.mark.parametrize("m", [33, 64, 512, 2048])
 def test_geglu_prefill_gate_up(gpu_lib, m):
-    """Chunked prefill: the fused pair at M=512 and 2048, sampled rows against the oracle,
-    then the chain into down_proj (config 3's GeGLU -> down)."""
+    """Chunked prefill: the fused pair at M=512 and 2048 (and short prompts of 33 and 64
+    rows, the 64-row tile), sampled rows against the oracle, then the chain into
+    down_proj (config 3's GeGLU -> down)."""
     import torch
 
     gate, up = _pair(15360, 3840, 20260630 + 2004)
@@ -137,7 +138,7 @@ def test_geglu_prefill_gate_up(gpu_lib, m):
     h = pair.forward(xd)
     hf = pair.forward(xd, out_dtype=torch.float32)
     torch.cuda.synchronize()
-    rows = np.sort(np.random.default_rng(m).choice(m, 12, replace=False))
+    rows = np.sort(np.random.default_rng(m).choice(m, min(m, 12), replace=False))
     rt = torch.from_numpy(rows).cuda()
     g_exact, u_exact = _exact_gu(x, gate, up, rows)
     _check(h[rt], g_exact, u_exact, f"prefill M={m} bf16")

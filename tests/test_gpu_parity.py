@@ -449,6 +449,28 @@ def test_forward_decode_slabs_past_32_rows(gpu_lib, proj, m):
     lin.close()
 
 
+@pytest.mark.parametrize("m", [33, 64])
+def test_gemm_short_prompt_mlp(gpu_lib, gemm_from_32, m):
+    """Short prompts and prefill tails on the MLP shapes (the 64-row tile): gate and
+    down on sampled rows against the oracle (the gate|up pair: test_gpu_geglu.py)."""
+    import torch
+
+    rows = np.unique(np.concatenate([np.linspace(0, m - 1, 8).astype(np.int64), [m - 1]]))
+    rt = torch.from_numpy(rows).cuda()
+    for proj in ("gate_proj", "down_proj"):
+        n, k = PROJ[proj]
+        tri = A.make_weights(n, k, seed=20260630 + 1000 + sorted(PROJ).index(proj))
+        x = A.make_activations(m, k, seed=6500 + m, outliers=True)
+        lin = gpu_lib.QuantizedLinear(*dev_triple(*tri))
+        y = lin.forward(dev_x(x))
+        yf = lin.forward(dev_x(x), out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        lin.close()
+        want = C.qmm_f64(np.ascontiguousarray(x[rows]), *tri)
+        assert_close(y[rt], want, f"{proj} m={m} bf16")
+        assert assert_close(yf[rt], want, f"{proj} m={m} f32") < 5e-4
+
+
 def test_gemm_prefill_chain_m2048_geglu(gpu_lib):
     """Chunked-prefill chain at M=2048: gate and up, GeGLU on the host (identical bf16
     bytes to both sides), then down_proj; sampled rows against the oracle."""

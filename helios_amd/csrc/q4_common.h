@@ -3,10 +3,11 @@
 // Tiled weight layout (built once per projection by q4_layout.hip, resident in HBM):
 //
 //   A row block is 16 output rows (the N side of one 16x16x32 MFMA tile); a group
-//   pair is 128 K values (two 64-wide quantization groups).  For row block rb and
-//   group pair gp the packed nibbles form one 1 KiB tile, 16 bytes per lane:
+//   pair is 128 K values (two 64-wide quantization groups).  Row block rb and group
+//   pair gp own one 1152-byte record (records [NB][GP]): a 1 KiB tile of the packed
+//   nibbles, 16 bytes per lane, then the 16 rows' scale/bias words (below):
 //
-//     tiles [NB][GP][64 lanes] of uint4
+//     tile of record (rb, gp): 64 lanes of uint4
 //     lane l -> row n = 16*rb + (l % 16), k-quarter kq = l / 16
 //     .x = word(g=2gp,   half 0)   .y = word(g=2gp,   half 1)
 //     .z = word(g=2gp+1, half 0)   .w = word(g=2gp+1, half 1)
@@ -22,8 +23,9 @@
 //   The values 1 + q/16 are exact in bf16, and the MFMA products with bf16 x are
 //   exact in fp32, so the only rounding is fp32 accumulation.
 //
-//   Scales and biases sit beside the tiles, one uint2 per (rb, gp, row):
-//     sb [NB][GP][16] of uint2, .x = s | b << 16 for group 2gp, .y for group 2gp+1
+//   Scales and biases follow their tile in the record, one uint2 per row:
+//     16 uint2, .x = s | b << 16 for group 2gp, .y for group 2gp+1
+//   (a row block's run of records is then one contiguous stream of weight bytes)
 //
 //   Padding: rows >= N and groups >= K/64 hold q = 0, s = 0, b = 0, so they add 0.
 //

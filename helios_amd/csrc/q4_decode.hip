@@ -3,7 +3,8 @@
 // 16-row slabs (one launch; slab = blockIdx.y).
 //
 // Bandwidth-bound: every weight byte is read once from HBM with 16-byte coalesced
-// loads (one 1 KiB tile per wave-load), scales/biases once per group, nibbles are
+// loads (one 1 KiB tile per wave-load, its scale/bias words right after it in the
+// same record), scales/biases once per group, nibbles are
 // expanded in registers (two VALU ops per bf16 pair) and the products run on the
 // matrix cores: per group, two v_mfma_f32_16x16x32_bf16 give -X_g (x times a
 // constant -1 operand, already in the accumulator layout) and two more give
@@ -90,8 +91,8 @@ __global__ __launch_bounds__(1024) void decode_kernel(
         const int left = cnt - base;
         // this pass's tiles and scales as bounded buffers: pairs i >= left read as zero
         const long first = (long)rb * gpairs + gpb;
-        const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * 64, (uint32_t)left * 1024u);
-        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * 16, (uint32_t)left * 128u);
+        const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * kRecU4, (uint32_t)left * kRecBytes);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * kRecU2, sb_span(left));
         // element offset of this lane's x operand at pair i, group 0, half 0 (x in LDS)
         const int xel = arow * k + 8 * kq + gpb * 128;
         const int kleft = k - gpb * 128;
@@ -100,8 +101,8 @@ __global__ __launch_bounds__(1024) void decode_kernel(
         uint2 sv[GPW];
 #pragma unroll
         for (int i = 0; i < GPW; ++i) {
-            wv[i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * 1024));
-            sv[i] = buffer_load8<kNonTemporal>(srs, (uint32_t)(col * 8 + i * 128));
+            wv[i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * kRecBytes));
+            sv[i] = buffer_load8<kNonTemporal>(srs, (uint32_t)(col * 8 + i * kRecBytes));
         }
         if (!synced) {
             __syncthreads();  // x is in LDS
@@ -239,11 +240,12 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
         const int left = cnt - pass * GPW;
         const int n_in = !live ? 0 : left < GPW ? left : GPW;
         const long first = (long)rb * gpairs + gpb;
-        const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * 64, (uint32_t)n_in * 1024u);
-        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * 16, (uint32_t)n_in * 128u);
+        const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * kRecU4, (uint32_t)n_in * kRecBytes);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * kRecU2, sb_span(n_in));
 #pragma unroll
-        for (int i = 0; i < GPW; ++i) wv[i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * 1024));
-        sv = buffer_load8<kNonTemporal>(srs, (uint32_t)(lane * 8));  // the chunk's 512 contiguous bytes
+        for (int i = 0; i < GPW; ++i) wv[i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * kRecBytes));
+        // lane (col, kq): pair kq's word for row col
+        sv = buffer_load8<kNonTemporal>(srs, (uint32_t)((lane >> 4) * kRecBytes + (lane & 15) * 8));
     };
 
     // x -> LDS (loads issued before any weight load), zero padding after each row,
@@ -410,11 +412,12 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(
         const int left = gpairs - gpb;
         const int n_in = !live ? 0 : left < GPW ? left : GPW;
         const long first = (long)rb * gpairs + gpb;
-        const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * 64, (uint32_t)n_in * 1024u);
-        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * 16, (uint32_t)n_in * 128u);
+        const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * kRecU4, (uint32_t)n_in * kRecBytes);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * kRecU2, sb_span(n_in));
 #pragma unroll
-        for (int i = 0; i < GPW; ++i) w[b][i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * 1024));
-        sv[b] = buffer_load8<kNonTemporal>(srs, (uint32_t)(lane * 8));  // the chunk's 512 contiguous bytes
+        for (int i = 0; i < GPW; ++i) w[b][i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * kRecBytes));
+        // lane (col, kq): pair kq's word for row col
+        sv[b] = buffer_load8<kNonTemporal>(srs, (uint32_t)((lane >> 4) * kRecBytes + (lane & 15) * 8));
     };
 
     // x -> LDS with zero padding after each row, and -X_g into the table; the first

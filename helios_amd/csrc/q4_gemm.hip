@@ -128,8 +128,8 @@ template <int OUT, int BM, int BN>
 __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ tiles, const uint2* __restrict__ sb,
                                                    const uint16_t* __restrict__ x, const uint4* __restrict__ xaug,
                                                    void* __restrict__ y, int m_rows, int n_rows, int kx, int groups,
-                                                   int gpairs, int mtiles, int ntiles, int octets, uint32_t tile_bytes,
-                                                   uint32_t sb_bytes, int g_split, long split_stride, int n_out,
+                                                   int gpairs, int mtiles, int ntiles, int octets, uint32_t rec_bytes,
+                                                   int g_split, long split_stride, int n_out,
                                                    const uint16_t* __restrict__ gelu_table) {
     // BM = 256: 2 x 4 waves of 128 x 64; BM = 128: 2 x 4 waves of 64 x 64 (more
     // workgroups for small M without splitting K); BN = 128: 2 x 2 waves
@@ -181,14 +181,14 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     // sized to the buffers (<= 2^31 bytes, checked by the host) so that kOutOfRange is
     // outside every range and reads as zero
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)kx * 2u);
-    const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles, tile_bytes);
-    const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, sb_bytes);
+    const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles, rec_bytes);
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, rec_bytes - kRecSbBytes);
     const __amdgpu_buffer_rsrc_t ars = make_rsrc(xaug, (uint32_t)(mtiles * (BM / 16) * octets) * 1024u);
 
     // DMA issue.  Per lane, the offsets are fixed for the whole K loop (rows past M and
     // row blocks past N at kOutOfRange) and computed once here; the step moves them by
-    // a scalar offset (group x 128 bytes of x, pair x 1 KiB of tiles, pair x 128 bytes
-    // of scale words), which stays inside the buffer for every in-range lane.  Past the
+    // a scalar offset (group x 128 bytes of x, pair x one record of tiled and of scale
+    // words), which stays inside the buffer for every in-range lane.  Past the
     // last group or pair the resource is swapped for an empty one: zeros, into slots
     // nobody reads again.  Branch-free, so they can sit anywhere in the product stream.
     const __amdgpu_buffer_rsrc_t zrs = make_rsrc(x, 0u);
@@ -207,12 +207,12 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int rb = rbw + 2 * wave + t;
-        wv[t] = rb < nblocks ? ((uint32_t)rb * (uint32_t)gpairs * 64u + (uint32_t)lane) * 16u : kOutOfRange;
+        wv[t] = rb < nblocks ? (uint32_t)rb * (uint32_t)gpairs * kRecBytes + (uint32_t)lane * 16u : kOutOfRange;
     }
     uint32_t sv;  // scale words of a pair (waves w < kSWaves): row block 8w + l/8, chunk l%8 of its 128 bytes
     {
         const int rb = rbw + 8 * wave + (lane >> 3);
-        sv = rb < nblocks ? (uint32_t)rb * (uint32_t)gpairs * 128u + (uint32_t)(lane & 7) * 16u : kOutOfRange;
+        sv = rb < nblocks ? (uint32_t)rb * (uint32_t)gpairs * kRecBytes + (uint32_t)(lane & 7) * 16u : kOutOfRange;
     }
     // x rows are kx long: group g >= kx / 64 (the low plane of a two-plane handle) reads
     // group g - kx / 64 of x (a scalar select)
@@ -222,10 +222,10 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
               (uint32_t)(g >= gx ? g - gx : g) * 128u);
     };
     auto dma_w = [&](int p, int part, uint4* wdst) {
-        dma16(p < p_end ? trs : zrs, wdst + (2 * wave + part) * 64, wv[part], (uint32_t)p * 1024u);
+        dma16(p < p_end ? trs : zrs, wdst + (2 * wave + part) * 64, wv[part], (uint32_t)p * kRecBytes);
     };
     auto dma_s = [&](int p, uint4* wdst) {
-        dma16(p < p_end ? srs : zrs, wdst + kWPair + 64 * wave, sv, (uint32_t)p * 128u);
+        dma16(p < p_end ? srs : zrs, wdst + kWPair + 64 * wave, sv, (uint32_t)p * kRecBytes);
     };
     auto dma_xa_part = [&](int o, int u) {
         const int m16 = kXaParts * wave + u;
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     };
     // bias operands of octet o: the A side (kXaParts 16-byte loads) and the scale/bias words
     // of its four group pairs for row blocks 2w, 2w+1 (lane l: row block 2w + l/32,
-    // 16-byte chunk l%32 of the row block's 512 contiguous bytes)
+    // pair 4o + (l%32)/8, 16-byte chunk l%8 of that record's 128 bytes of words)
     auto dma_xa = [&](int o) {
         int ln = threadIdx.x & 63;
         asm volatile("" : "+v"(ln));
@@ -244,7 +244,8 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         const int rb = rbw + 2 * wave + (ln >> 5);
         const int chunk = ln & 31;
         const bool ok = (rb < nblocks) & (4 * o + (chunk >> 3) < gpairs);
-        const uint32_t raw = ((uint32_t)rb * (uint32_t)gpairs + 4u * (uint32_t)o) * 128u + (uint32_t)chunk * 16u;
+        const uint32_t raw = ((uint32_t)rb * (uint32_t)gpairs + 4u * (uint32_t)o + (uint32_t)(chunk >> 3)) * kRecBytes +
+                             (uint32_t)(chunk & 7) * 16u;
         dma16(srs, g_xab + (kXaA + wave * 64), ok ? raw : kOutOfRange);
     };
 
@@ -655,7 +656,7 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     const int ntiles = (l.n + plan.bn - 1) / plan.bn;
     uint4* xaug = static_cast<uint4*>(workspace);
     float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.xaug_bytes);
-    if (l.tile_bytes() > kMaxBufferBytes || l.sb_bytes() > kMaxBufferBytes ||
+    if (l.rec_bytes() > kMaxBufferBytes ||
         (size_t)m * l.kx * 2 > kMaxBufferBytes || plan.xaug_bytes > kMaxBufferBytes)
         return hipErrorInvalidValue;
     {
@@ -665,22 +666,22 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
         if (e != hipSuccess) return e;
     }
     const dim3 grid((unsigned)(mtiles * ntiles), (unsigned)plan.splits), block(2 * plan.bn);
-    const uint32_t tb = (uint32_t)l.tile_bytes(), sbb = (uint32_t)l.sb_bytes();
+    const uint32_t rec_bytes = (uint32_t)l.rec_bytes();
     const long elems = (long)m * l.n;
     // one instantiation per (output mode, tile shape)
 #define Q4_GEMM_LAUNCH(MODE, YPTR, STRIDE)                                                                       \
     do {                                                                                                         \
         if (plan.bm == 64)                                                                                       \
             hipLaunchKernelGGL((gemm_kernel<MODE, 64, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,   \
-                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, STRIDE, n_out,  \
+                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split, STRIDE, n_out, \
                                gelu_table);                                                                      \
         else if (plan.bm == 256)                                                                                 \
             hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,  \
-                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, STRIDE, n_out,  \
+                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split, STRIDE, n_out, \
                                gelu_table);                                                                      \
         else                                                                                                     \
             hipLaunchKernelGGL((gemm_kernel<MODE, 128, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,  \
-                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, tb, sbb, plan.g_split, STRIDE, n_out,  \
+                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split, STRIDE, n_out, \
                                gelu_table);                                                                      \
     } while (0)
     if (plan.splits > 1) {

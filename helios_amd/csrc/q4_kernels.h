@@ -7,6 +7,24 @@
 
 namespace q4 {
 
+// Weight records: one per (16-row block, group pair), [row block][pair], 1152 bytes
+// each: the 1 KiB tile of tiled words (uint4 per lane) and then the block's 16 scale/
+// bias words for the pair (uint2 per row), so a kernel streaming a row block reads one
+// contiguous run.  Kernels take the record array as uint4 tiles (record t's words at
+// t * kRecU4 + lane) and as uint2 sb starting kRecSbBytes into it (record t's word for
+// row r at t * kRecU2 + r).
+constexpr int kRecBytes = 1152;
+constexpr int kRecSbBytes = 1024;
+constexpr int kRecU4 = kRecBytes / 16;
+constexpr int kRecU2 = kRecBytes / 8;
+
+// Bytes from the first of n consecutive records' scale/bias words to the end of the
+// last record: the size of a buffer resource over their words (0 for none, so that
+// every offset reads as zero).
+__host__ __device__ inline uint32_t sb_span(int n) {
+    return n > 0 ? (uint32_t)n * (uint32_t)kRecBytes - (uint32_t)kRecSbBytes : 0u;
+}
+
 struct Layout {
     int n = 0;   // output features
     int k = 0;   // input features of the tiled weight (2K for two-plane 8-bit handles)
@@ -15,8 +33,7 @@ struct Layout {
     int g = 0;   // groups per row (k / 64)
     int nb = 0;  // 16-row blocks
     int gp = 0;  // group pairs (ceil(g / 2))
-    size_t tile_bytes() const { return (size_t)nb * gp * 64 * 16; }
-    size_t sb_bytes() const { return (size_t)nb * gp * 16 * 8; }
+    size_t rec_bytes() const { return (size_t)nb * gp * kRecBytes; }
 };
 
 inline Layout make_layout(int n, int k) {

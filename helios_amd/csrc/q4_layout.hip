@@ -1,6 +1,7 @@
 // Weight-layout kernels: MLX affine layout -> tiled MFMA layout (one projection, or a
-// gate|up pair interleaved 8 rows at a time), and the bit-exact fp32 dequantize of
-// the tiled layout (the check that the tiles hold every bit).
+// gate|up pair interleaved 8 rows at a time) as records of tiled words and scale/bias
+// words (q4_kernels.h), and the bit-exact fp32 dequantize of the records (the check
+// that they hold every bit).
 #include "q4_common.h"
 #include "q4_kernels.h"
 
@@ -69,7 +70,7 @@ __global__ void repack_kernel(const uint32_t* __restrict__ w_a, const uint16_t* 
             out[2 * gi + h] = tile_word(u);
         }
     }
-    tiles[tid] = make_uint4(out[0], out[1], out[2], out[3]);
+    tiles[t * kRecU4 + lane] = make_uint4(out[0], out[1], out[2], out[3]);
     if (kq == 0) {
         uint32_t v[2];
 #pragma unroll
@@ -81,7 +82,7 @@ __global__ void repack_kernel(const uint32_t* __restrict__ w_a, const uint16_t* 
                 v[gi] = (uint32_t)s[idx] | ((uint32_t)b[idx] << 16);
             }
         }
-        sb[t * 16 + (lane & 15)] = make_uint2(v[0], v[1]);
+        sb[t * kRecU2 + (lane & 15)] = make_uint2(v[0], v[1]);
     }
 }
 
@@ -107,8 +108,8 @@ __global__ void dequantize_kernel(const uint4* __restrict__ tiles, const uint2* 
         row = (int)(rb * 16 + c);
         if (row >= n_rows) return;
     }
-    const uint4 wv = tiles[tid];
-    const uint2 sv = sb[t * 16 + (lane & 15)];
+    const uint4 wv = tiles[t * kRecU4 + lane];
+    const uint2 sv = sb[t * kRecU2 + (lane & 15)];
     const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
@@ -148,8 +149,8 @@ __global__ void embed_kernel(const uint4* __restrict__ tiles, const uint2* __res
     const long rb = valid ? id >> 4 : 0;
     const int col = valid ? id & 15 : 0;
     const long tile = rb * gpairs + gp;
-    const uint4 wv = valid ? tiles[tile * 64 + col + 16 * kq] : make_uint4(0, 0, 0, 0);
-    const uint2 sv = valid ? sb[tile * 16 + col] : make_uint2(0, 0);
+    const uint4 wv = valid ? tiles[tile * kRecU4 + col + 16 * kq] : make_uint4(0, 0, 0, 0);
+    const uint2 sv = valid ? sb[tile * kRecU2 + col] : make_uint2(0, 0);
     const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
@@ -241,8 +242,8 @@ __global__ void repack8_kernel(const uint32_t* __restrict__ w_a, const uint16_t*
             sbw[gi] = hi ? (sc16 | (bi << 16)) : sc;
         }
     }
-    tiles[tid] = make_uint4(out[0], out[1], out[2], out[3]);
-    if (kq == 0) sb[t * 16 + (lane & 15)] = make_uint2(sbw[0], sbw[1]);
+    tiles[t * kRecU4 + lane] = make_uint4(out[0], out[1], out[2], out[3]);
+    if (kq == 0) sb[t * kRecU2 + (lane & 15)] = make_uint2(sbw[0], sbw[1]);
 }
 
 // fp32 s*q + b of 8 codes of tiled row lane (col) for original group g and half h,
@@ -252,12 +253,12 @@ __device__ __forceinline__ void two_plane_values(const uint4* __restrict__ tiles
                                                  float v[8]) {
     const int glo = groups8 + g;
     const long thi = rb * gpairs + (g >> 1), tlo = rb * gpairs + (glo >> 1);
-    const uint4 whi = tiles[thi * 64 + col + 16 * kq];
-    const uint4 wlo = tiles[tlo * 64 + col + 16 * kq];
+    const uint4 whi = tiles[thi * kRecU4 + col + 16 * kq];
+    const uint4 wlo = tiles[tlo * kRecU4 + col + 16 * kq];
     const uint32_t ahi[4] = {whi.x, whi.y, whi.z, whi.w};
     const uint32_t alo[4] = {wlo.x, wlo.y, wlo.z, wlo.w};
     const uint32_t uhi = ahi[2 * (g & 1) + h], ulo = alo[2 * (glo & 1) + h];
-    const uint2 shi = sb[thi * 16 + col], slo = sb[tlo * 16 + col];
+    const uint2 shi = sb[thi * kRecU2 + col], slo = sb[tlo * kRecU2 + col];
     const uint32_t sbh = (g & 1) ? shi.y : shi.x, sbl = (glo & 1) ? slo.y : slo.x;
     const float sc = bf16_lo(sbl);  // s (the low plane's scale)
     const float bi = bf16_hi(sbh);  // b (the high plane's bias)

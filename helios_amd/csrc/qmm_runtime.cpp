@@ -206,8 +206,8 @@ struct Gemma4QLinear {
     int pair_rows = 0;  // F for a gate|up pair (tiled as q4::pair_layout), else 0
     const uint16_t* gelu_table = nullptr;  // the device's gelu table (pairs only)
     int device = 0;
-    uint4* tiles = nullptr;
-    uint2* sb = nullptr;
+    uint4* tiles = nullptr;  // the weight records (one allocation)
+    uint2* sb = nullptr;     // their scale/bias words: kRecSbBytes into the same allocation
 };
 
 struct Gemma4QLora {
@@ -243,7 +243,7 @@ Gemma4Status check_desc(const Gemma4QLinearDesc* desc, bool pair, const char* fn
     if (desc->out_features > (1u << 29) || desc->in_features > (1u << 23))
         return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, std::string(fn) + ": shape exceeds the supported range");
     const q4::Layout l = handle_layout(*desc, pair);
-    if (l.tile_bytes() > q4::kMaxBufferBytes || l.sb_bytes() > q4::kMaxBufferBytes)
+    if (l.rec_bytes() > q4::kMaxBufferBytes)
         return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
                     std::string(fn) + ": weights exceed 2 GiB per projection (split it along out_features)");
     return GEMMA4_OK;
@@ -251,7 +251,6 @@ Gemma4Status check_desc(const Gemma4QLinearDesc* desc, bool pair, const char* fn
 
 void release(Gemma4QLinear* h) {
     if (h->tiles) (void)hipFree(h->tiles);
-    if (h->sb) (void)hipFree(h->sb);
     h->tiles = nullptr;
     h->sb = nullptr;
     h->magic = 0;
@@ -287,8 +286,8 @@ Gemma4Status build_handle(const Gemma4QLinearDesc* desc, const Triple& main, con
             return hip_fail("gemma4_qgeglu: gelu table", e);
         }
     }
-    e = hipMalloc(&h->tiles, h->layout.tile_bytes());
-    if (e == hipSuccess) e = hipMalloc(&h->sb, h->layout.sb_bytes());
+    e = hipMalloc(&h->tiles, h->layout.rec_bytes());
+    if (e == hipSuccess) h->sb = reinterpret_cast<uint2*>(reinterpret_cast<char*>(h->tiles) + q4::kRecSbBytes);
     if (e != hipSuccess) {
         release(h);
         delete h;
@@ -570,7 +569,7 @@ Gemma4Status gemma4_qlinear_info(const Gemma4QLinear* linear, Gemma4QLinearInfo*
         out->in_features = linear->desc.in_features;
         out->bits = linear->desc.bits;
         out->group_size = linear->desc.group_size;
-        out->device_bytes = linear->layout.tile_bytes() + linear->layout.sb_bytes();
+        out->device_bytes = linear->layout.rec_bytes();
         out->device = linear->device;
         out->flags = linear->pair_rows ? GEMMA4_QLINEAR_GEGLU_PAIR : 0u;
         return ok();

@@ -31,11 +31,32 @@ def chk_buf(name, off, size, num_records, real_bytes):
     assert not bad.any(), (name, off[bad][:5], num_records)
 
 
+REC, REC_SB = 1152, 1024  # weight record bytes; its scale/bias words start 1 KiB in
+
+
 def layout(n, k):
     g = k // 64
     nb = (n + 15) // 16
     gp = (g + 1) // 2
-    return dict(n=n, k=k, g=g, nb=nb, gp=gp, tile_bytes=nb * gp * 1024, sb_bytes=nb * gp * 128)
+    # the kernels see the records as tiles (from the start) and as sb (REC_SB bytes in)
+    return dict(n=n, k=k, g=g, nb=nb, gp=gp, rec_bytes=nb * gp * REC, sb_bytes=nb * gp * REC - REC_SB)
+
+
+def sb_span(n):
+    n = np.asarray(n, np.int64)
+    return np.where(n > 0, n * REC - REC_SB, 0)
+
+
+def in_tile_part(off, size):
+    """Offsets from the record array's start that stay inside one record's tiled words."""
+    off = np.asarray(off, np.int64)
+    return ((off % REC) + size <= REC_SB).all()
+
+
+def in_sb_part(off, size):
+    """Offsets from the scale words' start (REC_SB in) that stay inside one record's words."""
+    off = np.asarray(off, np.int64)
+    return ((off % REC) + size <= REC - REC_SB).all()
 
 
 # ------------------------------------------------------------------------- GEMM
@@ -122,14 +143,18 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
                     chk_buf("gemm x", np.where(xv == OOB, OOB, xv + gm * 128), 16, xbytes, xbytes)
             for part in range(2):
                 rb = rbw + 2 * wave + part
-                wv = np.where(rb < nblocks, (rb * L["gp"] * 64 + lane) * 16, OOB)
+                wv = np.where(rb < nblocks, rb * L["gp"] * REC + lane * 16, OOB)
                 for p in (0, L["gp"] - 1):
-                    chk_buf("gemm w", np.where(wv == OOB, OOB, wv + p * 1024), 16, L["tile_bytes"], L["tile_bytes"])
+                    off = np.where(wv == OOB, OOB, wv + p * REC)
+                    chk_buf("gemm w", off, 16, L["rec_bytes"], L["rec_bytes"])
+                    assert in_tile_part(off[off != OOB], 16)
             if wave < SW:
                 rb = rbw + 8 * wave + (lane >> 3)
-                sv = np.where(rb < nblocks, rb * L["gp"] * 128 + (lane & 7) * 16, OOB)
+                sv = np.where(rb < nblocks, rb * L["gp"] * REC + (lane & 7) * 16, OOB)
                 for p in (0, L["gp"] - 1):
-                    chk_buf("gemm s", np.where(sv == OOB, OOB, sv + p * 128), 16, L["sb_bytes"], L["sb_bytes"])
+                    off = np.where(sv == OOB, OOB, sv + p * REC)
+                    chk_buf("gemm s", off, 16, L["sb_bytes"], L["sb_bytes"])
+                    assert in_sb_part(off[off != OOB], 16)
             for o in sorted({0, octets - 1}):
                 for u in (range(XA) if wave < XA_WAVES else ()):
                     m16 = XA * wave + u
@@ -139,8 +164,9 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
                 rb = rbw + 2 * wave + (lane >> 5)
                 chunk = lane & 31
                 ok = (rb < nblocks) & (4 * o + (chunk >> 3) < L["gp"])
-                raw = (rb * L["gp"] + 4 * o) * 128 + chunk * 16
+                raw = (rb * L["gp"] + 4 * o + (chunk >> 3)) * REC + (chunk & 7) * 16
                 chk_buf("gemm bias words", np.where(ok, raw, OOB), 16, L["sb_bytes"], L["sb_bytes"])
+                assert in_sb_part(raw[ok], 16)
                 assert XAA + wave * 64 + 63 < BIAS_SLOT  # the scale/bias part of the bias slot
             # LDS operand reads of the 16x16x32 product stream
             kq = lane >> 4
@@ -197,19 +223,31 @@ def test_gemm_accesses_two_plane(m, n, k, bm, bn):
 
 # ----------------------------------------------------------------------- decode
 
-def _chunk_reads(first, n_in, tile_bytes, sb_bytes):
-    """A chunk's weight loads: lane offsets lane*16 + i*1024 (i < 4) against a resource
-    of n_in pairs starting at pair `first`, and the scale words (one 8-byte load per
-    lane over the chunk's 512 bytes).  Vectorized over chunks: the largest in-range
-    offset of each chunk must end inside the real buffer."""
+def _chunk_reads(first, n_in, rec_bytes, n_max=4):
+    """A chunk's weight loads against resources over n_in records starting at record
+    `first`: tiled words at lane*16 + i*REC (i < n_max) over n_in*REC bytes, and the
+    scale words of pair i, row r at i*REC + 8r over sb_span(n_in) bytes from the first
+    record's words.  Vectorized over chunks: pairs i < n_in must read inside their own
+    record (and the buffer), pairs i >= n_in must fall outside the resource (zeros)."""
     first = np.asarray(first, np.int64)
     n_in = np.asarray(n_in, np.int64)
-    assert (n_in >= 0).all() and (n_in <= 4).all()
+    assert (n_in >= 0).all()
     live = n_in > 0
-    # largest lane offset below n_in * 1024 is (n_in - 1) * 1024 + 63 * 16; it ends 16 bytes later
-    assert ((first * 1024 + n_in * 1024)[live] <= tile_bytes).all()
-    assert ((first * 128 + n_in * 128)[live] <= sb_bytes).all()
-    assert (n_in * 1024 <= 2 ** 31).all()
+    # resources end inside the records array
+    assert ((first * REC + n_in * REC)[live] <= rec_bytes).all()
+    assert ((first * REC + REC_SB + sb_span(n_in))[live] <= rec_bytes).all()
+    assert (n_in * REC <= 2 ** 31).all()
+    lane = np.arange(64)
+    for i in range(n_max):
+        toff = lane * 16 + i * REC
+        soff = (lane & 15) * 8 + i * REC
+        inside = i < n_in
+        # in range exactly for the live pairs, and then within the tile / words part
+        assert ((toff.max() + 16 <= n_in * REC) == inside).all() or not live.any()
+        assert ((toff.min() >= n_in * REC) | inside).all()
+        assert ((soff.max() + 8 <= sb_span(n_in)) == inside).all() or not live.any()
+        assert ((soff.min() >= sb_span(n_in)) | inside).all()
+        assert in_tile_part(toff, 16) and in_sb_part(soff, 8)
 
 
 def audit_decode_stream(m_total, n, k, cus=256, kx=None):
@@ -253,7 +291,7 @@ def audit_decode_stream(m_total, n, k, cus=256, kx=None):
         assert (rb < L["nb"]).all()
         pas = C % passes
         n_in = np.where(live, np.minimum(cnt - pas * GPW, GPW), 0)
-        _chunk_reads(rb * L["gp"] + gp0 + pas * GPW, n_in, L["tile_bytes"], L["sb_bytes"])
+        _chunk_reads(rb * L["gp"] + gp0 + pas * GPW, n_in, L["rec_bytes"])
         if wave == 0:
             np.add.at(seen, rb[live & (pas == passes - 1)], 1)
     assert (seen == 1).all()
@@ -311,7 +349,7 @@ def audit_decode_rows(m, n, k, cus=256, GPW=4, NBUF=2, waves=4, per_cu=2):
     assert (rb < nb).all()
     gpb = (C % passes) * GPW
     n_in = np.where(live, np.minimum(GPW, gp - gpb), 0)
-    _chunk_reads(rb * gp + gpb, n_in, L["tile_bytes"], L["sb_bytes"])
+    _chunk_reads(rb * gp + gpb, n_in, L["rec_bytes"])
     seen = np.zeros(nb, np.int64)
     np.add.at(seen, rb[live & (C % passes == passes - 1)], 1)
     assert (seen == 1).all()

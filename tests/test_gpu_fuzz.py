@@ -1,6 +1,6 @@
 """Seeded random shapes through the C ABI on the GPU, against the oracle.
 
-Each case draws N (or F for a gate|up pair), K (a multiple of 64), M from one of eight
+Each projection case draws N (or F for a gate|up pair), K (a multiple of 64), M from one of eight
 row ranges (0, 1, 2, 3-4, 5-16, 17-31, 32-64, 65-300), 4 or 8 bits, a bf16 or fp32
 output, and the automatic path choice or the GEMM pinned from 32 rows.  Between them
 the cases reach every decode variant (row, per-row-block, streaming, global-x; 16-row
@@ -8,7 +8,9 @@ slabs), the GEMM's 256-, 128- and 64-row tiles with and without a K split, and t
 ragged edges (N not a multiple of 16, K not a multiple of 128, a last row block or
 group pair partly empty).  Sampled rows are checked with the bars of
 test_gpu_parity.py (bf16 max |err| <= 1e-2 RMS + ulp/2, fp32 <= 2e-3 RMS) and, for
-pairs, test_gpu_geglu.py.
+pairs, test_gpu_geglu.py.  LoRA (rank 1-96) and the greedy head (M 1-16, softcap 0
+or 30) get random shapes of their own, with the bars of test_gpu_lora.py and
+test_gpu_greedy.py.
 """
 
 import numpy as np
@@ -17,7 +19,7 @@ import pytest
 from oracle import affine as A
 from oracle import c_oracle as C
 from test_gpu_geglu import _check as check_geglu
-from test_gpu_parity import assert_close, dev_triple, dev_x
+from test_gpu_parity import BF16_REL, F32_REL, assert_close, dev_triple, dev_x, host_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -112,3 +114,99 @@ def test_random_shapes(gpu_lib, case):
         check_geglu(y[rt], g, u, what)
     else:
         assert_close(y[rt], C.qmm_f64(xs, *tri, bits=bits), what)
+
+
+def _lora_cases(count=12, seed=20261204):
+    """LoRA on random shapes: rank 1-96 (the fused one-launch path up to M = 4 and
+    rank 64, the two-kernel path otherwise), M 1-200."""
+    rng = np.random.default_rng(seed)
+    ranges = [(1, 1), (2, 2), (3, 4), (5, 16), (17, 64), (65, 200)]
+    cases = []
+    for i in range(count):
+        lo, hi = ranges[i % len(ranges)]
+        k = 64 * int(rng.integers(1, 65))
+        cases.append(dict(i=200 + i, n=int(rng.integers(1, 4001)), k=k, m=int(rng.integers(lo, hi + 1)),
+                          r=int(rng.integers(1, 97)), f32=bool(rng.random() < 0.4),
+                          scale=float(rng.choice([0.5, 2.0]))))
+    return cases
+
+
+@pytest.mark.parametrize("case", _lora_cases(), ids=lambda c: f"{c['i']}-N{c['n']}-K{c['k']}-M{c['m']}-r{c['r']}"
+                         f"{'-f32' if c['f32'] else ''}")
+def test_random_lora(gpu_lib, case):
+    import torch
+
+    from test_gpu_lora import check_bf16_two_roundings
+
+    n, k, m, r = case["n"], case["k"], case["m"], case["r"]
+    what = f"LoRA case {case['i']}: N={n} K={k} M={m} r={r} f32={case['f32']}"
+    print(what, flush=True)
+    seed = 88_000 + 10 * case["i"]
+    tri = _triple(n, k, 4, seed)
+    rng = np.random.default_rng(seed + 1)
+    a = (rng.standard_normal((r, k)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal((n, r)) * 0.02).astype(np.float32)
+    x = A.make_activations(m, k, seed=seed + 2, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*tri))
+    lora = gpu_lib.LoraAdapter(a, b, case["scale"])
+    dt = torch.float32 if case["f32"] else torch.bfloat16
+    y = lin.forward_lora(dev_x(x), lora, out_dtype=dt)
+    torch.cuda.synchronize()
+    lin.close()
+    lora.close()
+    rows = _rows(m, seed)
+    xs = np.ascontiguousarray(x[rows])
+    base = C.qmm_f64(xs, *tri).astype(np.float32)
+    want = A.lora_ops(xs, a, b, case["scale"], base, bf16=not case["f32"]).astype(np.float64)
+    got = host_bits(y[torch.from_numpy(rows).cuda()])
+    if case["f32"]:
+        ok, worst = A.check_f32_output(got, want, F32_REL)
+    else:
+        ok, worst = check_bf16_two_roundings(got, want)
+    assert ok, f"{what}: worst error / RMS = {worst:.3e}"
+
+
+def _greedy_cases(count=10, seed=20261205):
+    """The greedy head (softcap + first argmax) on random shapes, M 1-16."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        k = 64 * int(rng.integers(1, 65))
+        m = int(rng.integers(1, 17))
+        n = int(rng.integers(2, min(30000, 200_000_000 // (m * k)) + 1))
+        cases.append(dict(i=300 + i, n=n, k=k, m=m, cap=float(rng.choice([0.0, 30.0])),
+                          f32=bool(rng.random() < 0.4)))
+    return cases
+
+
+@pytest.mark.parametrize("case", _greedy_cases(), ids=lambda c: f"{c['i']}-N{c['n']}-K{c['k']}-M{c['m']}"
+                         f"-cap{int(c['cap'])}{'-f32' if c['f32'] else ''}")
+def test_random_greedy(gpu_lib, case):
+    import torch
+
+    from test_gpu_greedy import _check_token
+
+    n, k, m, cap = case["n"], case["k"], case["m"], case["cap"]
+    what = f"greedy case {case['i']}: N={n} K={k} M={m} cap={cap} f32={case['f32']}"
+    print(what, flush=True)
+    seed = 99_000 + 10 * case["i"]
+    tri = _triple(n, k, 4, seed)
+    x = A.make_activations(m, k, seed=seed + 1, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*tri))
+    dt = torch.float32 if case["f32"] else torch.bfloat16
+    tok, val, logits = lin.forward_greedy(dev_x(x), softcap=cap, out_dtype=dt, return_logits=True)
+    torch.cuda.synchronize()
+    lin.close()
+    sc = A.softcap_ops(C.qmm_f64(x, *tri).astype(np.float32), cap, bf16=not case["f32"])
+    lg = host_bits(logits)
+    if case["f32"]:
+        ok, worst = A.check_f32_output(lg, sc, F32_REL)
+        lgf = lg
+    else:
+        ok, worst = A.check_bf16_output(lg, sc, BF16_REL)
+        lgf = A.bf16_bits_to_f32(lg)
+    assert ok, f"{what}: logits worst error / RMS = {worst:.3e}"
+    tok, val = tok.cpu().numpy(), val.cpu().numpy()
+    assert np.array_equal(val, lgf[np.arange(m), tok]), what  # the value is the logit at the token
+    assert np.all(lgf <= val[:, None]), what                  # and the row's maximum
+    _check_token(tok, sc, bf16=not case["f32"])

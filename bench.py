@@ -19,14 +19,15 @@ The headline replays run `--warmup` times, then untimed for `--settle-ms` of wal
 time (the GPU's clock ramps for a few milliseconds once it gets busy, so a handful of
 replays would time the ramp), then exactly `--steps` timed replays.
 
-Also reported: the single GEMV of config 1 (gate_proj's shape at M=1) as its own
-field, the dominant kernel's roofline (the gate|up GeGLU pair at M=1, timed per launch
+Also reported: the single GEMV of gate_proj's shape at M=1 (x [1, 3840], W [15360, 3840])
+as its own field, the dominant kernel's roofline (the gate|up GeGLU pair at M=1, timed per launch
 from graph replays of back-to-back launches), every projection at M = 1, 4, 8, the
 lm_head at M = 1, 8, 16, the prefill GEMM at M = 256 (the reference's long-context
 chunk), 512 and 2048 (the seven projections, the GeGLU pair and the real 12B's
 full-attention shapes), practical peaks (a 1 GiB copy, a read-only streaming kernel,
 hipBLASLt on the gate shape), and the CPU baseline (the oracle's fp32 loop on the host
-cores, on bounded samples of configs 1-4, all threads and one thread).
+cores, on bounded samples of that GEMV, one decoder layer at M = 1, the lm_head at M = 1
+and one layer's prefill at M = 512, all threads and one thread).
 
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--quick]
     python bench.py --roofline-only   # the dominant kernel and a 1 GiB copy only (for rocprofv3)
@@ -121,7 +122,7 @@ def synthetic_weights(n: int, k: int, seed: int):
 
 def synthetic_activations(m: int, k: int, seed: int, outliers: bool = False) -> np.ndarray:
     """bf16 bits of a seeded x ~ N(0, 1) [m, k]; with ``outliers`` 1% of the entries
-    are scaled by 20 (the prefill configuration's activation outliers)."""
+    are scaled by 20 (the prefill workloads' activation outliers)."""
     import torch
 
     rng = np.random.Generator(np.random.PCG64(seed))
@@ -675,7 +676,7 @@ def cpu_model() -> str:
 
 def cpu_baseline(host, lm_triple=None, scale: float = 1.0) -> dict:
     """The oracle's fp32 qmm loop (dequantize a row's groups, then dot; OpenMP over
-    rows) on this host's cores, on bounded samples of four configurations, each timed
+    rows) on this host's cores, on bounded samples of four workloads, each timed
     on all threads and on 1 thread: the single GEMV (gate_proj shape, M = 1), the
     decoder layer's seven projections at M = 1 (the headline's workload and `value`),
     the lm_head at M = 1, and the seven projections at the prefill chunk M = 512.
@@ -718,11 +719,11 @@ def cpu_baseline(host, lm_triple=None, scale: float = 1.0) -> dict:
         return reps, el, nb, fl
 
     layer = [(host[name], k) for name, _, k in LAYER]
-    cases = [("config1_gemv_m1", [(host["gate_proj"], HIDDEN)], 1, 2.0, 1.0, 1.0, "GB/s"),
-             ("config2_layer_m1", layer, 1, 4.0, 2.0, 1.0, "GB/s"),
-             ("config3_prefill_m512", layer, 512, 4.0, 2.0, 1 / 32, "GFLOP/s")]
+    cases = [("gemv_gate_m1", [(host["gate_proj"], HIDDEN)], 1, 2.0, 1.0, 1.0, "GB/s"),
+             ("layer_m1", layer, 1, 4.0, 2.0, 1.0, "GB/s"),
+             ("layer_prefill_m512", layer, 512, 4.0, 2.0, 1 / 32, "GFLOP/s")]
     if lm_triple is not None:
-        cases.insert(2, ("config4_lm_head_m1", [(lm_triple, HIDDEN)], 1, 3.0, 1.5, 1 / 16, "GB/s"))
+        cases.insert(2, ("lm_head_m1", [(lm_triple, HIDDEN)], 1, 3.0, 1.5, 1 / 16, "GB/s"))
     out = {}
     for name, parts, m, t_all, t_one, frac_one, unit in cases:
         res = {}
@@ -733,7 +734,7 @@ def cpu_baseline(host, lm_triple=None, scale: float = 1.0) -> dict:
                           "rows_fraction": frac}
         res["unit"] = unit
         out[name] = res
-    head = out["config2_layer_m1"]["all_threads"]
+    head = out["layer_m1"]["all_threads"]
     return {
         "value": head["value"],
         "unit": "GB/s",
@@ -741,11 +742,11 @@ def cpu_baseline(host, lm_triple=None, scale: float = 1.0) -> dict:
         "kind": "port",
         "sample": f"{head['reps']} decoder-layer steps (7 projections, M=1) in {head['seconds']} s on {threads} "
                   "threads; C restatement of the fp32 dequantize-and-dot loop (oracle/q4_oracle.c), OpenMP over "
-                  "rows; 1-thread and other configurations under 'configs'",
+                  "rows; 1-thread and other workloads under 'workloads'",
         "cpu_model": cpu_model(),
         "threads_source": "OMP_NUM_THREADS" if env_threads.isdigit() else "os.cpu_count()",
         "host_cpus": os.cpu_count(),
-        "configs": out,
+        "workloads": out,
     }
 
 
@@ -931,7 +932,7 @@ def main() -> int:
     if traffic_rec is not None:
         roofline["traffic_source"] = traffic_rec.get("source")
 
-    # --- config 1: the single GEMV (x [1, 3840], W [15360, 3840]) ---
+    # --- the single GEMV of gate_proj's shape (x [1, 3840], W [15360, 3840]) ---
     n1, k1 = dims["gate_proj"]
     us1 = kernel_us(torch, lambda: Q.QuantizedLinear(*host["gate_proj"]), 1, k1, n1, xs[k1],
                     n1 * k1 // 2 + 4 * n1 * (k1 // 64))
@@ -985,7 +986,7 @@ def main() -> int:
             peaks = {"copy_GBps": round(cg, 1), "read_GBps": rd["GBps"], "read_probe": rd,
                      "dense_bf16_gemm_TFLOPS_gate_m2048": round(dense, 1),
                      "roofline_frac_of_read": round(gu_gbs / rd["GBps"], 4),
-                     "gemv_config1_frac_of_read": round(gbs1 / rd["GBps"], 4),
+                     "gemv_gate_m1_frac_of_read": round(gbs1 / rd["GBps"], 4),
                      "gemm_frac_of_dense": round(head["TFLOPS"] / dense, 4)}
 
     variants = None
@@ -1031,7 +1032,7 @@ def main() -> int:
         },
         "pct_hbm_peak": round(value / HBM_PEAK_GBS * 100, 2),
         "headline_settle": settle_info,
-        "config1_gemv_m1": gemv1,
+        "gemv_gate_m1": gemv1,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "decode_step_by_m": step_by_m,

@@ -127,7 +127,7 @@ def test_geglu_decode_gate_up(gpu_lib, m):
 def test_geglu_prefill_gate_up(gpu_lib, m):
     """Chunked prefill: the fused pair at M=512 and 2048 (and short prompts of 33 and 64
     rows, the 64-row tile), sampled rows against the oracle, then the chain into
-    down_proj (config 3's GeGLU -> down)."""
+    down_proj (the prefill MLP's GeGLU -> down)."""
     import torch
 
     gate, up = _pair(15360, 3840, 20260630 + 2004)

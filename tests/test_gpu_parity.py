@@ -13,7 +13,7 @@ property the kernels have:
     ACC_REL * RMS(y_exact) of y_exact (A.check_bf16_rounding), and at least
     RNE_FRAC of the outputs equal RNE(y_exact) exactly (a truncating or otherwise
     wrong rounding would match about half);
-  * where the correctly rounded outputs themselves meet north_star's literal bar
+  * where the correctly rounded outputs themselves meet the literal bar
     max |y - y_exact| <= 1e-2 * RMS (no half-ulp allowance), the kernel's do too
     (decode inputs without outliers: bf16 rounding alone can exceed the literal bar
     only when the largest output sits in a binade whose half ulp is > 1e-2 * RMS).
@@ -90,7 +90,7 @@ def assert_close(y_dev, y_exact, what=""):
 
 def assert_rounded(y_dev, y_exact, what="", literal=False):
     """bf16 output: one rounding of a value within ACC_REL * RMS of the exact result,
-    RNE(exact) on at least RNE_FRAC of the outputs; with `literal`, north_star's
+    RNE(exact) on at least RNE_FRAC of the outputs; with `literal`, the literal bar
     max |err| <= 1e-2 * RMS wherever RNE(exact) itself meets it."""
     y = host_bits(y_dev)
     ok, worst, equal = A.check_bf16_rounding(y, y_exact, ACC_REL)
@@ -356,7 +356,7 @@ def test_gemm_small_shapes(gpu_lib, gemm_from_32, n, k, m, f32):
 @pytest.mark.parametrize("proj", sorted(PROJ))
 @pytest.mark.parametrize("m", [512, 2048])
 def test_gemm_prefill_projections(gpu_lib, proj, m):
-    """Config 3's seven projections at the prefill chunks M = 512 and 2048, activations
+    """The seven projections at the prefill chunks M = 512 and 2048, activations
     with 1% outliers x20."""
     import torch
 

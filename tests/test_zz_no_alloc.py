@@ -55,7 +55,7 @@ def test_noalloc_matches_forward_on_consecutive_calls(gpu_lib, dtype_name, gemm_
                # by a smaller one on the same scratch
         (2048, 3840, 512),    # GEMM, K split over workgroups: group sums + partial planes
         (40, 384, 40),        # small GEMM
-        (3840, 15360, 2048),  # GEMM, the largest group-sum table of the configs
+        (3840, 15360, 2048),  # GEMM, the largest group-sum table of the benchmarked shapes
         (2048, 3840, 1),      # decode: no scratch
         (130, 1088, 300),     # GEMM with a ragged last octet
         (48, 576, 33),

@@ -1,0 +1,135 @@
+"""Concurrent use and graph capture of the C ABI on the GPU.
+
+A handle is immutable after create, so forward may run on several streams and host
+threads at once; per-call scratch comes from a stream-ordered pool and goes back on
+the caller's stream.  Every kernel is deterministic (split-K partial sums are added in
+split order), so concurrent results must equal the serial ones bit for bit:
+
+  * four host threads, each on its own stream (default priority), run the decode
+    path, the split-K GEMM, the gate|up pair and the greedy head on shared handles
+    with their own inputs, interleaved; every output equals the serial result on the
+    default stream;
+  * the same calls captured once in a graph and replayed five times, the inputs
+    rewritten by eager work between replays: every replay equals the eager result
+    for its inputs (the scratch allocations become graph nodes; no memset nodes).
+"""
+
+import threading
+
+import numpy as np
+import pytest
+
+from oracle import affine as A
+from test_gpu_parity import dev_triple, dev_x, random_triple
+
+pytestmark = pytest.mark.gpu
+
+K = 1024
+N = 4096
+F = 2048
+# decode at 1 and 5 rows; at 512 rows M*N*K = 2.1e9 takes the GEMM (128-row tiles, K
+# split in two)
+ROWS = (1, 5, 512)
+
+
+def _handles(gpu_lib):
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*random_triple(N, K, 11)))
+    pair = gpu_lib.QuantizedGeGLU(dev_triple(*random_triple(F, K, 12)), dev_triple(*random_triple(F, K, 13)))
+    head = gpu_lib.QuantizedLinear(*dev_triple(*random_triple(20000, K, 14)))
+    return lin, pair, head
+
+
+def _run(lin, pair, head, xs, torch):
+    """Every call of one round on the current stream: outputs in a list."""
+    outs = []
+    for x in xs:
+        outs.append(lin.forward(x))
+        outs.append(lin.forward(x, out_dtype=torch.float32))
+        outs.append(pair.forward(x))
+        if x.shape[0] <= 16:
+            tok, val, logits = head.forward_greedy(x, softcap=30.0, return_logits=True)
+            outs += [tok, val, logits]
+    return outs
+
+
+def _inputs(seed):
+    return [dev_x(A.make_activations(m, K, seed=seed + m, outliers=True)) for m in ROWS]
+
+
+def _same(a, b):
+    import torch
+
+    return (a.shape == b.shape and a.dtype == b.dtype
+            and torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8)))
+
+
+def test_threads_on_own_streams_match_serial(gpu_lib):
+    import torch
+
+    lin, pair, head = _handles(gpu_lib)
+    threads_n, rounds = 4, 6
+    inputs = [[_inputs(1000 * t + 10 * r) for r in range(rounds)] for t in range(threads_n)]
+    # serial reference on the default stream
+    want = [[_run(lin, pair, head, inputs[t][r], torch) for r in range(rounds)] for t in range(threads_n)]
+    torch.cuda.synchronize()
+
+    got = [[None] * rounds for _ in range(threads_n)]
+    errors = []
+    start = threading.Barrier(threads_n)
+
+    def worker(t):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                start.wait(timeout=60)
+                for r in range(rounds):
+                    got[t][r] = _run(lin, pair, head, inputs[t][r], torch)
+            s.synchronize()
+        except Exception as e:  # reported below, with the thread
+            errors.append((t, repr(e)))
+
+    ts = [threading.Thread(target=worker, args=(t,), daemon=True) for t in range(threads_n)]
+    for th in ts:
+        th.start()
+    for th in ts:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in ts), "a worker thread did not finish"
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for t in range(threads_n):
+        for r in range(rounds):
+            for i, (a, b) in enumerate(zip(got[t][r], want[t][r])):
+                assert _same(a, b), f"thread {t} round {r} output {i} differs from the serial result"
+    for h in (lin, pair, head):
+        h.close()
+
+
+def test_graph_replays_match_eager(gpu_lib):
+    import torch
+
+    lin, pair, head = _handles(gpu_lib)
+    xs = _inputs(5000)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _run(lin, pair, head, xs, torch)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = _run(lin, pair, head, xs, torch)
+    torch.cuda.synchronize()
+    for rep in range(5):
+        # eager work between replays: new inputs written into the captured buffers
+        for i, m in enumerate(ROWS):
+            xs[i].copy_(dev_x(A.make_activations(m, K, seed=7000 + 100 * rep + m, outliers=True)))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = _run(lin, pair, head, xs, torch)
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(outs, want)):
+            assert _same(a, b), f"replay {rep}: output {i} differs from the eager result"
+    del g
+    for h in (lin, pair, head):
+        h.close()

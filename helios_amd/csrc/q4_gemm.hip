@@ -12,7 +12,8 @@
 //
 // Tiling: a 512-thread workgroup computes a 256 (M) x 256 (N) tile as 2 x 4 waves
 // of 128 x 64 (two waves per SIMD, so one's MFMA and LDS latencies are covered by
-// the other's work); or 128 x 256 (2 x 4 waves of 64 x 64).  The kernel is written
+// the other's work); or 128 x 256 (2 x 4 waves of 64 x 64); or, for M <= 64,
+// 64 x 256 (2 x 4 waves of 32 x 64).  The kernel is written
 // for tiles of BN = 128 too (four waves, 78 KiB of LDS: two workgroups per CU); a
 // forced-plan sweep over the benchmark's shapes measured it within 6% of the two
 // tiles above where it helped at all, so the plan does not use it.  Everything streams through LDS by direct-to-LDS buffer loads
@@ -132,7 +133,8 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
                                                    int g_split, long split_stride, int n_out,
                                                    const uint16_t* __restrict__ gelu_table) {
     // BM = 256: 2 x 4 waves of 128 x 64; BM = 128: 2 x 4 waves of 64 x 64 (more
-    // workgroups for small M without splitting K); BN = 128: 2 x 2 waves
+    // workgroups for small M without splitting K); BM = 64: 2 x 4 waves of 32 x 64
+    // (M <= 64); BN = 128: 2 x 2 waves
     static_assert(BM == 256 || BM == 128 || BM == 64, "tile rows");
     static_assert(BN == 256 || BN == 128, "tile columns");
     constexpr int kWaves = 2 * (BN / kWN);        // 2 (M) x BN/64 (N) waves
@@ -583,7 +585,7 @@ __global__ void split_geglu_kernel(const float* __restrict__ part, void* __restr
 
 }  // namespace
 
-// Tile shape and split of K.  For each tile shape (256 x 256 or 128 x 256) and split
+// Tile shape and split of K.  For each tile shape (256, 128 or 64 rows x 256) and split
 // count (whole octets per split), the cost is
 // rounds-of-workgroups x octets-per-split x the measured step time, plus the partial
 // sums' extra traffic; the cheapest wins.

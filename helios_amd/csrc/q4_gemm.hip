@@ -587,12 +587,18 @@ __global__ void split_geglu_kernel(const float* __restrict__ part, void* __restr
 
 // Tile shape and split of K.  For each tile shape (256, 128 or 64 rows x 256) and split
 // count (whole octets per split), the cost is
-// rounds-of-workgroups x octets-per-split x the measured step time, plus the partial
-// sums' extra traffic; the cheapest wins.
+//   rounds of workgroups x (groups per split x the step time + kRoundUs)
+//   + for a split: kSplitUs + the partial sums' bytes / kPartialBytesPerUs,
+// and the cheapest wins.  The constants are fitted to every plan measured on the eight
+// prefill shapes (q, k, o, gate, down, the gate|up pair, the full-attention q and o) at
+// 13 row counts from 64 to 2048: the picks average 0.2% and at worst 4.4% over the
+// fastest plan of each case (with partial sums at 6 MB/us, no per-round or per-split
+// overhead beyond 3 us and 1.15 us per 128-row step: 1.3% and 23%, e.g. gate at 576
+// rows 140 us against 114 for the best plan).
 namespace {
 struct TileShape {
     int bm, bn, per_cu;
-    double step_us;  // one 64-wide group step of a workgroup at that occupancy (measured)
+    double step_us;  // one 64-wide group step of a workgroup (fitted with the constants below)
     int max_m;       // offered up to this many rows (0: any)
 };
 // The 64-row tile: for M <= 64, where the 128-row tile would pad half its rows
@@ -600,14 +606,16 @@ struct TileShape {
 // 38.7-41.1 us, down 3840x15360 35.8-36.7 vs 40.5-42.2, the gate|up pair 42.2-46.9 vs
 // 52.8-56.6; slower from 128 rows on).  Its step time is fitted at one workgroup per
 // CU (two fit, but then each runs at half the rate).
-constexpr TileShape kTileShapes[] = {{256, 256, 1, 2.0, 0}, {128, 256, 1, 1.15, 0}, {64, 256, 1, 0.8, 64}};
+constexpr TileShape kTileShapes[] = {{256, 256, 1, 2.0, 0}, {128, 256, 1, 1.2, 0}, {64, 256, 1, 0.7, 64}};
+constexpr double kRoundUs = 2.0;               // per round of workgroups: prologue, epilogue, ramp
+constexpr double kSplitUs = 6.0;               // a split's reduction launch
+constexpr double kPartialBytesPerUs = 4.0e6;   // partial sums written and read back
 }  // namespace
 
 GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
     GemmPlan p;
     const int octets = (l.g + 7) / 8;
     const long cus = device_cus();
-    const double bytes_per_us = 6.0e6;  // partial sums written and read back, largely through the caches
     double best = -1.0;
     for (const TileShape& ts : kTileShapes) {
         if (ts.max_m > 0 && m > ts.max_m) continue;
@@ -622,7 +630,7 @@ GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
             const size_t m16 = ((size_t)m + bm - 1) / bm * (bm / 16);
             if (m16 * octets * 64 * 16 + part > max_workspace) break;  // (more splits need more)
             const double rounds = (double)((tiles * s + cus * ts.per_cu - 1) / (cus * ts.per_cu));
-            const double t = rounds * per * 8 * ts.step_us + (s > 1 ? 3.0 + part / bytes_per_us : 0.0);
+            const double t = rounds * (per * 8 * ts.step_us + kRoundUs) + (s > 1 ? kSplitUs + part / kPartialBytesPerUs : 0.0);
             if (best < 0.0 || t < best) {
                 best = t;
                 p.bm = bm;

@@ -603,10 +603,13 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
         return hipGetLastError();
     }
     const size_t stream_lds = lds_bytes + (size_t)ms * 16;  // x rows one 16-byte unit longer
-    // K of a multiple of 8 pairs beyond 64 (down_proj) at M = 3-4: the one-pass global-x
-    // variant below is ahead of streaming (12.0 vs 12.6 us at M = 3, 12.5 vs 13.7 at 4;
-    // behind at M = 2)
-    const bool one_pass = MT >= 4 && l.gp % 8 == 0 && l.gp / 8 <= 16 && l.gp / 4 > 16;
+    // At M = 3-4, K too long for the per-row-block kernel but short enough for one pass
+    // of at most 16 waves, the global-x variant below is ahead of streaming: K of a
+    // multiple of 8 pairs beyond 64 (down_proj: 12.0 vs 12.6 us at M = 3, 12.5 vs 13.7
+    // at 4; behind at M = 2) and of 33-64 pairs in 4-pair waves (the full-attention o,
+    // 8192: 8.77 vs 9.08 at M = 3, 8.92 vs 9.32 at 4)
+    const bool one_pass = MT >= 4 && ((l.gp % 8 == 0 && l.gp / 8 <= 16 && l.gp / 4 > 16) ||
+                                      (l.gp > kXLdsMaxPairs && l.gp % 4 == 0 && l.gp / 4 <= 16));
     // persistent streaming kernel: 4 pairs per chunk, up to 8 waves per workgroup
     int waves = (l.gp + GPW - 1) / GPW;
     if (waves > 8) waves = 8;
@@ -620,10 +623,10 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
     // 16 rows of K) costs each workgroup more than its weights, and the per-block
     // kernel below, reading x straight from L2, is ahead: q_proj 4096x3840 at M = 16
     // 7.7 vs 9.0 us, at M = 64 20.4 vs 31.6; k_proj 2048x3840 at M = 128 19.4 vs
-    // 30.7; the fused qkv 8192x3840 (two blocks per workgroup) 20.9 vs 22.1 at M = 32
-    // (behind at one slab, 12.3 vs 12.0).  gate 15360x3840 (four per workgroup) stays
-    // streaming: 15.4 vs 20.7 at M = 16.
-    const bool few_blocks = MT == 16 && (per_wg == 1 || (per_wg == 2 && slabs > 1));
+    // 30.7; the fused qkv 8192x3840 (two blocks per workgroup) 20.9 vs 22.1 at M = 32,
+    // and in one slab 9.8 vs 10.9 at M = 9-10, 11.3 vs 12.0 at 14, 12.0 vs 12.1 at 16.
+    // gate 15360x3840 (four per workgroup) stays streaming: 15.4 vs 20.7 at M = 16.
+    const bool few_blocks = MT == 16 && per_wg <= 2;
     if (!one_pass && !few_blocks && lds_fit > 0) {
         const int grid = (l.nb + per_wg - 1) / per_wg;
         // one workgroup per CU and a long walk (the lm_head at M = 8: 126 vs 135 us):

@@ -601,12 +601,15 @@ struct TileShape {
     double step_us;  // one 64-wide group step of a workgroup (fitted with the constants below)
     int max_m;       // offered up to this many rows (0: any)
 };
-// The 64-row tile: for M <= 64, where the 128-row tile would pad half its rows
-// (measured at 33-64 rows against the 128-row plans: gate 15360x3840 32.6-35.3 vs
+// The 64-row tile: offered up to 128 rows.  At 33-64 rows the 128-row tile would pad
+// half its rows (measured against the 128-row plans: gate 15360x3840 32.6-35.3 vs
 // 38.7-41.1 us, down 3840x15360 35.8-36.7 vs 40.5-42.2, the gate|up pair 42.2-46.9 vs
-// 52.8-56.6; slower from 128 rows on).  Its step time is fitted at one workgroup per
-// CU (two fit, but then each runs at half the rate).
-constexpr TileShape kTileShapes[] = {{256, 256, 1, 2.0, 0}, {128, 256, 1, 1.2, 0}, {64, 256, 1, 0.7, 64}};
+// 52.8-56.6); at 65-128 rows it is ahead for the attention projections (q and o at
+// 80-128 rows 10-13%, the full-attention q and o at 128 4-5%) and 2-5% behind for
+// gate, down and the pair, which the step time below keeps on the 128-row tile.  The
+// step time is fitted at one workgroup per CU (two fit, but each then runs at half
+// the rate).
+constexpr TileShape kTileShapes[] = {{256, 256, 1, 2.0, 0}, {128, 256, 1, 1.2, 0}, {64, 256, 1, 0.85, 128}};
 constexpr double kRoundUs = 2.0;               // per round of workgroups: prologue, epilogue, ramp
 constexpr double kSplitUs = 6.0;               // a split's reduction launch
 constexpr double kPartialBytesPerUs = 4.0e6;   // partial sums written and read back

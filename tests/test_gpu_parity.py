@@ -472,6 +472,32 @@ def test_gemm_short_prompt_mlp(gpu_lib, gemm_from_32, m):
         assert assert_close(yf[rt], want, f"{proj} m={m} f32") < 5e-4
 
 
+@pytest.mark.parametrize("proj,m", [("q_proj", 80), ("o_proj", 113), ("q_proj", 128), ("full_q_proj", 128),
+                                    ("full_o_proj", 128)])
+def test_gemm_64_row_tile_two_row_tiles(gpu_lib, gemm_from_32, proj, m):
+    """The 64-row tile past 64 rows (two row tiles, the second ragged at 80 and 113):
+    the attention projections at 65-128 rows; sampled rows of both tiles against the
+    oracle."""
+    import torch
+
+    shapes = {**PROJ, **FULL_ATTENTION}
+    n, k = shapes[proj]
+    seed = (20260630 + 1000 + sorted(PROJ).index(proj) if proj in PROJ
+            else 20260630 + 6000 + sorted(FULL_ATTENTION).index(proj))
+    tri = A.make_weights(n, k, seed=seed)
+    x = A.make_activations(m, k, seed=6600 + m, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*tri))
+    y = lin.forward(dev_x(x))
+    yf = lin.forward(dev_x(x), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    lin.close()
+    rows = np.unique(np.concatenate([np.linspace(0, m - 1, 16).astype(np.int64), [63, 64, m - 1]]))
+    rt = torch.from_numpy(rows).cuda()
+    want = C.qmm_f64(np.ascontiguousarray(x[rows]), *tri)
+    assert_close(y[rt], want, f"{proj} m={m} bf16")
+    assert assert_close(yf[rt], want, f"{proj} m={m} f32") < 5e-4
+
+
 def test_gemm_prefill_chain_m2048_geglu(gpu_lib):
     """Chunked-prefill chain at M=2048: gate and up, GeGLU on the host (identical bf16
     bytes to both sides), then down_proj; sampled rows against the oracle."""

@@ -555,10 +555,11 @@ inline Split choose_split(int gpairs, int mt) {
 constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950 LDS per CU (and per workgroup)
 // row-block-per-wave kernel: M = 1 with this many 16-row blocks, 4 waves per
 // workgroup, at most this many workgroups per CU.  Measured against the streaming
-// kernel: ~0.4 us ahead for gate (960 blocks) and gate|up (1920); behind for the
-// qkv-sized 512 blocks, for the lm_head's 16384 and for every M > 1.
+// kernel: ~0.4 us ahead for gate (960 blocks) and gate|up (1920), 1.8% for the
+// lm_head's 16384 (91.6 vs 93.3 us); behind for the qkv-sized 512 blocks (9.2 vs
+// 6.4 us) and for every M > 1.
 constexpr int kRowsMinBlocks = 768;
-constexpr int kRowsMaxBlocks = 4096;
+constexpr int kRowsMaxBlocks = 16384;
 constexpr int kRowsWaves = 4;
 constexpr int kRowsPerCu = 2;
 // one workgroup per row block with x staged in LDS (decode_kernel<MT, 4, true>, 8

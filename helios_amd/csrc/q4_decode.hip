@@ -553,11 +553,12 @@ inline Split choose_split(int gpairs, int mt) {
 }
 
 constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950 LDS per CU (and per workgroup)
-// row-block-per-wave kernel: M = 1 with this many 16-row blocks, 4 waves per
-// workgroup, at most this many workgroups per CU.  Measured against the streaming
-// kernel: ~0.4 us ahead for gate (960 blocks) and gate|up (1920), 1.8% for the
-// lm_head's 16384 (91.6 vs 93.3 us); behind for the qkv-sized 512 blocks (9.2 vs
-// 6.4 us) and for every M > 1.
+// row-block-per-wave kernel: M = 1 and 2 with this many 16-row blocks, 4 waves per
+// workgroup, at most this many workgroups per CU.  Measured against the other
+// kernels: at M = 1 ~0.4 us ahead for gate (960 blocks) and gate|up (1920), 1.8% for
+// the lm_head's 16384 (91.6 vs 93.3 us); at M = 2 gate 10.6 vs 11.35 us, gate|up
+// 15.5 vs 17.4, the lm_head 92.1 vs 94.6; behind for the qkv-sized 512 blocks (9.2 vs
+// 6.4 us at M = 1) and from M = 3 on (gate 12.9 vs 11.9 at M = 3, 13.7 vs 12.0 at 4).
 constexpr int kRowsMinBlocks = 768;
 constexpr int kRowsMaxBlocks = 16384;
 constexpr int kRowsWaves = 4;
@@ -585,7 +586,7 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
     const unsigned slabs = (unsigned)((m + 15) / 16);
     const size_t static_lds = 2 * 8 * R * 64 * sizeof(float);
     const size_t lds_bytes = (size_t)ms * (l.k + GPW * 128) * 2 + (size_t)(l.gp + GPW) * 2 * 16 * 4;
-    if constexpr (MT == 1) {
+    if constexpr (MT <= 2) {
         if (l.nb >= kRowsMinBlocks && l.nb <= kRowsMaxBlocks && lds_bytes <= kLdsPerCu && op.mode < kOutGreedyBf16) {
             // many row blocks: one wave per block, no cross-wave reduction
             int grid = (l.nb + kRowsWaves - 1) / kRowsWaves;

@@ -95,7 +95,7 @@ def test_geglu_small_shapes(gpu_lib, gemm_from_32, f, k, m, f32):
     pair.close()
 
 
-@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
 def test_geglu_decode_gate_up(gpu_lib, m):
     """The Gemma 4 12B MLP front half at decode (gate and up 15360 x 3840)."""
     import torch

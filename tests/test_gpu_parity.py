@@ -170,7 +170,7 @@ def test_forward_odd_group_count_and_3d_input(gpu_lib):
 
 
 @pytest.mark.parametrize("proj", sorted(PROJ))
-@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
 def test_forward_decode_projections(gpu_lib, proj, m):
     """Config shapes at full size: decoder projections at decode batch M."""
     import torch
@@ -191,7 +191,7 @@ def test_forward_decode_projections(gpu_lib, proj, m):
     lin.close()
 
 
-@pytest.mark.parametrize("m", [1, 8, 16])
+@pytest.mark.parametrize("m", [1, 2, 8, 16])
 def test_lm_head_decode_and_verify(gpu_lib, m):
     """The lm_head (262144 x 3840) at decode M = 1 and at the verify blocks M = 8 and
     16 (native_model.cc:1782-1795, called at :2006 with the block of

@@ -561,14 +561,19 @@ constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950 LDS per CU (and per workgrou
 // 6.4 us at M = 1) and from M = 3 on (gate 12.9 vs 11.9 at M = 3, 13.7 vs 12.0 at 4).
 constexpr int kRowsMinBlocks = 768;
 constexpr int kRowsMaxBlocks = 16384;
+// at M = 2 only up to this many group pairs of K: 8-bit gate and the gate|up pair (60
+// pairs) are 6-7% behind streaming there (17.0 vs 16.0 us, 27.3 vs 25.5)
+constexpr int kRowsM2MaxPairs = 32;
 constexpr int kRowsWaves = 4;
 constexpr int kRowsPerCu = 2;
 // one workgroup per row block with x staged in LDS (decode_kernel<MT, 4, true>, 8
 // waves of 4 pairs, one pass): for K of at most 32 pairs and up to this many row
-// blocks (twice as many for M > 1) it is ahead of the streaming kernel at every M
-// (0.5-0.8 us at M = 1, 1-3 us at M = 8 for q/k/v/o and their fused qkv, 1.2 us for
-// gate at M = 4 and 8); it is behind for the gate|up pair, the lm_head, down (K of
-// 120 pairs) and gate at M = 1 (the row kernel's case).
+// blocks (twice as many for M > 1) it is ahead of the streaming kernel (0.5-0.8 us at
+// M = 1, 1-3 us at M = 8 for q/k/v/o and their fused qkv, 0.8 us for the qkv at
+// M = 3-4); it is behind for the gate|up pair, the lm_head, down (K of 120 pairs) and
+// gate at M = 1-2 (the row kernel's case).  For gate at M = 3-16 the two are within
+// the spread between machines (streaming 6% ahead at M = 3-4 on one, 3% behind on
+// another).
 constexpr int kXLdsMaxPairs = 32;
 constexpr int kXLdsMaxBlocks = 512;
 constexpr size_t kXLdsMaxBytes = 64 * 1024;
@@ -587,7 +592,8 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
     const size_t static_lds = 2 * 8 * R * 64 * sizeof(float);
     const size_t lds_bytes = (size_t)ms * (l.k + GPW * 128) * 2 + (size_t)(l.gp + GPW) * 2 * 16 * 4;
     if constexpr (MT <= 2) {
-        if (l.nb >= kRowsMinBlocks && l.nb <= kRowsMaxBlocks && lds_bytes <= kLdsPerCu && op.mode < kOutGreedyBf16) {
+        if (l.nb >= kRowsMinBlocks && l.nb <= kRowsMaxBlocks && lds_bytes <= kLdsPerCu && op.mode < kOutGreedyBf16 &&
+            (MT == 1 || l.gp <= kRowsM2MaxPairs)) {
             // many row blocks: one wave per block, no cross-wave reduction
             int grid = (l.nb + kRowsWaves - 1) / kRowsWaves;
             const int cap = device_cus() * kRowsPerCu;
@@ -605,13 +611,17 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
         return hipGetLastError();
     }
     const size_t stream_lds = lds_bytes + (size_t)ms * 16;  // x rows one 16-byte unit longer
-    // At M = 3-4, K too long for the per-row-block kernel but short enough for one pass
+    // From M = 3, K too long for the per-row-block kernel but short enough for one pass
     // of at most 16 waves, the global-x variant below is ahead of streaming: K of a
     // multiple of 8 pairs beyond 64 (down_proj: 12.0 vs 12.6 us at M = 3, 12.5 vs 13.7
-    // at 4; behind at M = 2) and of 33-64 pairs in 4-pair waves (the full-attention o,
-    // 8192: 8.77 vs 9.08 at M = 3, 8.92 vs 9.32 at 4)
+    // at 4; behind at M = 2), and K of 33-64 pairs in 4-pair waves when there are no
+    // more row blocks than CUs (the full-attention o, 8192 x 240 blocks: 8.77 vs 9.08 at
+    // M = 3, 8.92 vs 9.32 at 4; 8-bit q, 60 pairs x 256 blocks).  With more blocks
+    // streaming stays ahead (8-bit gate, 960 blocks: 17.1 vs 28.1 us at M = 3; the
+    // 8-bit gate|up pair and qkv likewise).
     const bool one_pass = MT >= 4 && ((l.gp % 8 == 0 && l.gp / 8 <= 16 && l.gp / 4 > 16) ||
-                                      (l.gp > kXLdsMaxPairs && l.gp % 4 == 0 && l.gp / 4 <= 16));
+                                      (l.gp > kXLdsMaxPairs && l.gp % 4 == 0 && l.gp / 4 <= 16 &&
+                                       l.nb <= device_cus()));
     // persistent streaming kernel: 4 pairs per chunk, up to 8 waves per workgroup
     int waves = (l.gp + GPW - 1) / GPW;
     if (waves > 8) waves = 8;
@@ -626,9 +636,11 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
     // kernel below, reading x straight from L2, is ahead: q_proj 4096x3840 at M = 16
     // 7.7 vs 9.0 us, at M = 64 20.4 vs 31.6; k_proj 2048x3840 at M = 128 19.4 vs
     // 30.7; the fused qkv 8192x3840 (two blocks per workgroup) 20.9 vs 22.1 at M = 32,
-    // and in one slab 9.8 vs 10.9 at M = 9-10, 11.3 vs 12.0 at 14, 12.0 vs 12.1 at 16.
-    // gate 15360x3840 (four per workgroup) stays streaming: 15.4 vs 20.7 at M = 16.
-    const bool few_blocks = MT == 16 && per_wg <= 2;
+    // and in one slab 9.8 vs 10.9 at M = 9-10, 11.3 vs 12.0 at 14, 12.0 vs 12.1 at 16
+    // (but not its 8-bit twin, 60 pairs: streaming 13.9 / 15.3 vs 16.1 / 17.1 us at
+    // M = 6 / 8).  gate 15360x3840 (four per workgroup) stays streaming: 15.4 vs 20.7
+    // at M = 16.
+    const bool few_blocks = MT == 16 && (per_wg == 1 || (per_wg == 2 && (slabs > 1 || l.gp <= kXLdsMaxPairs)));
     if (!one_pass && !few_blocks && lds_fit > 0) {
         const int grid = (l.nb + per_wg - 1) / per_wg;
         // one workgroup per CU and a long walk (the lm_head at M = 8: 126 vs 135 us):

@@ -35,7 +35,8 @@ def test_q8_dequantize_bit_exact(gpu_lib, n, k):
 
 
 @pytest.mark.parametrize("n,k,m", [(4096, 3840, 1), (2048, 3840, 4), (3840, 15360, 8), (300, 640, 17),
-                                   (15360, 3840, 1), (256, 640, 33), (130, 1088, 300), (512, 3840, 512)])
+                                   (15360, 3840, 1), (15360, 3840, 4), (8192, 3840, 6), (4096, 3840, 3),
+                                   (256, 640, 33), (130, 1088, 300), (512, 3840, 512)])
 @pytest.mark.parametrize("f32", [False, True])
 def test_q8_forward(gpu_lib, gemm_from_32, n, k, m, f32):
     import torch

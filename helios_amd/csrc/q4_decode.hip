@@ -561,8 +561,10 @@ constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950 LDS per CU (and per workgrou
 // 6.4 us at M = 1) and from M = 3 on (gate 12.9 vs 11.9 at M = 3, 13.7 vs 12.0 at 4).
 constexpr int kRowsMinBlocks = 768;
 constexpr int kRowsMaxBlocks = 16384;
-// at M = 2 only up to this many group pairs of K: 8-bit gate and the gate|up pair (60
-// pairs) are 6-7% behind streaming there (17.0 vs 16.0 us, 27.3 vs 25.5)
+// at M = 2 only up to this many group pairs of K (the measured gains above are at 30
+// pairs); with 60 pairs (8-bit gate and gate|up pair) the row kernel and streaming
+// were within the spread between machines (6-7% behind on one, 3-7% ahead on
+// another), so those keep streaming
 constexpr int kRowsM2MaxPairs = 32;
 constexpr int kRowsWaves = 4;
 constexpr int kRowsPerCu = 2;

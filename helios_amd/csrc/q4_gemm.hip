@@ -10,10 +10,14 @@
 //   xaug_kernel), B = [b, b, s, s] taken straight from the scale/bias words.
 // Every product is exact; rounding is fp32 accumulation only.
 //
-// Tiling: a 512-thread workgroup computes a 256 (M) x 256 (N) tile as 2 x 4 waves
-// of 128 x 64 (two waves per SIMD, so one's MFMA and LDS latencies are covered by
-// the other's work); or 128 x 256 (2 x 4 waves of 64 x 64); or, for M <= 64,
-// 64 x 256 (2 x 4 waves of 32 x 64).  The kernel is written
+// Tiling: a 512-thread workgroup computes a 256 (M) x 256 (N) tile as eight waves
+// side by side along N, each all 256 rows x 32 columns (two waves per SIMD, so one's
+// MFMA and LDS latencies are covered by the other's work); or 128 x 256, or 64 x 256
+// (eight waves of 128 or 64 x 32).  A wave expands only its own two row blocks'
+// nibbles and reads every x row of the tile from LDS: expansion is VALU work and was
+// the wider cost (measured against 2 x 4 waves of BM/2 x 64, with bit-identical
+// results: the 64-row tile 8-13% faster, the 128-row tile 3-9%, the 256-row tile
+// 0-6%).  The kernel is written
 // for tiles of BN = 128 too (four waves, 78 KiB of LDS: two workgroups per CU); a
 // forced-plan sweep over the benchmark's shapes measured it within 6% of the two
 // tiles above where it helped at all, so the plan does not use it.  Everything streams through LDS by direct-to-LDS buffer loads
@@ -27,7 +31,7 @@
 namespace q4 {
 namespace {
 
-constexpr int kWN = 64;               // wave tile columns
+constexpr int kWN = 32;               // wave tile columns (the wave tile spans all BM rows)
 constexpr int kNT = kWN / 16;         // 16x16 tiles per wave along N
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -132,19 +136,17 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
                                                    int gpairs, int mtiles, int ntiles, int octets, uint32_t rec_bytes,
                                                    int g_split, long split_stride, int n_out,
                                                    const uint16_t* __restrict__ gelu_table) {
-    // BM = 256: 2 x 4 waves of 128 x 64; BM = 128: 2 x 4 waves of 64 x 64 (more
-    // workgroups for small M without splitting K); BM = 64: 2 x 4 waves of 32 x 64
-    // (M <= 64); BN = 128: 2 x 2 waves
+    // BN / 32 waves of BM x 32: BM = 256; BM = 128 (more workgroups for small M
+    // without splitting K); BM = 64 (M <= 128)
     static_assert(BM == 256 || BM == 128 || BM == 64, "tile rows");
     static_assert(BN == 256 || BN == 128, "tile columns");
-    constexpr int kWaves = 2 * (BN / kWN);        // 2 (M) x BN/64 (N) waves
+    constexpr int kWaves = BN / kWN;              // side by side along N
     constexpr int kRB = BN / 16;                  // 16-row weight blocks per workgroup tile
     constexpr int kXChunks = BM * 8;              // 16-byte chunks of one x group tile (BM rows x 64 bf16)
     constexpr int kWPair = kRB * 64;              // uint4: tiled words of the pair
     constexpr int kSPair = kRB * 16 / 2;          // uint4: scale/bias words of the pair
     constexpr int kXaA = BM / 16 * 64;            // uint4: the bias A operands of the tile's rows
-    constexpr int kWM = BM / 2;                   // wave tile rows
-    constexpr int kMT = kWM / 16;                 // 16x16 tiles per wave along M
+    constexpr int kMT = BM / 16;                  // 16x16 tiles per wave along M
     constexpr int kXParts = BM * 8 / (64 * kWaves);  // 16-byte x loads per wave per group
     // bias A-operand loads per wave per octet: BM / 16 row blocks over the waves (with
     // BM = 64, waves 0-3 load one each and the rest none)
@@ -175,8 +177,6 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     const int lane = threadIdx.x & 63;
     const int col = lane & 15;
     const int kq = lane >> 4;
-    const int wm = wave & 1;
-    const int wn = wave >> 1;
     const int rbw = nt * kRB;  // first 16-row weight block of the workgroup
     const int nblocks = (n_rows + 15) / 16;
 
@@ -275,12 +275,12 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         uint32_t swv[kNT];  // and its scale/bias word
 #pragma unroll
         for (int j = 0; j < kNT; ++j) {
-            const int rbl = wn * kNT + j;
+            const int rbl = wave * kNT + j;
             tw[j] = reinterpret_cast<const uint2*>(wp + rbl * 64 + ln)[gpar];
             swv[j] = reinterpret_cast<const uint32_t*>(sbl + rbl * 16 + lcol)[gpar];
         }
         auto a_frag = [&](int i, int h) {
-            const int r = wm * kWM + 16 * i + lcol;
+            const int r = 16 * i + lcol;
             return __builtin_bit_cast(bf16x8, xs[r * 8 + ((4 * h + lkq) ^ ((r >> 1) & 7))]);
         };
         // The wave's 32 tiles in one stream, software-pipelined and kept in this order
@@ -330,10 +330,10 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     auto bias = [&]() {
         bf16x8 bb[kNT];
 #pragma unroll
-        for (int j = 0; j < kNT; ++j) bb[j] = bias_operand(reinterpret_cast<const uint2*>(g_xab + kXaA)[((wn * kNT + j) * 4 + kq) * 16 + col]);
+        for (int j = 0; j < kNT; ++j) bb[j] = bias_operand(reinterpret_cast<const uint2*>(g_xab + kXaA)[((wave * kNT + j) * 4 + kq) * 16 + col]);
 #pragma unroll
         for (int i = 0; i < kMT; ++i) {
-            const bf16x8 aa = __builtin_bit_cast(bf16x8, g_xab[(wm * kMT + i) * 64 + lane]);
+            const bf16x8 aa = __builtin_bit_cast(bf16x8, g_xab[i * 64 + lane]);
 #pragma unroll
             for (int j = 0; j < kNT; ++j) acc[i][j] = mfma16x16x32(aa, bb[j], acc[i][j]);
         }
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
 
     // store: lane holds rows 4*kq + e of column col of each 16x16 tile.  The GeGLU
     // store takes its lane coordinates afresh (mbcnt), so nothing lane-dependent of
-    // its own stays live across the main loop (which runs at the 256-VGPR limit).
+    // its own stays live across the main loop (some 200 VGPRs in the 256-row tile).
     const int slane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
 
     // bf16 GeGLU: the gelu table (5.5 KiB) into the x ring's first slot, free now
@@ -452,7 +452,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     for (int i = 0; i < kMT; ++i) {
 #pragma unroll
         for (int j = 0; j < kNT; ++j) {
-            const int rb = rbw + wn * kNT + j;
+            const int rb = rbw + wave * kNT + j;
             if constexpr (OUT == kOutGegluBf16) {  // rows e and e + 1 share one GeGLU pass
                 // all values first, stores after the loop: with no store between them
                 // the LDS table reads are issued together rather than waited for one by one
@@ -462,7 +462,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
             }
             if constexpr (OUT == kOutGegluF32) {  // no memory reads: value and store together
                 const int c = slane & 15;
-                const int m = mt * BM + wm * kWM + 16 * i + 4 * (slane >> 4);
+                const int m = mt * BM + 16 * i + 4 * (slane >> 4);
                 const int hn = geglu2_col(c, rb);
 #pragma unroll
                 for (int e = 0; e < 4; e += 2) {
@@ -472,7 +472,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
                 }
                 continue;
             }
-            const int m = mt * BM + wm * kWM + 16 * i + 4 * kq;
+            const int m = mt * BM + 16 * i + 4 * kq;
             {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -495,8 +495,8 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         for (int i = 0; i < kMT; ++i) {
 #pragma unroll
             for (int j = 0; j < kNT; ++j) {
-                const int m = mt * BM + wm * kWM + 16 * i + 4 * (slane >> 4);
-                const int hn = geglu2_col(c, rbw + wn * kNT + j);
+                const int m = mt * BM + 16 * i + 4 * (slane >> 4);
+                const int hn = geglu2_col(c, rbw + wave * kNT + j);
 #pragma unroll
                 for (int e = 0; e < 4; e += 2) {
                     const int mr = geglu2_row(c, m + e, m + e + 1);
@@ -591,28 +591,28 @@ __global__ void split_geglu_kernel(const float* __restrict__ part, void* __restr
 //   + for a split: kSplitUs + the partial sums' bytes / kPartialBytesPerUs,
 // and the cheapest wins.  The constants are fitted to every plan measured on the eight
 // prefill shapes (q, k, o, gate, down, the gate|up pair, the full-attention q and o) at
-// 13 row counts from 64 to 2048: the picks average 0.2% and at worst 4.4% over the
-// fastest plan of each case (with partial sums at 6 MB/us, no per-round or per-split
-// overhead beyond 3 us and 1.15 us per 128-row step: 1.3% and 23%, e.g. gate at 576
-// rows 140 us against 114 for the best plan).
+// 14 row counts from 64 to 2048: the picks average 0.1% and at worst 3.4% over the
+// fastest plan of each case, and moving any one constant by a grid step costs at most
+// 0.1% more on average.  (Partial sums at 6 MB/us, no per-round or per-split overhead
+// beyond 3 us and 1.15 us per 128-row step gave 1.3% and 23% when fitted to the
+// kernel's earlier wave layout: gate at 576 rows 140 us against 114 for the best plan.)
 namespace {
 struct TileShape {
     int bm, bn, per_cu;
     double step_us;  // one 64-wide group step of a workgroup (fitted with the constants below)
     int max_m;       // offered up to this many rows (0: any)
 };
-// The 64-row tile: offered up to 128 rows.  At 33-64 rows the 128-row tile would pad
-// half its rows (measured against the 128-row plans: gate 15360x3840 32.6-35.3 vs
-// 38.7-41.1 us, down 3840x15360 35.8-36.7 vs 40.5-42.2, the gate|up pair 42.2-46.9 vs
-// 52.8-56.6); at 65-128 rows it is ahead for the attention projections (q and o at
-// 80-128 rows 10-13%, the full-attention q and o at 128 4-5%) and 2-5% behind for
-// gate, down and the pair, which the step time below keeps on the 128-row tile.  The
-// step time is fitted at one workgroup per CU (two fit, but each then runs at half
-// the rate).
-constexpr TileShape kTileShapes[] = {{256, 256, 1, 2.0, 0}, {128, 256, 1, 1.2, 0}, {64, 256, 1, 0.85, 128}};
+// The 64-row tile: offered up to 128 rows.  Best plan of each tile, measured: at 64
+// rows the 128-row tile, half of it padding, is 8-20% behind (q 4096x3840 28.4 us vs
+// 31.4, gate 15360x3840 32.9 vs 37.9, down 3840x15360 34.2 vs 38.9, the gate|up pair
+// 43.4 vs 52.2); at 96-128 rows the 64-row tile stays 5-13% ahead for the attention
+// projections (q, k, o and the full-attention q) and within 3% either way for gate,
+// down, the pair and the full-attention o.  The step time is fitted at one workgroup
+// per CU (two fit, but each then runs at half the rate).
+constexpr TileShape kTileShapes[] = {{256, 256, 1, 1.9, 0}, {128, 256, 1, 1.1, 0}, {64, 256, 1, 0.7, 128}};
 constexpr double kRoundUs = 2.0;               // per round of workgroups: prologue, epilogue, ramp
-constexpr double kSplitUs = 6.0;               // a split's reduction launch
-constexpr double kPartialBytesPerUs = 4.0e6;   // partial sums written and read back
+constexpr double kSplitUs = 3.0;               // a split's reduction launch
+constexpr double kPartialBytesPerUs = 3.0e6;   // partial sums written and read back
 }  // namespace
 
 GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {

@@ -6,8 +6,14 @@
 //   from the tiled nibbles in registers (no dequantized weights anywhere), then
 //   acc += 16*s * P_g on the fp32 accumulators (one VALU FMA per output per group);
 // * the bias term: one extra MFMA per tile per 8 groups on an augmented K of 32,
-//   A = [Xh, Xl, -16Xh, -16Xl] per group (X_g = Xh + Xl split into two bf16, from
-//   xaug_kernel), B = [b, b, s, s] taken straight from the scale/bias words.
+//   A = [Xh, Xl, -16Xh, -16Xl] per group (X_g = Xh + Xl split into two bf16),
+//   B = [b, b, s, s] taken straight from the scale/bias words.  In the 64- and
+//   128-row tiles X_g comes from the x tile in LDS: two MFMAs of an all-ones A
+//   against a row tile's x fragments (as B) sum the group's 64 values of its 16 rows,
+//   each wave for its own row tiles.  The 256-row tile takes it from xaug_kernel, a
+//   pre-pass: there every wave reads the 256 rows' fragments from LDS already (about
+//   256 KiB per CU per group step), and reading them again cost more than the
+//   pre-pass's launch (gate 15360x3840 at 2048 rows 228.5 -> 232.4 us).
 // Every product is exact; rounding is fp32 accumulation only.
 //
 // Tiling: a 512-thread workgroup computes a 256 (M) x 256 (N) tile as eight waves
@@ -37,14 +43,32 @@ constexpr int kNT = kWN / 16;         // 16x16 tiles per wave along N
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 
+// The bias MFMA's A operand for one 16-row tile and one octet, as 64 lanes of 16 B:
+// lane (m = l%16, kq = l/16), element e -> group 8*octet + 2*kq + e/4, term e%4 in
+// {Xh, Xl, -16 Xh, -16 Xl}.  Lane (m, kq) packs it from X of row m for groups 2kq and
+// 2kq + 1.
+__device__ __forceinline__ uint4 bias_a_operand(float x0, float x1) {
+    uint32_t w[4];
+    const float xs[2] = {x0, x1};
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        const uint16_t xh = f32_to_bf16(xs[gi]);
+        const uint16_t xl = f32_to_bf16(xs[gi] - __uint_as_float((uint32_t)xh << 16));
+        const uint16_t nxh = f32_to_bf16(-16.0f * __uint_as_float((uint32_t)xh << 16));
+        const uint16_t nxl = f32_to_bf16(-16.0f * __uint_as_float((uint32_t)xl << 16));
+        w[2 * gi] = (uint32_t)xh | ((uint32_t)xl << 16);
+        w[2 * gi + 1] = (uint32_t)nxh | ((uint32_t)nxl << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // ---------------------------------------------------------------------------
-// X_g = sum of x over each 64-wide group, as the augmented-K MFMA A operand:
-// xaug[m16][octet][lane] (16 B), lane (m = l%16, kq = l/16), element e ->
-// group 8*octet + 2*kq + e/4, term e%4 in {Xh, Xl, -16 Xh, -16 Xl}.
+// X_g for the 256-row tile: bias A operands of every 16-row block and octet,
+// xaug[m16][octet][lane] (16 B, as bias_a_operand).  One 512-thread workgroup per
+// 1 KiB block (16 rows x one octet): eight lanes sum one (row, group) from its 128
+// contiguous bytes, two rounds cover the 16 x 8 pairs, the sums meet in LDS and one
+// wave packs the block.
 // ---------------------------------------------------------------------------
-// One 512-thread workgroup per 1 KiB block (16 rows x one octet): eight lanes sum one
-// (row, group) from its 128 contiguous bytes, two rounds cover the 16 x 8 pairs, the
-// sums meet in LDS and one wave packs the block.
 __global__ __launch_bounds__(512) void xaug_kernel(const uint16_t* __restrict__ x, uint4* __restrict__ xaug,
                                                    int m_rows, int kx, int groups, int octets) {
     // x rows are kx long; group g >= kx / 64 (the low plane of a two-plane handle) is
@@ -79,18 +103,7 @@ __global__ __launch_bounds__(512) void xaug_kernel(const uint16_t* __restrict__ 
     __syncthreads();
     if (t >= 64) return;
     const int kq = t >> 4;
-    uint32_t w[4];
-#pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-        const float sum = gsum[2 * kq + gi][t & 15];
-        const uint16_t xh = f32_to_bf16(sum);
-        const uint16_t xl = f32_to_bf16(sum - __uint_as_float((uint32_t)xh << 16));
-        const uint16_t nxh = f32_to_bf16(-16.0f * __uint_as_float((uint32_t)xh << 16));
-        const uint16_t nxl = f32_to_bf16(-16.0f * __uint_as_float((uint32_t)xl << 16));
-        w[2 * gi] = (uint32_t)xh | ((uint32_t)xl << 16);
-        w[2 * gi + 1] = (uint32_t)nxh | ((uint32_t)nxl << 16);
-    }
-    xaug[(long)unit * 64 + t] = make_uint4(w[0], w[1], w[2], w[3]);
+    xaug[(long)unit * 64 + t] = bias_a_operand(gsum[2 * kq][t & 15], gsum[2 * kq + 1][t & 15]);
 }
 
 // B operand of the bias MFMA from one scale/bias word pair: [b0 b0 s0 s0 b1 b1 s1 s1]
@@ -148,21 +161,26 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     constexpr int kXaA = BM / 16 * 64;            // uint4: the bias A operands of the tile's rows
     constexpr int kMT = BM / 16;                  // 16x16 tiles per wave along M
     constexpr int kXParts = BM * 8 / (64 * kWaves);  // 16-byte x loads per wave per group
-    // bias A-operand loads per wave per octet: BM / 16 row blocks over the waves (with
-    // BM = 64, waves 0-3 load one each and the rest none)
-    constexpr int kXaParts = BM / 16 >= kWaves ? BM / 16 / kWaves : 1;
-    constexpr int kXaWaves = BM / 16 >= kWaves ? kWaves : BM / 16;
+    // X_g summed in the kernel (64 and 128 rows), or read from xaug (256 rows)
+    constexpr bool kXIn = BM < 256;
+    // in the kernel: row tiles whose X_g a wave sums, tiles wave + 8t (BM = 64: waves
+    // 0-3 one each, the rest none)
+    constexpr int kXTiles = kXIn ? (kMT + kWaves - 1) / kWaves : 0;
+    // from xaug: 16-byte loads of bias A operands per wave per octet
+    constexpr int kXaParts = BM / 16 / kWaves;
     constexpr int kSWaves = kRB / 8;              // waves that load a pair's scale words (1 KiB each)
     constexpr int kTW = kMT * kNT >= 12 ? 9 : 5;  // product-stream tile after which a pair's weights are issued
     static_assert(kRB == 2 * kWaves, "two row blocks of tiled words per wave per pair");
-    static_assert(kXParts >= 1 && kXaParts * kXaWaves == BM / 16, "every wave loads x; the bias operands are covered");
+    static_assert(kXParts >= 1 && (kXIn ? kMT <= kXTiles * kWaves : kXaParts * kWaves == kMT),
+                  "every wave loads x; every row tile's X_g is summed or loaded");
     __shared__ uint4 g_xs0[kXChunks];             // x group tiles (BM rows x 64: 16 or 32 KiB)
     __shared__ uint4 g_xs1[kXChunks];
     __shared__ uint4 g_xs2[kXChunks];
     __shared__ uint4 g_wp0[kWPair + kSPair];      // a pair's weights: 9 or 18 KiB
     __shared__ uint4 g_wp1[kWPair + kSPair];
-    // one octet's bias operands: A side for the tile's rows [m16][lane], then the
-    // scale/bias words as uint2 [row block][pair][column]
+    // one octet's bias operands: A side for the tile's rows [m16][lane] (written by the
+    // waves, or DMA from xaug), then the scale/bias words as uint2 [row block][pair][column]
+    // (DMA)
     __shared__ uint4 g_xab[kXaA + kRB * 4 * 16 / 2];
     int mt, nt;
     tile_of((int)blockIdx.x, (int)gridDim.x, mtiles, ntiles, mt, nt);
@@ -185,7 +203,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)kx * 2u);
     const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles, rec_bytes);
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb, rec_bytes - kRecSbBytes);
-    const __amdgpu_buffer_rsrc_t ars = make_rsrc(xaug, (uint32_t)(mtiles * (BM / 16) * octets) * 1024u);
+    const __amdgpu_buffer_rsrc_t ars = make_rsrc(xaug, kXIn ? 0u : (uint32_t)(mtiles * (BM / 16) * octets) * 1024u);
 
     // DMA issue.  Per lane, the offsets are fixed for the whole K loop (rows past M and
     // row blocks past N at kOutOfRange) and computed once here; the step moves them by
@@ -229,19 +247,19 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     auto dma_s = [&](int p, uint4* wdst) {
         dma16(p < p_end ? srs : zrs, wdst + kWPair + 64 * wave, sv, (uint32_t)p * kRecBytes);
     };
-    auto dma_xa_part = [&](int o, int u) {
-        const int m16 = kXaParts * wave + u;
-        dma16(ars, g_xab + m16 * 64, (uint32_t)lane * 16u, (uint32_t)(((mt * (BM / 16) + m16) * octets + o) * 1024));
-    };
-    // bias operands of octet o: the A side (kXaParts 16-byte loads) and the scale/bias words
-    // of its four group pairs for row blocks 2w, 2w+1 (lane l: row block 2w + l/32,
-    // pair 4o + (l%32)/8, 16-byte chunk l%8 of that record's 128 bytes of words)
+    // bias operands of octet o: from xaug (256 rows) the A side, kXaParts 16-byte loads;
+    // the scale/bias words of its four group pairs for row blocks 2w, 2w+1 (lane l: row
+    // block 2w + l/32, pair 4o + (l%32)/8, 16-byte chunk l%8 of that record's 128 bytes
+    // of words)
     auto dma_xa = [&](int o) {
         int ln = threadIdx.x & 63;
         asm volatile("" : "+v"(ln));
-        if (kXaWaves == kWaves || wave < kXaWaves) {
+        if constexpr (!kXIn) {
 #pragma unroll
-            for (int u = 0; u < kXaParts; ++u) dma_xa_part(o, u);
+            for (int u = 0; u < kXaParts; ++u) {
+                const int m16 = kXaParts * wave + u;
+                dma16(ars, g_xab + m16 * 64, (uint32_t)lane * 16u, (uint32_t)(((mt * (BM / 16) + m16) * octets + o) * 1024));
+            }
         }
         const int rb = rbw + 2 * wave + (ln >> 5);
         const int chunk = ln & 31;
@@ -252,6 +270,15 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     };
 
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u));
+    // X_g of row 16 (wave + 8t) + col for the lane's two groups of the octet (2kq, 2kq + 1)
+    float xk[kXTiles > 0 ? kXTiles : 1][2];
+    f32x4 xsum[kXTiles > 0 ? kXTiles : 1];  // the current group's sums: every element X_g of row col
+#pragma unroll
+    for (int t = 0; t < kXTiles; ++t) {
+        xk[t][0] = xk[t][1] = 0.0f;
+        xsum[t] = zero;
+    }
     f32x4 acc[kMT][kNT];
 #pragma unroll
     for (int i = 0; i < kMT; ++i)
@@ -283,6 +310,18 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
             const int r = 16 * i + lcol;
             return __builtin_bit_cast(bf16x8, xs[r * 8 + ((4 * h + lkq) ^ ((r >> 1) & 7))]);
         };
+        // X_g of the wave's row tiles: their x fragments as the B operand
+        // (B[k][n] = x[16i + n][k]) against ones, so every output of column n is the sum
+        // of row n's 64 values.  Read again here rather than taken from the product
+        // stream, which would need a branch per row tile.
+        if (kXIn && (kMT % kWaves == 0 || wave < kMT)) {
+#pragma unroll
+            for (int t = 0; t < kXTiles; ++t) {
+                const bf16x8 b0 = a_frag(wave + kWaves * t, 0), b1 = a_frag(wave + kWaves * t, 1);
+                xsum[t] = mfma16x16x32(ones, b0, zero);
+                xsum[t] = mfma16x16x32(ones, b1, xsum[t]);
+            }
+        }
         // The wave's 32 tiles in one stream, software-pipelined and kept in this order
         // (a scheduling fence after each tile): tile t's two products, then tile t-3's
         // scale FMAs, which do not wait for them; row 0 expands each row block's words
@@ -339,22 +378,35 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         }
     };
 
-    // Step g: (1) wait until this wave's loads for group g (issued during step g-2:
-    // x of g and, for even g, the pair g/2) are done, leaving in flight only the loads
-    // of step g-1 (its x, for even g-1 its pair, and the bias operands it may have
-    // issued first); (2) barrier: everyone's data for g is in LDS and everyone is done
-    // with the slots refilled next; (3) at g = 8o + 8, the bias term of octet o (its
-    // operands were loaded at step 8o + 1 and have been waited for since); at
-    // g = 8o + 1, the bias operands of octet o (the barrier above follows the last
-    // read of the previous octet's); (4) multiply, with the loads for group g+2 (and
-    // pair (g+2)/2) spread through the products.  Every step issues the same loads
-    // (past the end they read zeros), so the counts are fixed.
+    // Step g: (0) at g = 8o + 8, write the A operands of octet o (the slot's last
+    // reads, octet o - 1's bias term, were followed by seven barriers); (1) wait until
+    // this wave's loads for group g (issued during step g-2: x of g and, for even g,
+    // the pair g/2) are done, leaving in flight only the loads of step g-1 (its x, for
+    // even g-1 its pair, and the bias words it may have issued first), and its LDS
+    // writes have landed; (2) barrier: everyone's data for g is in LDS and everyone is
+    // done with the slots refilled next; (3) at g = 8o + 8, the bias term of octet o
+    // (its scale/bias words were loaded at step 8o + 1 and have been waited for
+    // since); at g = 8o + 1, the scale/bias words of octet o (the barrier above
+    // follows the last read of the previous octet's); (4) multiply, with the loads for
+    // group g+2 (and pair (g+2)/2) spread through the products, and keep the lane's
+    // X_g.  Every step issues the same loads (past the end they read zeros), so the
+    // counts are fixed.
     auto issues_xa = [&](int g) { return (g & 7) == 1 && g > g_begin + 1; };
     auto issued = [&](int g) {  // loads this wave issues at step g
-        return kXParts + ((g & 1) == 0 ? 2 + (wave < kSWaves ? 1 : 0) : 0) +
-               (issues_xa(g) ? (wave < kXaWaves ? kXaParts : 0) + 1 : 0);
+        return kXParts + ((g & 1) == 0 ? 2 + (wave < kSWaves ? 1 : 0) : 0) + (issues_xa(g) ? 1 + (kXIn ? 0 : kXaParts) : 0);
+    };
+    // the octet's A operands of the wave's row tiles into the bias slot; X_g restarts.
+    // (At the top of a step, before its barrier: written at the end of one, inlined in
+    // every step of the unrolled loop, it cost 40-50 more VGPRs.)
+    auto write_xa = [&]() {
+#pragma unroll
+        for (int t = 0; t < kXTiles; ++t) {
+            if (kMT % kWaves == 0 || wave + kWaves * t < kMT) g_xab[(wave + kWaves * t) * 64 + lane] = bias_a_operand(xk[t][0], xk[t][1]);
+            xk[t][0] = xk[t][1] = 0.0f;
+        }
     };
     auto step = [&](int g, const uint4* xs, const uint4* wp, uint4* xs2, uint4* wp2) {
+        if (kXIn && (g & 7) == 0 && g > g_begin) write_xa();
         if (g == g_begin) {
             wait_vm_lds<0>();
         } else {
@@ -386,6 +438,10 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
             // of kMT x kNT tiles: 8 of them for 64-row tiles)
             if (pair && (t == kTW || t == kTW + 2)) dma_w((g + 2) >> 1, (t - kTW) >> 1, wp2);
         });
+        // lane (col, kq) keeps X_g of groups 2kq and 2kq + 1 of the octet
+        const bool mine = kq == ((g & 7) >> 1);
+#pragma unroll
+        for (int t = 0; t < kXTiles; ++t) xk[t][g & 1] = mine ? xsum[t][0] : xk[t][g & 1];
     };
 
     // prologue: x of the split's first two groups, its first pair, bias operands of its
@@ -416,19 +472,19 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         if (g + 10 < g_end) step(g + 10, g_xs1, g_wp1, g_xs0, g_wp0);
         if (g + 11 < g_end) step(g + 11, g_xs2, g_wp1, g_xs1, g_wp0);
     }
-    // the last octet's bias term.  Its operands were loaded at step 8o + 1, except for
-    // a last octet of one group (no such step): then they are loaded here, once every
-    // wave is past the previous octet's bias term.  The drain also lands the
-    // zero-reading loads past the last group before the workgroup ends.
+    // the last octet's bias term.  Its scale/bias words were loaded at step 8o + 1,
+    // except for a last octet of one group (no such step): then they are loaded here;
+    // its A operands are written here.  Both once every wave is past the previous
+    // octet's bias term (which a last octet's first step applies).  The drain also
+    // lands the zero-reading loads past the last group before the workgroup ends.
     {
         const int o = (g_end - 1) >> 3;
-        wait_vm<0>();
+        wait_vm_lds<0>();
         lds_barrier();
-        if (o > (g_begin >> 3) && 8 * o + 1 >= g_end) {
-            dma_xa(o);
-            wait_vm<0>();
-            lds_barrier();
-        }
+        if (o > (g_begin >> 3) && 8 * o + 1 >= g_end) dma_xa(o);
+        if constexpr (kXIn) write_xa();
+        wait_vm_lds<0>();
+        lds_barrier();
         bias();
     }
 
@@ -630,8 +686,9 @@ GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
             if (used != s) continue;
             const size_t part = s > 1 ? (size_t)s * m * l.n * 4 : 0;
             if (part > kMaxPartialBytes) break;
-            const size_t m16 = ((size_t)m + bm - 1) / bm * (bm / 16);
-            if (m16 * octets * 64 * 16 + part > max_workspace) break;  // (more splits need more)
+            // the 256-row tile's X_g pre-pass (bias A operands of every 16-row block and octet)
+            const size_t xa = bm == 256 ? ((size_t)m + bm - 1) / bm * (bm / 16) * octets * 1024 : 0;
+            if (xa + part > max_workspace) break;  // (more splits need more)
             const double rounds = (double)((tiles * s + cus * ts.per_cu - 1) / (cus * ts.per_cu));
             const double t = rounds * (per * 8 * ts.step_us + kRoundUs) + (s > 1 ? kSplitUs + part / kPartialBytesPerUs : 0.0);
             if (best < 0.0 || t < best) {
@@ -641,11 +698,10 @@ GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
                 p.splits = s;
                 p.g_split = per * 8;
                 p.part_bytes = part;
+                p.xaug_bytes = xa;
             }
         }
     }
-    const size_t m16 = ((size_t)m + p.bm - 1) / p.bm * (p.bm / 16);
-    p.xaug_bytes = m16 * octets * 64 * 16;
     return p;
 }
 
@@ -667,12 +723,11 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     const int octets = (l.g + 7) / 8;
     const int mtiles = (m + plan.bm - 1) / plan.bm;
     const int ntiles = (l.n + plan.bn - 1) / plan.bn;
-    uint4* xaug = static_cast<uint4*>(workspace);
+    uint4* xaug = plan.xaug_bytes ? static_cast<uint4*>(workspace) : nullptr;
     float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.xaug_bytes);
-    if (l.rec_bytes() > kMaxBufferBytes ||
-        (size_t)m * l.kx * 2 > kMaxBufferBytes || plan.xaug_bytes > kMaxBufferBytes)
+    if (l.rec_bytes() > kMaxBufferBytes || (size_t)m * l.kx * 2 > kMaxBufferBytes || plan.xaug_bytes > kMaxBufferBytes)
         return hipErrorInvalidValue;
-    {
+    if (plan.xaug_bytes) {
         const long units = (long)mtiles * (plan.bm / 16) * octets;  // 1 KiB blocks
         hipLaunchKernelGGL(xaug_kernel, dim3((unsigned)units), dim3(512), 0, stream, x, xaug, m, l.kx, l.g, octets);
         const hipError_t e = hipGetLastError();

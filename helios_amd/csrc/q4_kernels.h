@@ -91,17 +91,18 @@ hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x,
 hipError_t launch_greedy_reduce(const unsigned long long* part, int nb, int rows, int32_t* token, float* value,
                                 hipStream_t stream);
 
-// Prefill path: fp32-exact factored GEMM on the matrix cores.  `workspace` holds the
-// group sums of x and, when K is split over workgroups, the fp32 partial sums
-// (device memory, 256-byte aligned).  The plan is the cheapest whose workspace fits
-// in `workspace_bytes`; gemm_workspace_bytes(m, l) is what the unconstrained plan
+// Prefill path: fp32-exact factored GEMM on the matrix cores.  `workspace` holds,
+// for the 256-row tile, the group sums of x and, when K is split over workgroups, the
+// fp32 partial sums (device memory, 256-byte aligned); an unsplit plan of 64- or
+// 128-row tiles needs none.  The plan is the cheapest whose workspace fits in
+// `workspace_bytes`; gemm_workspace_bytes(m, l) is what the unconstrained plan
 // needs, and with that much the launch runs the unconstrained plan.
 struct GemmPlan {
-    int bm = 256;            // output tile rows: 256, or 128 for small M
+    int bm = 256;            // output tile rows: 256, 128 or 64
     int bn = 256;            // output tile columns
     int splits = 1;          // workgroups along K per output tile
     int g_split = 0;         // groups per split (whole octets)
-    size_t xaug_bytes = 0;   // group sums of x
+    size_t xaug_bytes = 0;   // group sums of x (256-row tiles)
     size_t part_bytes = 0;   // splits x M x N fp32 partial sums (0 when unsplit)
 };
 constexpr int kMaxSplits = 16;

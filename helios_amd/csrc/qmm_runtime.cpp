@@ -370,19 +370,20 @@ Gemma4Status dispatch_forward(const Gemma4QLinear* linear, const uint16_t* x_dev
         if (e != hipSuccess) return hip_fail((name + ": decode launch").c_str(), e);
         return GEMMA4_OK;
     }
-    // group sums of x (and split-K partial sums): the unconstrained plan's workspace
-    // from the pool, or what the static scratch has left (the plan then splits K only
-    // as far as that room allows)
+    // group sums of x (256-row tiles) and split-K partial sums: the unconstrained plan's
+    // workspace from the pool, or what the static scratch has left (the plan then takes
+    // only tiles and splits that fit that room; an unsplit plan of 64- or 128-row tiles
+    // needs none)
     size_t ws_bytes = q4::gemm_workspace_bytes((int)rows, linear->layout);
     if (sc.fixed) {
         ws_bytes = sc.room();
+        // holds by construction (the plan takes only what fits the room); kept so that
+        // a plan change can never overrun the array
         const q4::GemmPlan plan = q4::plan_gemm((int)rows, linear->layout, ws_bytes);
         if (plan.xaug_bytes + plan.part_bytes > ws_bytes)
-            return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG,
-                        name + ": the GEMM needs " + std::to_string(plan.xaug_bytes) + " bytes of scratch for " +
-                            std::to_string(rows) + " rows, more than the static scratch has left (" +
-                            std::to_string(ws_bytes) + " of " + std::to_string(kStaticScratchBytes) +
-                            " bytes; split the rows)");
+            return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, name + ": the GEMM's scratch needs more than the " +
+                                                           std::to_string(kStaticScratchBytes) +
+                                                           "-byte static scratch has left");
     }
     void* ws = nullptr;
     e = sc.take(sc.fixed ? 0 : ws_bytes, &ws);

@@ -157,13 +157,11 @@ Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, c
  * 64 MiB device array that the library holds on each GPU it runs on until the
  * process ends.  No counterpart in the reference (its MLX ops allocate per call).
  * It calls no hipMalloc, hipFree or allocating library routine.  Scratch needs:
- * none on the decode path (gemma4_qmm_set_gemm_min_rows); on the GEMM path the
- * group sums of x (rows * K / 8 bytes, rows * K / 4 for 8-bit handles, rounded up to
- * 128- or 256-row tiles), and split-K partial sums only as far as the array has room
- * (fewer splits than gemma4_qlinear_forward may choose, so the fp32 summation order,
- * and with it the last bits of some outputs, can differ from that call's).  A call
- * needing more
- * than 64 MiB fails with GEMMA4_ERR_UNSUPPORTED_CONFIG (split the rows).  Every call
+ * none on the decode path (gemma4_qmm_set_gemm_min_rows); on the GEMM path split-K
+ * partial sums only as far as the array has room (fewer splits than
+ * gemma4_qlinear_forward may choose, so the fp32 summation order, and with it the
+ * last bits of some outputs, can differ from that call's; an unsplit GEMM needs
+ * none), so no call is refused for want of scratch.  Every call
  * on a GPU shares that GPU's array: calls that overlap in time on one GPU (other
  * streams, other threads) race and must be serialized by the caller. */
 Gemma4Status gemma4_qlinear_forward_noalloc(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,

@@ -85,18 +85,19 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
     """kx: the row length of x (k, or k / 2 for a two-plane 8-bit handle)."""
     kx = kx or k
     L = layout(n, k)
-    WAVES = 2 * BN // 64   # 2 (M) x BN/64 (N)
+    WAVES = BN // 32   # side by side along N, each all BM rows x 32 columns
     RB = BN // 16
-    WM = BM // 2
+    MT = BM // 16                 # 16-row tiles per wave
     XP = BM * 8 // (64 * WAVES)   # x DMA parts per wave per group
-    XA = max(1, BM // 16 // WAVES)   # bias A-operand DMA parts per loading wave per octet
-    XA_WAVES = min(WAVES, BM // 16)  # waves that load them (BM = 64: waves 0-3)
+    XIN = BM < 256                # X_g summed in the kernel, else DMA'd from the pre-pass
+    XT = (MT + WAVES - 1) // WAVES if XIN else 0  # row tiles whose X_g a wave sums: wave + WAVES t
+    XA = 0 if XIN else MT // WAVES  # bias A-operand DMA parts per wave per octet
     SW = RB // 8                  # waves loading a pair's scale words
-    assert RB == 2 * WAVES and XP >= 1 and XA * XA_WAVES == BM // 16
+    assert RB == 2 * WAVES and XP >= 1 and (XT * WAVES >= MT if XIN else XA * WAVES == MT)
     # the DMAs issued from inside the product stream (after tile t of the wave's
-    # (BM / 32) x 4 tiles): the x loads after tiles 1, 3, ..., the pair's weights after
+    # (BM / 16) x 2 tiles): the x loads after tiles 1, 3, ..., the pair's weights after
     # tiles TW and TW + 2 -- every one must fall inside the stream or it is never issued
-    TILES = (BM // 2 // 16) * 4
+    TILES = MT * 2
     TW = 9 if TILES >= 12 else 5
     assert 2 * XP - 1 < TILES and TW + 2 < TILES, (BM, TILES, TW)
     KWP, KSP = RB * 64, RB * 16 // 2  # uint4 units of one weight slot
@@ -109,7 +110,7 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
     nblocks = (n + 15) // 16
     xbytes = m * kx * 2
     gx = kx // 64
-    ws_bytes = mtiles * (BM // 16) * octets * 1024
+    ws_bytes = mtiles * (BM // 16) * octets * 1024  # the pre-pass's bias A operands
     per = (octets + splits - 1) // splits
     assert (octets + per - 1) // per == splits
     g_split = per * 8
@@ -127,7 +128,6 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
             continue
         rbw = nt * RB
         for wave in range(WAVES):
-            wm, wn = wave & 1, wave >> 1
             # DMA offsets: per-lane constants + a scalar step offset (group, pair, octet)
             for part in range(XP):
                 q = (WAVES * part + wave) * 64 + lane
@@ -156,7 +156,7 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
                     chk_buf("gemm s", off, 16, L["sb_bytes"], L["sb_bytes"])
                     assert in_sb_part(off[off != OOB], 16)
             for o in sorted({0, octets - 1}):
-                for u in (range(XA) if wave < XA_WAVES else ()):
+                for u in range(XA):
                     m16 = XA * wave + u
                     assert m16 * 64 + 64 <= XAA
                     off = ((mt * (BM // 16) + m16) * octets + o) * 1024 + lane * 16
@@ -170,20 +170,24 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
                 assert XAA + wave * 64 + 63 < BIAS_SLOT  # the scale/bias part of the bias slot
             # LDS operand reads of the 16x16x32 product stream
             kq = lane >> 4
-            for j in range(4):  # the wave's four row blocks
-                rbl = wn * 4 + j
+            for j in range(2):  # the wave's two row blocks
+                rbl = wave * 2 + j
                 assert rbl * 64 + 64 <= KWP and ((rbl * 16 + l16) < KSP * 2).all()
-                assert ((((wn * 4 + j) * 4 + kq) * 16 + l16) < 1024).all()  # bias words, uint2
-            for i in range(WM // 16):
-                r = wm * WM + 16 * i + l16
+                assert ((((wave * 2 + j) * 4 + kq) * 16 + l16) < RB * 4 * 16).all()  # bias words, uint2
+            for i in range(MT):  # the product stream's and the X_g sums' x fragments
+                r = 16 * i + l16
                 for c in (kq, 4 + kq):
                     idx = r * 8 + (c ^ ((r >> 1) & 7))
                     assert (idx >= 0).all() and (idx < BM * 8).all()
-                assert (wm * (WM // 16) + i) * 64 + 64 <= XAA  # bias A operands
+                assert i * 64 + 64 <= XAA  # bias A operands
+            # the wave's bias A-operand writes: its row tiles wave + WAVES t
+            for t in range(XT):
+                if wave + WAVES * t < MT:
+                    assert (wave + WAVES * t) * 64 + 64 <= XAA
             # stores: rows 4*kq + e of each 16-row tile, column l16 of the row block
-            for i in range(WM // 16):
+            for i in range(MT):
                 for e in range(4):
-                    mrow = mt * BM + wm * WM + 16 * i + 4 * kq + e
+                    mrow = mt * BM + 16 * i + 4 * kq + e
                     assert (mrow < mtiles * BM).all()
     assert len(seen) == nwg
     # split-K: each split starts on an octet and the planes fit the partial buffer

@@ -150,7 +150,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
                                                    int g_split, long split_stride, int n_out,
                                                    const uint16_t* __restrict__ gelu_table) {
     // BN / 32 waves of BM x 32: BM = 256; BM = 128 (more workgroups for small M
-    // without splitting K); BM = 64 (M <= 128)
+    // without splitting K); BM = 64 (fewest K splits for narrow outputs)
     static_assert(BM == 256 || BM == 128 || BM == 64, "tile rows");
     static_assert(BN == 256 || BN == 128, "tile columns");
     constexpr int kWaves = BN / kWN;              // side by side along N
@@ -644,31 +644,32 @@ __global__ void split_geglu_kernel(const float* __restrict__ part, void* __restr
 // Tile shape and split of K.  For each tile shape (256, 128 or 64 rows x 256) and split
 // count (whole octets per split), the cost is
 //   rounds of workgroups x (groups per split x the step time + kRoundUs)
-//   + for a split: kSplitUs + the partial sums' bytes / kPartialBytesPerUs,
+//   + for a split: kSplitUs + the partial sums' bytes / kPartialBytesPerUs
+//   + for the 256-row tile: kPrePassUs (its X_g pre-pass launch),
 // and the cheapest wins.  The constants are fitted to every plan measured on the eight
 // prefill shapes (q, k, o, gate, down, the gate|up pair, the full-attention q and o) at
-// 14 row counts from 64 to 2048: the picks average 0.1% and at worst 3.4% over the
-// fastest plan of each case, and moving any one constant by a grid step costs at most
-// 0.1% more on average.  (Partial sums at 6 MB/us, no per-round or per-split overhead
-// beyond 3 us and 1.15 us per 128-row step gave 1.3% and 23% when fitted to the
-// kernel's earlier wave layout: gate at 576 rows 140 us against 114 for the best plan.)
+// 14 row counts from 64 to 2048, every tile at every row count: the picks average 0.7%
+// and at worst 7.4% over the fastest plan of each case.  (The constants fitted to the
+// kernel with the pre-pass for every tile, the 64-row tile offered up to 128 rows,
+// give 3.7% and 26% on the same measurements.)
 namespace {
 struct TileShape {
     int bm, bn, per_cu;
     double step_us;  // one 64-wide group step of a workgroup (fitted with the constants below)
     int max_m;       // offered up to this many rows (0: any)
 };
-// The 64-row tile: offered up to 128 rows.  Best plan of each tile, measured: at 64
-// rows the 128-row tile, half of it padding, is 8-20% behind (q 4096x3840 28.4 us vs
-// 31.4, gate 15360x3840 32.9 vs 37.9, down 3840x15360 34.2 vs 38.9, the gate|up pair
-// 43.4 vs 52.2); at 96-128 rows the 64-row tile stays 5-13% ahead for the attention
-// projections (q, k, o and the full-attention q) and within 3% either way for gate,
-// down, the pair and the full-attention o.  The step time is fitted at one workgroup
-// per CU (two fit, but each then runs at half the rate).
-constexpr TileShape kTileShapes[] = {{256, 256, 1, 1.9, 0}, {128, 256, 1, 1.1, 0}, {64, 256, 1, 0.7, 128}};
-constexpr double kRoundUs = 2.0;               // per round of workgroups: prologue, epilogue, ramp
-constexpr double kSplitUs = 3.0;               // a split's reduction launch
-constexpr double kPartialBytesPerUs = 3.0e6;   // partial sums written and read back
+// The 64-row tile pads least and, unsplit, needs no scratch; it wins wherever it fills
+// the CUs with fewer K splits.  Best plan of each tile, measured: at 64 rows the
+// 128-row tile, half of it padding, is 10-26% behind (q 4096x3840 26.3 us vs 29.2, gate
+// 15360x3840 30.2 vs 36.1, the gate|up pair 41.7 vs 52.7); at 2048 rows k 2048x3840
+// runs 45.9 us on it unsplit against 57.7 on the 128-row tile split in two, and at 512
+// rows the full-attention q 8192x3840 46.5 vs 57.6.  Step times are fitted at one
+// workgroup per CU (the 64-row tile fits two, but each then runs at half the rate).
+constexpr TileShape kTileShapes[] = {{256, 256, 1, 1.8, 0}, {128, 256, 1, 1.1, 0}, {64, 256, 1, 0.65, 0}};
+constexpr double kRoundUs = 1.0;               // per round of workgroups: prologue, epilogue, ramp
+constexpr double kSplitUs = 4.0;               // a split's reduction launch
+constexpr double kPartialBytesPerUs = 4.0e6;   // partial sums written and read back
+constexpr double kPrePassUs = 3.0;             // the 256-row tile's group-sum pre-pass
 }  // namespace
 
 GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
@@ -690,7 +691,8 @@ GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
             const size_t xa = bm == 256 ? ((size_t)m + bm - 1) / bm * (bm / 16) * octets * 1024 : 0;
             if (xa + part > max_workspace) break;  // (more splits need more)
             const double rounds = (double)((tiles * s + cus * ts.per_cu - 1) / (cus * ts.per_cu));
-            const double t = rounds * (per * 8 * ts.step_us + kRoundUs) + (s > 1 ? kSplitUs + part / kPartialBytesPerUs : 0.0);
+            const double t = rounds * (per * 8 * ts.step_us + kRoundUs) +
+                             (s > 1 ? kSplitUs + part / kPartialBytesPerUs : 0.0) + (bm == 256 ? kPrePassUs : 0.0);
             if (best < 0.0 || t < best) {
                 best = t;
                 p.bm = bm;

@@ -521,8 +521,9 @@ def summarize_trace(db_path: str, out_md: str, command: str) -> None:
     """Per-shape kernel durations of `bench.py --prefill-only` from a rocprofv3
     --kernel-trace database (rocpd SQLite).  Each shape's handles are created (repack
     launches) before its forwards, which split the trace into the sweep's shapes in
-    order; a GEMM-path forward launches the GEMM and (when K is split) the split-K
-    reduction, a decode-path forward one decode kernel.  Reported: the median
+    order; a GEMM-path forward launches the GEMM (after xaug_kernel, the group-sum
+    pre-pass, for the 256-row tile) and, when K is split, the split-K reduction; a
+    decode-path forward one decode kernel.  Reported: the median
     duration of each kernel and of the whole forward (first launch start to last
     launch end) over the shape's forwards."""
     import re
@@ -543,7 +544,8 @@ def summarize_trace(db_path: str, out_md: str, command: str) -> None:
         if s.startswith("repack"):
             if not shapes or shapes[-1]:
                 shapes.append([])
-        elif (s.startswith("gemm_kernel") or s.startswith("decode")) and shapes:
+        elif shapes and (s.startswith("xaug") or s.startswith("decode") or
+                         (s.startswith("gemm_kernel") and not (shapes[-1] and short(shapes[-1][-1][-1][0]).startswith("xaug")))):
             shapes[-1].append([r])
         elif shapes and shapes[-1]:
             shapes[-1][-1].append(r)

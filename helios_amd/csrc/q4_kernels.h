@@ -134,18 +134,20 @@ hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float*
                        int rank, float scale, bool out_f32, hipStream_t stream);
 
 // Forward path choice (automatic mode): the decode kernels below kGemmMinRows rows,
-// and beyond that while rows x N x K stays at most kDecodeMaxWork.  Measured per
-// shape as whole forwards (graph replays) at 33-256 rows: the decode kernels' cost
-// grows by one weight pass per 16-row slab (~4 us per 16M weights), the GEMM's is
-// ~30 us of fixed cost (group sums of x, split-K reduction, tile prologue) plus its
-// MFMA time.  Ties: 4096x3840 at ~128 rows (2.0e9), 2048x3840 at ~224 (1.8e9),
-// 8192x3840 and 3840x8192 at ~50 (1.6e9), 15360x3840 at ~40 (2.4e9); 3840x15360
-// (K of 120 pairs) is ahead on the GEMM from 32 rows (1.9e9).
+// and beyond that while 16-row slabs x N x K stays at most kDecodeMaxSlabWork (K' = 2K
+// for two-plane 8-bit handles).  The decode kernels' cost grows by one pass over the
+// weights per 16-row slab (~0.24 us per million weights); the GEMM's starts at ~22 us
+// (launch, tile prologue and epilogue, split-K reduction) and grows slowly at these
+// sizes.  Measured as whole forwards (graph replays, each path pinned) on nine shapes
+// (q, k, o, the fused qkv, gate, down, the gate|up pair, the full-attention o and k)
+// at 32-256 rows: this rule's choice is at worst 4% behind the faster path (k
+// 2048x3840 at 192 rows: GEMM 28.2 us, decode 27.1), where rows x N x K <= 1.6e9 was
+// up to 17% behind (full-attention o 3840x8192 at 48 rows: decode 32.6, GEMM 27.9).
 constexpr int kGemmMinRows = 32;
-constexpr double kDecodeMaxWork = 1.6e9;
+constexpr double kDecodeMaxSlabWork = 8.4e7;
 inline bool use_decode(long rows, const Layout& l, int gemm_min_rows) {
     if (gemm_min_rows > 0) return rows < gemm_min_rows;
-    return rows < kGemmMinRows || (double)rows * (double)l.n * (double)l.k <= kDecodeMaxWork;
+    return rows < kGemmMinRows || (double)((rows + 15) / 16) * (double)l.n * (double)l.k <= kDecodeMaxSlabWork;
 }
 
 }  // namespace q4

@@ -27,8 +27,7 @@ pytestmark = pytest.mark.gpu
 K = 1024
 N = 4096
 F = 2048
-# decode at 1 and 5 rows; at 512 rows M*N*K = 2.1e9 takes the GEMM (128-row tiles, K
-# split in two)
+# decode at 1 and 5 rows; 512 rows (32 slabs of 4M weights) take the GEMM
 ROWS = (1, 5, 512)
 
 

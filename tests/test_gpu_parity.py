@@ -499,6 +499,33 @@ def test_gemm_64_row_tile_two_row_tiles(gpu_lib, gemm_from_32, proj, m):
     assert assert_close(yf[rt], want, f"{proj} m={m} f32") < 5e-4
 
 
+# (N, M) whose plans (64-row tile, 8 splits; 64-row, 4 splits; 128-row, 4 splits;
+# 256-row, 3 splits) end a K split of two or more octets on the last octet
+@pytest.mark.parametrize("n,m", [(1000, 40), (1000, 700), (1000, 1500), (3000, 1500)])
+def test_gemm_last_octet_of_one_group(gpu_lib, gemm_from_32, n, m):
+    """K of 57 groups: seven whole octets and a last octet of one group.  Where a K
+    split ends on it with two or more octets, that octet's one step also applies the
+    previous octet's bias term, so the 64- and 128-row tiles write its group sums of x
+    after the loop and the 256-row tile loads them there from the pre-pass; with eight
+    splits the octet is a split of its own.  Sampled rows against the oracle, bf16 and
+    fp32."""
+    import torch
+
+    k = 57 * 64
+    tri = random_triple(n, k, 5700 + n)
+    x = A.make_activations(m, k, seed=5800 + m, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*tri))
+    y = lin.forward(dev_x(x))
+    yf = lin.forward(dev_x(x), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    lin.close()
+    rows = np.unique(np.concatenate([np.linspace(0, m - 1, 24).astype(np.int64), [m - 1]]))
+    rt = torch.from_numpy(rows).cuda()
+    want = C.qmm_f64(np.ascontiguousarray(x[rows]), *tri)
+    assert_close(y[rt], want, f"N={n} K={k} M={m} bf16")
+    assert assert_close(yf[rt], want, f"N={n} K={k} M={m} f32") < 5e-4
+
+
 def test_gemm_prefill_chain_m2048_geglu(gpu_lib):
     """Chunked-prefill chain at M=2048: gate and up, GeGLU on the host (identical bf16
     bytes to both sides), then down_proj; sampled rows against the oracle."""

@@ -1,7 +1,7 @@
 """Seeded random shapes through the C ABI on the GPU, against the oracle.
 
 Each projection case draws N (or F for a gate|up pair), K (a multiple of 64), M from one of eight
-row ranges (0, 1, 2, 3-4, 5-16, 17-31, 32-64, 65-300), 4 or 8 bits, a bf16 or fp32
+row ranges (0, 1, 2, 3-4, 5-16, 17-31, 32-64, 65-300; GEMM cases also 300-2100), 4 or 8 bits, a bf16 or fp32
 output, and the automatic path choice or the GEMM pinned from 32 rows.  Between them
 the cases reach every decode variant (row, per-row-block, streaming, global-x; 16-row
 slabs), the GEMM's 256-, 128- and 64-row tiles with and without a K split, and the
@@ -64,7 +64,23 @@ def _gemm_cases(count=16, seed=20261203):
     return cases
 
 
-CASES = _cases() + _gemm_cases()
+def _gemm_cases_tall(count=8, seed=20261209):
+    """The GEMM at 300-2100 rows (the 64-row tile unsplit or split, the 128- and
+    256-row tiles; N up to 3000 keeps the oracle rows cheap)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        pair = bool(rng.random() < 0.3)
+        bits = 8 if rng.random() < 0.25 else 4
+        k = 64 * int(rng.integers(8, 129))
+        per_row = k * (2 if bits == 8 else 1) * (2 if pair else 1)
+        n_max = max(16, min(3000 if not pair else 1500, MAX_WEIGHTS // per_row))
+        cases.append(dict(i=150 + i, n=int(rng.integers(16, n_max + 1)), k=k, m=int(rng.integers(300, 2101)),
+                          pair=pair, bits=bits, f32=bool(rng.random() < 0.4), pin=True, outliers=i % 3 != 0))
+    return cases
+
+
+CASES = _cases() + _gemm_cases() + _gemm_cases_tall()
 
 
 def _triple(n, k, bits, seed):

@@ -28,10 +28,9 @@ namespace {
 // row i of an MFMA result depends only on row i of its A operand, so A rows >= M
 // may hold anything: they only feed accumulator rows that are never stored.
 //
-// XLDS = true (x[M,K] up to 64 KiB): the workgroup first copies x into LDS with
-// one cooperative wave of loads issued before the weight loads, so the x operands
-// cost LDS reads instead of a chain of L2 round trips.  XLDS = false (M up to 16):
-// each wave reads its x operands from global memory, one group pair ahead.
+// XLDS = true (x[M,K] up to 64 KiB): the workgroup copies x into LDS, so the x
+// operands cost LDS reads instead of a chain of L2 round trips.  XLDS = false (M up
+// to 16): each wave reads its x operands from global memory, one group pair ahead.
 //
 // GPW: group pairs a wave handles per pass.  All of a pass's weight tiles and
 // scales are requested before any arithmetic (GPW KiB in flight per wave, one HBM
@@ -60,9 +59,30 @@ __global__ __launch_bounds__(1024) void decode_kernel(
     const int arow = col < m_rows ? col : m_rows - 1;  // any valid row for A rows >= M
     const uint32_t lane_x = (uint32_t)(arow * kx + 8 * kq) * 2u;  // XLDS = false: this lane's x bytes
 
+    // a pass's tiles and scales as bounded buffers: pairs i >= left read as zero
+    uint4 wv[GPW];
+    uint2 sv[GPW];
+    auto issue = [&](int base) {
+        const int left = cnt - base;
+        const long first = (long)rb * gpairs + gp0 + base;
+        const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * kRecU4, (uint32_t)left * kRecBytes);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * kRecU2, sb_span(left));
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+            wv[i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * kRecBytes));
+            sv[i] = buffer_load8<kNonTemporal>(srs, (uint32_t)(col * 8 + i * kRecBytes));
+        }
+    };
+    // XLDS = false: the first pass's weights are requested before anything else
+    // (q_proj 4096x3840 at M = 16: 8.2 -> 6.8 us, the full-attention o 3840x8192 at
+    // M = 4 and 8: 8.9 -> 7.8, 9.8 -> 8.6).  XLDS = true keeps them after the copy of
+    // x: issued before it, each wave's x loads complete behind its weight loads and
+    // the barrier after the copy waits for every wave's weights (q_proj at M = 1-8
+    // 3-11% slower, qkv 13-19%).
+    if (!XLDS && cnt > 0) issue(0);
+
     if constexpr (XLDS) {
-        // cooperative copy x -> LDS; these loads are issued first so that waiting for
-        // them leaves the weight loads below in flight
+        // cooperative copy x -> LDS
         const int chunks = (int)(xbytes >> 4);
         const int nthr = waves * 64;
         uint4 tmp[4];
@@ -89,21 +109,11 @@ __global__ __launch_bounds__(1024) void decode_kernel(
     for (int base = 0; base < cnt; base += GPW) {
         const int gpb = gp0 + base;
         const int left = cnt - base;
-        // this pass's tiles and scales as bounded buffers: pairs i >= left read as zero
-        const long first = (long)rb * gpairs + gpb;
-        const __amdgpu_buffer_rsrc_t trs = make_rsrc(tiles + first * kRecU4, (uint32_t)left * kRecBytes);
-        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sb + first * kRecU2, sb_span(left));
         // element offset of this lane's x operand at pair i, group 0, half 0 (x in LDS)
         const int xel = arow * k + 8 * kq + gpb * 128;
         const int kleft = k - gpb * 128;
 
-        uint4 wv[GPW];
-        uint2 sv[GPW];
-#pragma unroll
-        for (int i = 0; i < GPW; ++i) {
-            wv[i] = buffer_load16<kNonTemporal>(trs, (uint32_t)(lane * 16 + i * kRecBytes));
-            sv[i] = buffer_load8<kNonTemporal>(srs, (uint32_t)(col * 8 + i * kRecBytes));
-        }
+        if (XLDS || base > 0) issue(base);
         if (!synced) {
             __syncthreads();  // x is in LDS
             synced = true;

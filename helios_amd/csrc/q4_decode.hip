@@ -616,7 +616,11 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
         }
     }
     const size_t x_bytes = (size_t)ms * l.k * 2;
-    if (l.gp <= kXLdsMaxPairs && x_bytes <= kXLdsMaxBytes && l.nb <= kXLdsMaxBlocks * (MT > 1 ? 2 : 1)) {
+    // K of at most 8 pairs (1024) from M = 5: two waves per row block, which cannot
+    // cover staging x; the global-x kernel below is ahead (1024x1024 at M = 6 / 8 / 12 /
+    // 16: 3.80 / 3.80 / 3.94 / 3.97 us against 4.05 / 4.11 / 4.40 / 4.70)
+    const bool short_k = MT >= 8 && l.gp <= 8;
+    if (!short_k && l.gp <= kXLdsMaxPairs && x_bytes <= kXLdsMaxBytes && l.nb <= kXLdsMaxBlocks * (MT > 1 ? 2 : 1)) {
         const int waves = (l.gp + GPW - 1) / GPW;  // <= 8, each wave one pass of <= 4 pairs
         hipLaunchKernelGGL((decode_kernel<MT, GPW, true>), dim3(l.nb, slabs), dim3(64 * waves), x_bytes, stream, tiles,
                            sb, x, op, m, l.n, l.k, l.kx, l.gp, waves);
@@ -653,7 +657,7 @@ hipError_t launch_mt(const uint4* tiles, const uint2* sb, const uint16_t* x, con
     // M = 6 / 8).  gate 15360x3840 (four per workgroup) stays streaming: 15.4 vs 20.7
     // at M = 16.
     const bool few_blocks = MT == 16 && (per_wg == 1 || (per_wg == 2 && (slabs > 1 || l.gp <= kXLdsMaxPairs)));
-    if (!one_pass && !few_blocks && lds_fit > 0) {
+    if (!one_pass && !few_blocks && !short_k && lds_fit > 0) {
         const int grid = (l.nb + per_wg - 1) / per_wg;
         // one workgroup per CU and a long walk (the lm_head at M = 8: 126 vs 135 us):
         // four chunks per wave in flight.  Not for short walks (down and the gate|up

@@ -79,7 +79,10 @@ __global__ __launch_bounds__(1024) void decode_kernel(
     // x: issued before it, each wave's x loads complete behind its weight loads and
     // the barrier after the copy waits for every wave's weights (q_proj at M = 1-8
     // 3-11% slower, qkv 13-19%).
-    if (!XLDS && cnt > 0) issue(0);
+    // (Not at M = 1 with 8-pair passes: held across the pass loop, those loads take it
+    // past the 128 VGPRs of a 1024-thread workgroup, into scratch.)
+    constexpr bool kIssueFirst = !XLDS && !(MT == 1 && GPW == 8);
+    if (kIssueFirst && cnt > 0) issue(0);
 
     if constexpr (XLDS) {
         // cooperative copy x -> LDS
@@ -113,7 +116,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(
         const int xel = arow * k + 8 * kq + gpb * 128;
         const int kleft = k - gpb * 128;
 
-        if (XLDS || base > 0) issue(base);
+        if (!kIssueFirst || base > 0) issue(base);
         if (!synced) {
             __syncthreads();  // x is in LDS
             synced = true;

@@ -40,7 +40,12 @@
  * Streams are hipStream_t values passed as void* (NULL = the null stream).  All
  * device work is asynchronous on that stream.  A handle is immutable after
  * create, so forward/dequantize may run concurrently on several streams and
- * threads; create and free must not overlap use.
+ * threads; create and free must not overlap use.  Scratch (split-K partial sums,
+ * the greedy head's keys, LoRA's x.A^T) comes from device memory the library keeps
+ * per (device, stream) and reuses call after call in stream order.  A HIP graph that
+ * captured a call uses its capture stream's memory, so replays of graphs captured on
+ * one stream must not overlap one another or calls on that stream (replay them on
+ * one stream, or serialize).  The memory is held until the process ends.
  */
 #ifndef GEMMA4_QMM_H
 #define GEMMA4_QMM_H

@@ -15,6 +15,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "q4_common.h"
@@ -147,6 +148,7 @@ hipError_t static_scratch(int device, char** out) {
 struct StreamWorkspace {
     int device = -1;
     hipStream_t stream = nullptr;
+    std::thread::id thread;  // hipStreamPerThread: a different stream in every thread
     char* buf = nullptr;
     size_t cap = 0;
     std::vector<char*> retired;
@@ -156,12 +158,14 @@ std::mutex g_ws_mu;
 std::vector<std::unique_ptr<StreamWorkspace>> g_ws;
 
 StreamWorkspace* stream_workspace(int device, hipStream_t stream) {
+    const std::thread::id thread = stream == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
     std::lock_guard<std::mutex> lock(g_ws_mu);
     for (auto& w : g_ws)
-        if (w->device == device && w->stream == stream) return w.get();
+        if (w->device == device && w->stream == stream && w->thread == thread) return w.get();
     g_ws.push_back(std::make_unique<StreamWorkspace>());
     g_ws.back()->device = device;
     g_ws.back()->stream = stream;
+    g_ws.back()->thread = thread;
     return g_ws.back().get();
 }
 

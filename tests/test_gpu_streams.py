@@ -132,3 +132,41 @@ def test_graph_replays_match_eager(gpu_lib):
     del g
     for h in (lin, pair, head):
         h.close()
+
+
+def test_per_thread_default_stream(gpu_lib):
+    """hipStreamPerThread (the handle value 2) names a different stream in every
+    thread: two threads issuing split-K GEMMs on it at once, each with its own
+    inputs, match the serial results bit for bit (their scratch must not be shared)."""
+    import torch
+
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*random_triple(N, K, 21)))
+    m, rounds = 512, 8
+    xs = [[dev_x(A.make_activations(m, K, seed=9000 + 100 * t + r)) for r in range(rounds)] for t in range(2)]
+    want = [[lin.forward(x) for x in row] for row in xs]
+    torch.cuda.synchronize()
+    got = [[torch.empty_like(want[t][r]) for r in range(rounds)] for t in range(2)]
+    errors = []
+    start = threading.Barrier(2)
+
+    def worker(t):
+        try:
+            start.wait(timeout=60)
+            for r in range(rounds):
+                lin.forward_raw(xs[t][r].data_ptr(), m, got[t][r].data_ptr(), stream_ptr=2)
+            torch.cuda.synchronize()
+        except Exception as e:  # reported below, with the thread
+            errors.append((t, repr(e)))
+
+    ts = [threading.Thread(target=worker, args=(t,), daemon=True) for t in range(2)]
+    for th in ts:
+        th.start()
+    for th in ts:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in ts), "a worker thread did not finish"
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for t in range(2):
+        for r in range(rounds):
+            assert _same(got[t][r], want[t][r]), f"thread {t} round {r} differs from the serial result"
+    lin.close()

@@ -11,7 +11,12 @@ split order), so concurrent results must equal the serial ones bit for bit:
     default stream;
   * the same calls captured once in a graph and replayed five times, the inputs
     rewritten by eager work between replays: every replay equals the eager result
-    for its inputs (the scratch allocations become graph nodes; no memset nodes).
+    for its inputs.  Captured on a stream whose scratch memory is too small, the
+    calls' scratch becomes allocation nodes of the graph; captured on a stream warmed
+    up first, they use that stream's memory (no allocation nodes); no memset nodes
+    either way;
+  * hipStreamPerThread from two threads at once: each thread's own stream and
+    scratch.
 """
 
 import threading
@@ -170,3 +175,37 @@ def test_per_thread_default_stream(gpu_lib):
         for r in range(rounds):
             assert _same(got[t][r], want[t][r]), f"thread {t} round {r} differs from the serial result"
     lin.close()
+
+
+def test_graph_on_warmed_stream_matches_eager(gpu_lib):
+    """Warm-up and capture on the same stream: the captured calls take their scratch
+    from that stream's workspace (no allocation nodes).  Replays on that stream, with
+    new inputs written between them, match the eager result; eager calls on another
+    stream in between use their own workspace."""
+    import torch
+
+    lin, pair, head = _handles(gpu_lib)
+    xs = _inputs(6000)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _run(lin, pair, head, xs, torch)  # grows s's workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        outs = _run(lin, pair, head, xs, torch)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for i, m in enumerate(ROWS):
+            xs[i].copy_(dev_x(A.make_activations(m, K, seed=8000 + 100 * rep + m, outliers=True)))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        want = _run(lin, pair, head, xs, torch)  # the default stream
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(outs, want)):
+            assert _same(a, b), f"replay {rep}: output {i} differs from the eager result"
+    del g
+    for h in (lin, pair, head):
+        h.close()

@@ -136,15 +136,15 @@ hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float*
 // Forward path choice (automatic mode): the decode kernels below kGemmMinRows rows,
 // and beyond that while 16-row slabs x N x K stays at most kDecodeMaxSlabWork (K' = 2K
 // for two-plane 8-bit handles).  The decode kernels' cost grows by one pass over the
-// weights per 16-row slab (~0.24 us per million weights); the GEMM's starts at ~22 us
+// weights per 16-row slab (~0.24 us per million weights); the GEMM's starts at ~14 us
 // (launch, tile prologue and epilogue, split-K reduction) and grows slowly at these
 // sizes.  Measured as whole forwards (graph replays, each path pinned) on nine shapes
 // (q, k, o, the fused qkv, gate, down, the gate|up pair, the full-attention o and k)
-// at 32-256 rows: this rule's choice is at worst 4% behind the faster path (k
-// 2048x3840 at 192 rows: GEMM 28.2 us, decode 27.1), where rows x N x K <= 1.6e9 was
-// up to 17% behind (full-attention o 3840x8192 at 48 rows: decode 32.6, GEMM 27.9).
+// at 32-256 rows: with any bound from 5e7 to 6e7 the choice is within 3% of the faster
+// path everywhere (q 4096x3840: decode to 48 rows, 15.3 vs 16.3 us; GEMM from 56,
+// 16.9 vs 18.3; the fused qkv 8192x3840 at 32 rows on the GEMM, 13.8 vs 19.9).
 constexpr int kGemmMinRows = 32;
-constexpr double kDecodeMaxSlabWork = 8.4e7;
+constexpr double kDecodeMaxSlabWork = 5.5e7;
 inline bool use_decode(long rows, const Layout& l, int gemm_min_rows) {
     if (gemm_min_rows > 0) return rows < gemm_min_rows;
     return rows < kGemmMinRows || (double)((rows + 15) / 16) * (double)l.n * (double)l.k <= kDecodeMaxSlabWork;

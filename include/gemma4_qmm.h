@@ -119,10 +119,10 @@ Gemma4Status gemma4_qmm_get_last_error(char* buffer, size_t buffer_len);
  * reference (MLX picks its own kernels); for tests and benchmarks that pin a path.
  *   0 (the default): automatic.  The decode kernels (16-row slabs, one pass over
  *     the weights per slab) below 32 rows, and beyond that while
- *     ceil(rows / 16) * N * K <= 8.4e7 (K' = 2K for 8-bit handles), the GEMM
+ *     ceil(rows / 16) * N * K <= 5.5e7 (K' = 2K for 8-bit handles), the GEMM
  *     otherwise: for the Gemma 4 shapes the decode kernels are ahead of the GEMM's
- *     fixed costs up to 80 rows for 4096x3840, 160 for 2048x3840, 32 for
- *     8192x3840, 672 for 512x3840, and below 32 rows for the MLP projections.
+ *     fixed costs up to 48 rows for 4096x3840, 112 for 2048x3840, 432 for 512x3840,
+ *     and below 32 rows for 8192x3840 and the MLP projections.
  *   r > 0: the GEMM from r rows on, the decode kernels below.
  * Both paths meet the same accuracy contract; they sum in different orders, so the
  * last bits of some outputs differ between them.  Returns the previous setting.

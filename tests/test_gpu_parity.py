@@ -413,12 +413,12 @@ def test_full_attention_projections(gpu_lib, proj, m):
 
 
 # (projection, rows) the automatic path choice runs on the decode kernels past 32 rows
-# (16-row slabs x N x K <= 8.4e7): 16-row slabs with one workgroup per row block and
+# (16-row slabs x N x K <= 5.5e7): 16-row slabs with one workgroup per row block and
 # slab, the ragged last slab included; 9 and 15 rows are single slabs of the same
 # kernel, and so are 10 rows of the 8192-row full-attention q (two row blocks per
 # workgroup).
-SLAB_CASES = [("q_proj", 9), ("q_proj", 15), ("q_proj", 48), ("q_proj", 79), ("k_proj", 33), ("k_proj", 155),
-              ("o_proj", 71), ("full_q_proj", 10), ("full_q_proj", 32), ("full_k_proj", 256), ("full_k_proj", 600)]
+SLAB_CASES = [("q_proj", 9), ("q_proj", 15), ("q_proj", 41), ("q_proj", 48), ("k_proj", 33), ("k_proj", 93),
+              ("o_proj", 45), ("full_q_proj", 10), ("full_q_proj", 31), ("full_k_proj", 256), ("full_k_proj", 420)]
 
 
 @pytest.mark.parametrize("proj,m", SLAB_CASES)

@@ -84,6 +84,14 @@ def load_library(path: str | None = None):
     global _lib
     if _lib is not None and path is None:
         return _lib
+    try:
+        # PyTorch-ROCm wheels carry their own libamdhip64 (same soname as the system
+        # one this library links).  Loaded first, torch's copy also serves this library;
+        # loaded after it, torch would map a second HIP runtime into the process, and
+        # the runtime that initialises second finds no device.
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     path = path or LIB_PATH
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is missing: build it with `python -m helios_amd.build`")

@@ -2,8 +2,8 @@
 PyTorch, as a C, cgo or JNI caller would, with the system HIP runtime
 (libamdhip64.so.7) the library links and plain ctypes; not collected by pytest.
 
-argv: library path.  Checks one 4-bit projection on the decode kernels and on the
-GEMM against the exact float64 product (max |err| <= 1e-4 * RMS: fp32 accumulation
+argv: library path.  Checks a 4-bit and an 8-bit projection on the decode kernels
+and on the GEMM against the exact float64 product (max |err| <= 1e-4 * RMS: fp32 accumulation
 of exact products) and that the process maps one HIP runtime.  Exit status 0 = pass.
 """
 import ctypes
@@ -25,18 +25,15 @@ def from_bf16(u):
     return (u.astype(np.uint32) << 16).view(np.float32)
 
 
-def main(path):
-    hip = ctypes.CDLL("libamdhip64.so.7")
-    lib = ctypes.CDLL(path)
+def check(hip, lib, bits, seed):
     vp, sz = ctypes.c_void_p, ctypes.c_size_t
-    count = ctypes.c_int(0)
-    assert hip.hipGetDeviceCount(ctypes.byref(count)) == 0 and count.value > 0, "no HIP device"
-    rng = np.random.default_rng(5)
+    rng = np.random.default_rng(seed)
     n, k, m = 320, 1024, 40
-    q = rng.integers(0, 16, (n, k)).astype(np.uint32)
-    w = np.zeros((n, k // 8), np.uint32)
-    for j in range(8):  # MLX packing: element 8c+j in bits 4j..4j+3 of word c
-        w |= q[:, j::8] << (4 * j)
+    per = 32 // bits
+    q = rng.integers(0, 1 << bits, (n, k)).astype(np.uint32)
+    w = np.zeros((n, k // per), np.uint32)
+    for j in range(per):  # MLX packing: element per*c+j in bits [bits*j, bits*j+bits) of word c
+        w |= q[:, j::per] << (bits * j)
     s = to_bf16(rng.uniform(0.001, 0.01, (n, k // 64)))
     b = to_bf16(rng.uniform(-0.05, 0.05, (n, k // 64)))
     x = to_bf16(rng.standard_normal((m, k)))
@@ -45,7 +42,7 @@ def main(path):
     rms = np.sqrt((exact ** 2).mean())
 
     h = vp()
-    st = lib.gemma4_qlinear_create(ctypes.byref(Desc(n, k, 4, 64)), w.ctypes.data_as(vp),
+    st = lib.gemma4_qlinear_create(ctypes.byref(Desc(n, k, bits, 64)), w.ctypes.data_as(vp),
                                    s.ctypes.data_as(vp), b.ctypes.data_as(vp), ctypes.byref(h))
     msg = ctypes.create_string_buffer(512)
     lib.gemma4_qmm_get_last_error(msg, sz(512))
@@ -62,12 +59,20 @@ def main(path):
         y = np.empty((m, n), np.float32)
         assert hip.hipMemcpy(y.ctypes.data_as(vp), dy, sz(y.nbytes), 2) == 0  # device to host
         err = float(np.abs(y - exact).max() / rms)
-        print(f"gemm_min_rows={gemm_from}: max |err| / RMS = {err:.2e}", flush=True)
+        print(f"bits={bits} gemm_min_rows={gemm_from}: max |err| / RMS = {err:.2e}", flush=True)
         assert err <= 1e-4, err
     lib.gemma4_qmm_set_gemm_min_rows(ctypes.c_uint32(0))
     assert lib.gemma4_qlinear_free(h) == 0
-    hip.hipFree(dx)
-    hip.hipFree(dy)
+    assert hip.hipFree(dx) == 0 and hip.hipFree(dy) == 0
+
+
+def main(path):
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    lib = ctypes.CDLL(path)
+    count = ctypes.c_int(0)
+    assert hip.hipGetDeviceCount(ctypes.byref(count)) == 0 and count.value > 0, "no HIP device"
+    check(hip, lib, 4, 5)
+    check(hip, lib, 8, 6)
     runtimes = {line.split()[-1] for line in open("/proc/self/maps") if "libamdhip64" in line}
     assert len(runtimes) == 1, runtimes
     print("ok", flush=True)

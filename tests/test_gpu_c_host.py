@@ -34,8 +34,8 @@ def test_load_library_maps_one_hip_runtime():
 
 @pytest.mark.gpu
 def test_c_abi_without_torch(gpu_lib):
-    """create -> forward (decode kernels, then the GEMM) -> free from a process with no
-    torch, against the exact product."""
+    """create -> forward (decode kernels, then the GEMM) -> free of a 4-bit and an 8-bit
+    projection from a process with no torch, against the exact product."""
     from helios_amd import build
 
     r = _run([os.path.join(ROOT, "tests", "c_abi_host.py"), build.LIB_PATH], 110)

@@ -20,7 +20,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 LIB_NAME = "libgemma4_qmm.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-SOURCES = ["qmm_runtime.cpp", "q4_layout.hip", "q4_decode.hip", "q4_gemm.hip", "q4_lora.hip"]
+SOURCES = ["qmm_runtime.cpp", "q4_layout.hip", "q4_decode.hip", "q4_limbs.hip", "q4_gemm.hip", "q4_lora.hip"]
 ARCH = "gfx950"
 # measurement aid for the benchmark (a read-only HBM streaming kernel), its own library
 PROBE_SOURCES = ["hbm_probe.hip"]

@@ -18,6 +18,8 @@
 // sum: no atomics, no second pass), decode_stream_kernel (the same split, persistent
 // workgroups walking row blocks) and decode_rows_kernel (M = 1: one wave per row
 // block).
+#include <atomic>
+
 #include "q4_common.h"
 #include "q4_kernels.h"
 
@@ -698,8 +700,17 @@ int device_cus() {
     return cus[dev];
 }
 
+namespace {
+std::atomic<int> g_decode_variant{0};
+}  // namespace
+
+int set_decode_variant(int v) { return g_decode_variant.exchange(v); }
+int decode_variant() { return g_decode_variant.load(std::memory_order_relaxed); }
+
 hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, const OutParams& op, int m,
                          const Layout& l, hipStream_t stream) {
+    if (m == 1 && decode_variant() != 2 && limb_lds_bytes(l) <= kLdsPerCu)
+        return launch_decode_limbs(tiles, x, op, l, stream);
     if (m == 1) return launch_mt<1>(tiles, sb, x, op, m, l, stream);
     if (m == 2) return launch_mt<2>(tiles, sb, x, op, m, l, stream);
     if (m <= 4) return launch_mt<4>(tiles, sb, x, op, m, l, stream);

@@ -86,6 +86,19 @@ struct OutParams;
 hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, const OutParams& op, int m,
                          const Layout& l, hipStream_t stream);
 
+// Decode kernel family (a process-wide choice for tests and benchmarks): 0 automatic,
+// 1 the int8-limb kernel wherever it applies (one row of x), 2 the bf16 kernels only.
+// set_decode_variant returns the previous choice (an atomic exchange).
+int set_decode_variant(int v);
+int decode_variant();
+
+// One row of x on the int8 matrix cores (q4_limbs.hip): x split exactly into three
+// int8 limbs per group once per workgroup, every output mode.  limb_lds_bytes is its
+// dynamic LDS; the launch fails (hipErrorInvalidValue) when that exceeds the CU's LDS.
+size_t limb_lds_bytes(const Layout& l);
+hipError_t launch_decode_limbs(const uint4* tiles, const uint16_t* x, const OutParams& op, const Layout& l,
+                               hipStream_t stream);
+
 // token[m] (and value[m] when not null) = argmax over the keys part[m][0..nb) left by
 // the greedy modes, for m < rows.
 hipError_t launch_greedy_reduce(const unsigned long long* part, int nb, int rows, int32_t* token, float* value,

@@ -551,6 +551,10 @@ uint32_t gemma4_qmm_set_gemm_min_rows(uint32_t rows) {
     return g_gemm_min_rows.exchange(rows > (uint32_t)INT_MAX ? (uint32_t)INT_MAX : rows);
 }
 
+uint32_t gemma4_qmm_set_decode_kernel(uint32_t variant) {
+    return (uint32_t)q4::set_decode_variant(variant > 2u ? 0 : (int)variant);
+}
+
 Gemma4Status gemma4_qlinear_create(const Gemma4QLinearDesc* desc, const uint32_t* weight,
                                    const uint16_t* scales, const uint16_t* biases, Gemma4QLinear** out) {
     try {

@@ -102,6 +102,7 @@ def load_library(path: str | None = None):
         "gemma4_qmm_runtime_version": [ctypes.POINTER(_Version)],
         "gemma4_qmm_get_last_error": [ctypes.c_char_p, ctypes.c_size_t],
         "gemma4_qmm_set_gemm_min_rows": [ctypes.c_uint32],
+        "gemma4_qmm_set_decode_kernel": [ctypes.c_uint32],
         "gemma4_qlinear_create": [ctypes.POINTER(_Desc), vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qlinear_create_device": [ctypes.POINTER(_Desc), vp, vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qlinear_free": [vp],
@@ -122,7 +123,7 @@ def load_library(path: str | None = None):
     for name, args in sig.items():
         fn = getattr(lib, name)
         fn.argtypes = args
-        fn.restype = ctypes.c_uint32 if name == "gemma4_qmm_set_gemm_min_rows" else st
+        fn.restype = ctypes.c_uint32 if name.startswith("gemma4_qmm_set_") else st
     _lib = lib
     return lib
 
@@ -155,6 +156,25 @@ def set_gemm_min_rows(rows: int) -> int:
     if not 0 <= int(rows) < 2 ** 32:
         raise ValueError(f"rows must be in [0, 2**32), got {rows}")
     return int(load_library().gemma4_qmm_set_gemm_min_rows(int(rows)))
+
+
+def set_decode_kernel(variant: int) -> int:
+    """Pins the decode kernel family for this process: 0 (the default) chooses by
+    shape, 1 the int8 matrix-core kernel for every one-row call it can run, 2 the bf16
+    kernels only.  Returns the previous setting."""
+    if int(variant) not in (0, 1, 2):
+        raise ValueError(f"variant must be 0, 1 or 2, got {variant}")
+    return int(load_library().gemma4_qmm_set_decode_kernel(int(variant)))
+
+
+@contextlib.contextmanager
+def decode_kernel(variant: int):
+    """set_decode_kernel for the duration of a with-block."""
+    prev = set_decode_kernel(variant)
+    try:
+        yield
+    finally:
+        set_decode_kernel(prev)
 
 
 @contextlib.contextmanager

@@ -129,6 +129,17 @@ Gemma4Status gemma4_qmm_get_last_error(char* buffer, size_t buffer_len);
  * Takes effect for calls issued after it returns (a process-wide atomic). */
 uint32_t gemma4_qmm_set_gemm_min_rows(uint32_t rows);
 
+/* Decode kernel family of the forward calls in this process.  No counterpart in the
+ * reference; for tests and benchmarks that pin a kernel.
+ *   0 (the default): automatic, chosen per shape.
+ *   1: the int8 matrix-core kernel (x split exactly into three int8 limbs per
+ *      64-column group) for every one-row call it can run.
+ *   2: the bf16 matrix-core kernels only.
+ * All meet the same accuracy contract and sum in different orders.  Values above 2
+ * are taken as 0.  Returns the previous setting; takes effect for calls issued after
+ * it returns. */
+uint32_t gemma4_qmm_set_decode_kernel(uint32_t variant);
+
 /* Load one projection's weight triple from HOST memory in MLX layout onto the
  * current HIP device (the per-prefix tensors the reference keeps in Impl::tensors,
  * native_model.cc:84-104, :3550-3566).  The host arrays may be freed on return. */

@@ -388,3 +388,83 @@ def test_decode_stream_accesses_two_plane(m, n, k):
 @pytest.mark.parametrize("n,k", [(15360, 3840), (30720, 3840), (8192 + 48, 128), (8192, 640), (16 * 512, 3840)])
 def test_decode_rows_accesses(n, k):
     audit_decode_rows(1, n, k)
+
+
+def limb_config(nb, gp, cus=256):
+    """q4_limbs.hip limb_config: (waves, workgroups per CU, chunks in flight, strided)."""
+    nch = (gp + 1) // 2
+    if nch >= 32 and nb <= cus:
+        return 16, 1, 3, False
+    if nb <= 4 * cus:
+        return 8, 1, 2, False
+    return 8, 3, 1, True
+
+
+def audit_decode_limbs(n, k, kx=None, cus=256):
+    """decode_limb_kernel (one row of x): per-workgroup row blocks, chunks of two
+    records dealt to the waves in turn, x' limbs and the per-group table in LDS, the
+    (row block, wave) slots, and the final stores."""
+    kx = k if kx is None else kx
+    L = layout(n, k)
+    nb, gp = L["nb"], L["gp"]
+    waves, per_cu, nbuf, strided = limb_config(nb, gp, cus)
+    grid = min(nb, cus * per_cu)
+    nch = (gp + 1) // 2
+    stride = 784  # 4 groups x 3 limbs x 4 quarters x 16 B, then a zero unit
+    nrb_max = (nb + grid - 1) // grid
+    lds = nch * stride + nch * 4 * 8 + nrb_max * waves * 16 * 4
+    assert lds <= LDS_BYTES
+    lane = np.arange(64)
+    col, quarter = lane & 15, lane >> 4
+    sb_off = (quarter >> 1) * REC + REC_SB + col * 8 + (quarter & 1) * 4
+    seen = np.zeros((nb, nch), np.int64)
+    stored = np.zeros(nb, np.int64)
+    for b in range(grid):
+        if strided:
+            rb0, nrb, rbs = b, (nb - b + grid - 1) // grid, grid
+        else:
+            rb0 = b * nb // grid
+            nrb, rbs = (b * nb + nb) // grid - rb0, 1
+        total = nrb * nch
+        for w in range(waves):
+            mine = (total - w + waves - 1) // waves if w < total else 0
+            for i in range(mine + nbuf):  # the issues past the last chunk read nothing
+                f = w + i * waves
+                live = f < total
+                i_rb, c = divmod(f, nch)
+                left = gp - 2 * c
+                nrec = min(2, left) if live else 0
+                first = (rb0 + i_rb * rbs) * gp + 2 * c if live else 0
+                base = first * REC
+                for off, size in ((lane * 16, 16), (REC + lane * 16, 16), (sb_off, 4)):
+                    inr = off < nrec * REC
+                    assert (base + off[inr] + size <= L["rec_bytes"]).all()
+                    assert (off[inr] + size <= nrec * REC).all()
+                if live:
+                    assert rb0 + i_rb * rbs < nb and i_rb < nrb
+                    seen[rb0 + i_rb * rbs, c] += 1
+                    # slot of (row block, wave) and the chunk's LDS operands
+                    assert (i_rb * waves + w) * 16 + 15 < nrb * waves * 16
+                    assert c * stride + 768 + 16 <= nch * stride
+                    assert (c * 4 + 3) * 8 + 8 <= nch * 32
+        for r in range(nrb):
+            stored[rb0 + r * rbs] += 1
+    assert (seen == 1).all() and (stored == 1).all()
+    # staging: unit u of x' (u < nch * 32) -> limbs and table; x reads below kx * 2 bytes
+    u = np.arange(nch * 32)
+    g, h, kq = u >> 3, (u >> 2) & 1, u & 3
+    base = (g >> 2) * stride + (g & 3) * 192 + kq * 16 + h * 8
+    assert (base + 128 + 8 <= nch * stride).all() and ((base % stride) + 128 + 8 <= 768).all()
+    assert (g * 8 + 8 <= nch * 32).all()
+    xu = u[u < (k // 64) * 8]
+    assert (xprime_offset(xu, k, kx) + 16 <= kx * 2).all()
+
+
+@pytest.mark.parametrize("n,k", DECODE_SHAPES + [(8192, 3840), (1000, 192), (16, 128), (30720, 3840)])
+def test_decode_limb_accesses(n, k):
+    audit_decode_limbs(n, k)
+
+
+@pytest.mark.parametrize("n,k", [(15360, 3840), (48, 576), (130, 1088), (3840, 15360), (262144, 3840)])
+def test_decode_limb_accesses_two_plane(n, k):
+    audit_decode_limbs(n, 2 * k, kx=k)

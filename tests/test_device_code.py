@@ -104,3 +104,17 @@ def test_decode_register_budgets():
         if "decode_rows_kernel" in name:
             # two waves per SIMD (two 4-wave workgroups per CU)
             assert vgprs <= 256, f"{name}: {vgprs} VGPRs"
+
+
+def test_limb_register_budgets():
+    """decode_limb_kernel's launch shapes (q4_limbs.hip limb_config) assume its
+    occupancy: three 8-wave workgroups per CU for one chunk in flight (6 waves per
+    SIMD: at most 85 VGPRs), one 16-wave workgroup per CU (4 per SIMD: 128)."""
+    asm = hbuild.device_asm("q4_limbs.hip")
+    meta = [(n, v, p) for n, v, p in _kernel_meta(asm) if "decode_limb_kernel" in n]
+    assert len(meta) == 3
+    for name, vgprs, private in meta:
+        assert private == 0, f"{name} spills to scratch"
+        nbuf, waves = map(int, re.search(r"decode_limb_kernelILi(\d+)ELi(\d+)E", name).groups())
+        limit = 85 if nbuf == 1 else (128 if waves == 16 else 256)
+        assert vgprs <= limit, f"{name}: {vgprs} VGPRs"

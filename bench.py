@@ -76,9 +76,16 @@ SEED_BASE = 20260630
 ROTATE_BYTES = 512 << 20
 COPY_BYTES = 1 << 30
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_decode_m1_traffic.json")
-# the kernel that runs the gate|up GeGLU pair at M = 1 (2 x 15360 rows: one wave per
-# 16-row block)
-DOM_KERNEL = "decode_rows_kernel"
+# launches of the same step under the reference's own call structure (q, k and v
+# each their own quantized_linear, native_model.cc:993, :1005, :1009; gate and up as
+# the GeGLU pair; down)
+STEP_UNFUSED = [("q_proj", ("q_proj",)), ("k_proj", ("k_proj",)), ("v_proj", ("v_proj",)), ("o_proj", ("o_proj",)),
+                ("gate_up_geglu", ("gate_proj", "up_proj")), ("down_proj", ("down_proj",))]
+# the kernel that runs the gate|up GeGLU pair at M = 1: the int8 matrix-core decode
+# kernel, 1920 row blocks dealt round a grid of three 8-wave workgroups per CU with
+# one chunk in flight per wave
+DOM_KERNEL = "decode_limb_kernel"
+DOM_INSTANCE = "decode_limb_kernel<1,8,true>"
 
 
 def weight_bytes(n: int, k: int) -> int:
@@ -536,19 +543,7 @@ def summarize_trace(db_path: str, out_md: str, command: str) -> None:
         n = n.replace("(anonymous namespace)::", "").replace("void ", "").replace("q4::", "")
         return re.sub(r"\(.*", "", n)
 
-    shapes = []  # per shape: list of forwards, each a list of launches
-    for r in rows:
-        if "q4::" not in r[0]:
-            continue
-        s = short(r[0])
-        if s.startswith("repack"):
-            if not shapes or shapes[-1]:
-                shapes.append([])
-        elif shapes and (s.startswith("xaug") or s.startswith("decode") or
-                         (s.startswith("gemm_kernel") and not (shapes[-1] and short(shapes[-1][-1][-1][0]).startswith("xaug")))):
-            shapes[-1].append([r])
-        elif shapes and shapes[-1]:
-            shapes[-1][-1].append(r)
+    shapes = _trace_forwards(rows, short)  # per shape: list of forwards, each a list of launches
     names = prefill_sweep_names()
     md = ["# Prefill GEMM sweep: kernel durations per forward", "", "Command (from the repository root):", "",
           "```", command, "```", "",
@@ -575,17 +570,116 @@ def summarize_trace(db_path: str, out_md: str, command: str) -> None:
     print("\n".join(md))
 
 
-def model_run(torch, Q, decode_steps: int = 128, prefill_tokens: int = 16384, chunk: int = 2048,
-              layers: int = 48) -> dict:
-    """The 48-layer Gemma-style 12B decoder's quantized matmuls (the other ops of the
-    model are not run): 16K-token chunked prefill (M = 2048 chunks) then 128 decode
-    steps at M = 1, each layer as qkv, o, the gate|up GeGLU pair and down, then the
-    greedy lm_head on the last position.  Weights are random 4-bit codes with bf16
-    scales and biases of a N(0, 0.02) weight's size, generated on the device (6.6 GB,
-    far beyond the 256 MiB Infinity Cache), activations N(0, 1).  Timed with events
-    around the launches only."""
+# launches of `--decode-only`, in the order it runs them: (launch, rows)
+DECODE_PROFILE = [("k_proj", 1), ("q_proj", 1), ("o_proj", 1), ("qkv_proj", 1), ("gate_proj", 1), ("down_proj", 1),
+                  ("gate_up_geglu", 1), ("qkv_proj", 8), ("o_proj", 8), ("gate_proj", 8), ("down_proj", 8),
+                  ("gate_up_geglu", 8)]
+
+
+def _trace_forwards(rows, short):
+    """Kernel launches of a trace in start order, grouped per shape (each shape's
+    handles are created, with repack launches, before its forwards) and per forward (a
+    GEMM-path forward starts with the GEMM, or xaug_kernel for the 256-row tile; a
+    decode-path forward is one decode kernel)."""
+    shapes = []
+    for r in rows:
+        if "q4::" not in r[0]:
+            continue
+        s = short(r[0])
+        if s.startswith("repack"):
+            if not shapes or shapes[-1]:
+                shapes.append([])
+        elif shapes and (s.startswith("xaug") or s.startswith("decode") or
+                         (s.startswith("gemm_kernel") and not (shapes[-1] and short(shapes[-1][-1][-1][0]).startswith("xaug")))):
+            shapes[-1].append([r])
+        elif shapes and shapes[-1]:
+            shapes[-1][-1].append(r)
+    return shapes
+
+
+def summarize_decode(db_path: str, fetch_dir: str, write_dir: str, line_file: str, out_md: str, command: str) -> None:
+    """Per-launch summary of `bench.py --decode-only` from a rocprofv3 kernel trace
+    (rocpd SQLite) and FETCH_SIZE / WRITE_SIZE passes (csv): the median duration of
+    each decode launch and its HBM bytes per dispatch, each counter scaled by what it
+    reads for the run's 1 GiB copy, against the launch's algorithmic bytes."""
+    import re
+    import sqlite3
+
+    def short(n):
+        n = n.replace("(anonymous namespace)::", "").replace("void ", "").replace("q4::", "")
+        return re.sub(r"\(.*", "", n)
+
+    with open(line_file) as f:
+        line = json.loads([l for l in f if l.startswith("{")][-1])
+    rows = list(sqlite3.connect(db_path).execute(
+        "select name, grid_x, grid_y, workgroup_x, duration, start from kernels order by start"))
+    shapes = _trace_forwards(rows, short)
+
+    def counter_shapes(d, counter):
+        """per shape (split at repack dispatches, in dispatch order): the mean counter
+        value of its decode dispatches, and the copy kernel's value"""
+        recs = [r for r in _csv_rows(d, "counter_collection.csv") if r["Counter_Name"] == counter]
+        recs.sort(key=lambda r: int(r.get("Dispatch_Id") or r.get("Correlation_Id") or 0))
+        per, cpy = [], []
+        for r in recs:
+            n = r["Kernel_Name"]
+            if "rocclr_copybuffer" in n.lower():
+                cpy.append(float(r["Counter_Value"]))
+            elif "q4::" not in n:
+                continue
+            elif short(n).startswith("repack"):
+                if not per or per[-1]:
+                    per.append([])
+            elif short(n).startswith("decode") and per:
+                per[-1].append(float(r["Counter_Value"]))
+        return [sum(v) / len(v) if v else None for v in per], (sum(cpy) / len(cpy) if cpy else None)
+
+    fetch, f_cpy = counter_shapes(fetch_dir, "FETCH_SIZE")
+    write, w_cpy = counter_shapes(write_dir, "WRITE_SIZE")
+    f_scale = line["copy_bytes"] / (f_cpy * 1024) if f_cpy else None
+    w_scale = line["copy_bytes"] / (w_cpy * 1024) if w_cpy else None
+    md = ["# Decode launches at M = 1 and 8: durations and HBM traffic", "", "Command (from the repository root):", "",
+          "```", command, "```", "", "bench.py --decode-only line (HIP-event timing, no profiler):", "", "```",
+          json.dumps(line), "```", "",
+          "Per launch: the kernel (workgroups x 16-row slabs), its median duration over the launch's dispatches in "
+          "the kernel trace (back-to-back launches over rotated weight copies in a replayed graph), the bench's own "
+          "figure, and HBM bytes per dispatch from FETCH_SIZE + WRITE_SIZE (KiB per dispatch, scaled by what each "
+          f"counter reads for the 1 GiB copy: fetch x{f_scale:.4f}, write x{w_scale:.4f}) against the algorithmic "
+          "bytes.", "",
+          "| launch | kernel | dispatches | median us (trace) | us (bench) | algorithmic MB | HBM MB | ratio | GB/s |",
+          "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for i, (name, m) in enumerate(DECODE_PROFILE):
+        key = f"{name}_m{m}"
+        if i >= len(shapes) or not shapes[i]:
+            continue
+        fwds = shapes[i]
+        k0 = short(fwds[0][0][0])
+        durs = sorted(p[4] for f in fwds for p in f if short(p[0]) == k0)
+        med = durs[len(durs) // 2] / 1e3
+        rec = line["launches"][key]
+        hbm = None
+        if i < len(fetch) and i < len(write) and fetch[i] is not None and write[i] is not None:
+            hbm = fetch[i] * 1024 * f_scale + write[i] * 1024 * w_scale
+        md.append(f"| {key} | {k0} {fwds[0][0][1] // max(fwds[0][0][3], 1)}x{fwds[0][0][2]} | {len(durs)} | "
+                  f"{med:.2f} | {rec['us']:.2f} | {rec['algo_bytes'] / 1e6:.2f} | "
+                  f"{(hbm / 1e6) if hbm else float('nan'):.2f} | "
+                  f"{(hbm / rec['algo_bytes']) if hbm else float('nan'):.3f} | {rec['algo_bytes'] / (med * 1e3):.0f} |")
+    if len(shapes) != len(DECODE_PROFILE):
+        md += ["", f"(trace holds {len(shapes)} launches, the run {len(DECODE_PROFILE)}: labels may not line up)"]
+    with open(out_md, "w") as f:
+        f.write("\n".join(md) + "\n")
+    print("\n".join(md))
+
+
+def build_decoder(torch, Q, layers: int = 48, seed: int = SEED_BASE + 5):
+    """Weights of the 48-layer Gemma-style 12B decoder's quantized projections, made on
+    the device: random 4-bit codes with bf16 scales in [0.002, 0.005) and biases in
+    [-0.03, -0.01) (a N(0, 0.02) weight's size; 6.6 GB, far beyond the 256 MiB
+    Infinity Cache).  Each layer holds q|k|v as one handle (8192 x 3840, q, k, v
+    concatenated along N), o, the gate|up GeGLU pair and down, plus per-layer RMSNorm
+    weights; one greedy lm_head (262144 x 3840) follows."""
     g = torch.Generator(device="cuda")
-    g.manual_seed(SEED_BASE + 5)
+    g.manual_seed(seed)
 
     def triple(n, k):
         w = torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32, device="cuda", generator=g)
@@ -597,9 +691,95 @@ def model_run(torch, Q, decode_steps: int = 128, prefill_tokens: int = 16384, ch
     for _ in range(layers):
         net.append({"qkv": Q.QuantizedLinear(*triple(8192, HIDDEN)), "o": Q.QuantizedLinear(*triple(HIDDEN, 4096)),
                     "mlp": Q.QuantizedGeGLU(triple(15360, HIDDEN), triple(15360, HIDDEN)),
-                    "down": Q.QuantizedLinear(*triple(HIDDEN, 15360))})
+                    "down": Q.QuantizedLinear(*triple(HIDDEN, 15360)),
+                    "norm": (torch.rand((2, HIDDEN), device="cuda", generator=g) * 0.2 - 0.1).bfloat16()})
     lm = Q.QuantizedLinear(*triple(262144, HIDDEN))
     torch.cuda.synchronize()
+    return net, lm
+
+
+def free_decoder(net, lm) -> None:
+    for L in net:
+        for name in ("qkv", "o", "mlp", "down"):
+            L[name].close()
+    lm.close()
+
+
+def rms_norm(torch, x, w, eps: float = 1e-6):
+    """Gemma RMSNorm in fp32, rounded to bf16: x / sqrt(mean(x^2) + eps) * (1 + w)."""
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * (1.0 + w.float())).bfloat16()
+
+
+def decoder_forward_m1(torch, net, lm, x0, states=None):
+    """One decode token through the chained decoder, every projection on the library:
+    per layer RMSNorm -> q|k|v -> attention over the token's own position (one key, so
+    each query head's output is the value of its KV head; RoPE at position 0 is the
+    identity) -> o -> residual add -> RMSNorm -> gate|up GeGLU -> down -> residual add;
+    then the greedy lm_head (softcap 30) on the final RMSNorm.  Attention and norms are
+    plain torch bf16/fp32 ops.  Returns the token tensor [1] (int32); with `states` (a
+    list) the residual stream after every layer is appended to it."""
+    x = x0
+    for L in net:
+        h = rms_norm(torch, x, L["norm"][0])
+        qkv = L["qkv"].forward(h)
+        v = qkv[:, 6144:8192].reshape(1, 8, 256)
+        attn = v.repeat_interleave(2, dim=1).reshape(1, 4096)  # 16 query heads over 8 KV heads
+        x = (x.float() + L["o"].forward(attn).float()).bfloat16()
+        hh = L["mlp"].forward(rms_norm(torch, x, L["norm"][1]))
+        x = (x.float() + L["down"].forward(hh).float()).bfloat16()
+        if states is not None:
+            states.append(x)
+    token = lm.forward_greedy(rms_norm(torch, x, net[-1]["norm"][0]), softcap=30.0)
+    return token if isinstance(token, torch.Tensor) else token[0]
+
+
+def decoder_check(torch, net, lm, replays: int = 3, seed: int = SEED_BASE + 6) -> dict:
+    """The chained decode forward run eagerly and as a HIP graph replayed `replays`
+    times (with eager work and synchronizations between replays): whether every
+    residual state and the token are finite / equal bit for bit across them."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x0 = torch.randn((1, HIDDEN), device="cuda", generator=g).bfloat16()
+    eager_states = []
+    eager_tok = decoder_forward_m1(torch, net, lm, x0, eager_states).clone()
+    torch.cuda.synchronize()
+    finite = all(bool(torch.isfinite(s).all()) for s in eager_states)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        decoder_forward_m1(torch, net, lm, x0)  # warms the capture stream's scratch
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap_states = []
+    with torch.cuda.graph(graph, stream=stream):
+        cap_tok = decoder_forward_m1(torch, net, lm, x0, cap_states)
+    equal, tokens = True, []
+    for _ in range(replays):
+        graph.replay()
+        torch.cuda.synchronize()
+        equal &= all(torch.equal(a, b) for a, b in zip(eager_states, cap_states))
+        tokens.append(int(cap_tok.item()))
+        # eager work between replays (the program's own use of the stream)
+        decoder_forward_m1(torch, net, lm, x0)
+        torch.cuda.synchronize()
+    del graph
+    return {"finite": finite, "graph_equals_eager": bool(equal), "token": int(eager_tok.item()),
+            "replay_tokens": tokens, "token_stable": all(t == int(eager_tok.item()) for t in tokens),
+            "final_rms": round(float(eager_states[-1].float().pow(2).mean().sqrt()), 4)}
+
+
+def model_run(torch, Q, decode_steps: int = 128, prefill_tokens: int = 16384, chunk: int = 2048,
+              layers: int = 48) -> dict:
+    """The 48-layer Gemma-style 12B decoder's quantized matmuls, timed alone (the other
+    ops of the model are not in the timed region): 16K-token chunked prefill (M = 2048
+    chunks) then 128 decode steps at M = 1, each layer as qkv, o, the gate|up GeGLU
+    pair and down, then the greedy lm_head on the last position.  Inputs of the timed
+    passes are fixed N(0, 1) activations.  Timed with events around the launches only.
+    Then `decoder_check`: the chained forward (norms, attention and residuals between
+    the projections) checked eager against graph replays."""
+    net, lm = build_decoder(torch, Q, layers)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEED_BASE + 7)
     # each projection's input and output, contiguous [chunk, width]; a pass over M rows
     # uses the first M rows of each
     xin = {k: torch.randn((chunk, k), device="cuda", generator=g).bfloat16() for k in (HIDDEN, 4096, 15360)}
@@ -643,14 +823,12 @@ def model_run(torch, Q, decode_steps: int = 128, prefill_tokens: int = 16384, ch
     torch.cuda.synchronize()
     decode_ms = e0.elapsed_time(e1) / decode_steps
     del graph
+    check = decoder_check(torch, net, lm)
     layer_w = sum(n * k // 2 + 4 * n * (k // 64) for _, n, k in LAYER)
     lm_w = 262144 * HIDDEN // 2 + 4 * 262144 * (HIDDEN // 64)
     step_bytes = layers * sum(algo_bytes(1, n, k) for _, n, k in LAYER) + algo_bytes(1, 262144, HIDDEN)
     prefill_flops = layers * sum(algo_flops(prefill_tokens, n, k) for _, n, k in LAYER) + algo_flops(1, 262144, HIDDEN)
-    for L in net:
-        for h in L.values():
-            h.close()
-    lm.close()
+    free_decoder(net, lm)
     return {
         "workload": f"{layers}-layer Gemma-style 12B decoder, quantized matmuls only: {prefill_tokens}-token prefill "
                     f"in chunks of {chunk}, then {decode_steps} decode steps (each layer qkv, o, gate|up GeGLU pair, "
@@ -662,6 +840,7 @@ def model_run(torch, Q, decode_steps: int = 128, prefill_tokens: int = 16384, ch
         "prefill_ms": round(prefill_ms, 2),
         "prefill_TFLOPS": round(prefill_flops / (prefill_ms * 1e-3) / 1e12, 1),
         "prefill_tokens_per_s": round(prefill_tokens / (prefill_ms * 1e-3), 1),
+        "chained_forward_check": check,
     }
 
 
@@ -813,6 +992,12 @@ def main() -> int:
                     help="write profiles/gate_prefill_m2048.md from rocprofv3 output over --gemm-only")
     ap.add_argument("--summarize-trace", nargs=3, metavar=("RESULTS_DB", "OUT_MD", "CMD"),
                     help="write a per-shape summary of a rocprofv3 kernel trace of --prefill-only (no GPU)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="the decode launches of DECODE_PROFILE (M = 1 and 8) and a 1 GiB copy, one JSON line "
+                         "(for rocprofv3 kernel traces and counter passes)")
+    ap.add_argument("--summarize-decode", nargs=6,
+                    metavar=("RESULTS_DB", "FETCH_DIR", "WRITE_DIR", "LINE", "OUT_MD", "CMD"),
+                    help="write the per-launch summary of rocprofv3 output over --decode-only (no GPU)")
     args = ap.parse_args()
     if args.summarize_profiles:
         summarize_profiles(*args.summarize_profiles)
@@ -822,6 +1007,9 @@ def main() -> int:
         return 0
     if args.summarize_gemm:
         summarize_gemm(*args.summarize_gemm)
+        return 0
+    if args.summarize_decode:
+        summarize_decode(*args.summarize_decode)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -837,12 +1025,13 @@ def main() -> int:
     log("quantizing one decoder layer")
     host = quantized_layer()
     dims = {name: (n, k) for name, n, k in LAYER}
-    fused = {name: fused_triple(host, parts) for name, parts in STEP if name != PAIR}
+    launches = dict(STEP + STEP_UNFUSED)
+    fused = {name: fused_triple(host, parts) for name, parts in launches.items() if name != PAIR}
     # N of each launch's output and its K
     step_nk = {name: (sum(dims[p][0] for p in parts) if name != PAIR else dims[parts[0]][0], dims[parts[0]][1])
-               for name, parts in STEP}
+               for name, parts in launches.items()}
     wbytes_of = {name: sum(dims[p][0] * dims[p][1] // 2 + 4 * dims[p][0] * (dims[p][1] // 64) for p in parts)
-                 for name, parts in STEP}
+                 for name, parts in launches.items()}
 
     def maker(name):
         if name == PAIR:
@@ -853,7 +1042,7 @@ def main() -> int:
           for k in {k for _, _, k in LAYER}}
     f_gu, k_gu = step_nk[PAIR]
     gu_bytes = pair_algo_bytes(1, f_gu, k_gu)
-    gu_kernel = f"{DOM_KERNEL}<1,4,2> gate|up GeGLU pair F={f_gu} K={k_gu} M=1"
+    gu_kernel = f"{DOM_INSTANCE} gate|up GeGLU pair F={f_gu} K={k_gu} M=1"
 
     def pair_us(m):
         return kernel_us(torch, maker(PAIR), m, k_gu, f_gu, xs[k_gu], wbytes_of[PAIR])
@@ -875,6 +1064,17 @@ def main() -> int:
               flush=True)
         return 0
 
+    if args.decode_only:
+        res = {}
+        for name, m in DECODE_PROFILE:
+            n, k = step_nk[name]
+            us = kernel_us(torch, maker(name), m, k, n, xs[k], wbytes_of[name])
+            ab = pair_algo_bytes(m, n, k) if name == PAIR else algo_bytes(m, n, k)
+            res[f"{name}_m{m}"] = {"us": round(us, 3), "algo_bytes": ab, "GBps": round(ab / (us * 1e-6) / 1e9, 1)}
+        cgbs = copy_gbs(torch)
+        print(json.dumps({"launches": res, "copy_bytes": COPY_BYTES, "copy_GBps": round(cgbs, 1)}), flush=True)
+        return 0
+
     if args.roofline_only:
         us_gu = pair_us(1)
         cgbs = copy_gbs(torch)
@@ -885,18 +1085,20 @@ def main() -> int:
                           "read_probe_bytes": rd["bytes"], "read_probe_GBps": rd["GBps"]}), flush=True)
         return 0
 
-    layer_w_bytes = sum(wbytes_of.values())
+    layer_w_bytes = sum(wbytes_of[name] for name, _ in STEP)
     copies = max(2, -(-ROTATE_BYTES // layer_w_bytes))
     log(f"uploading {copies} copies of the layer ({copies * layer_w_bytes / 2**20:.0f} MiB)")
     layers = [{name: maker(name)() for name, _ in STEP} for _ in range(copies)]
     ys = {name: torch.empty((16, n), dtype=torch.bfloat16, device="cuda") for name, (n, _) in step_nk.items()}
 
-    def step_fn(m):
+    def step_fn(m, step=STEP, sets=None):
+        sets = layers if sets is None else sets
+
         def fn():
             for c in range(copies):
-                for name, _ in STEP:
+                for name, _ in step:
                     n, k = step_nk[name]
-                    layers[c][name].forward(xs[k][:m], out=ys[name][:m])
+                    sets[c][name].forward(xs[k][:m], out=ys[name][:m])
         return fn
 
     # --- headline: one decoder layer's projections at M=1 (4 launches), graph-replayed ---
@@ -907,7 +1109,7 @@ def main() -> int:
     step_bytes = sum(algo_bytes(1, n, k) for _, n, k in LAYER)
     value = step_bytes / (ms_step * 1e-3) / 1e9
     step_by_m = {}
-    for m in ((4, 8) if not args.quick else ()):
+    for m in ((4, 8, 16) if not args.quick else ()):
         ms_m = graph_ms(torch, step_fn(m), max(10, args.steps // 4), 2, settle_ms=50.0) / copies
         step_by_m[f"m{m}"] = {"ms_per_step": round(ms_m, 5),
                               "GBps": round(sum(algo_bytes(m, n, k) for _, n, k in LAYER) / (ms_m * 1e-3) / 1e9, 1)}
@@ -915,6 +1117,17 @@ def main() -> int:
         for lin in lin_set.values():
             lin.close()
     del layers
+    # the same step under the reference's call structure: q, k and v as three launches
+    unfused = None
+    if not args.quick:
+        sets = [{name: maker(name)() for name, _ in STEP_UNFUSED} for _ in range(copies)]
+        ms_u = graph_ms(torch, step_fn(1, STEP_UNFUSED, sets), max(10, args.steps // 4), 2, settle_ms=50.0) / copies
+        unfused = {"launches": [name for name, _ in STEP_UNFUSED], "ms_per_step": round(ms_u, 5),
+                   "GBps": round(step_bytes / (ms_u * 1e-3) / 1e9, 1)}
+        for lin_set in sets:
+            for lin in lin_set.values():
+                lin.close()
+        del sets
 
     # --- dominant kernel: the gate|up GeGLU pair at M=1 ---
     us_gu = pair_us(1)
@@ -1038,6 +1251,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "decode_step_by_m": step_by_m,
+        "decode_step_unfused_m1": unfused,
         "decode_per_projection": per_proj,
         "lm_head": lm,
         "prefill_gemm": gemm,

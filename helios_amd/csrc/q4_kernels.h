@@ -158,9 +158,13 @@ hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float*
 // 16.9 vs 18.3; the fused qkv 8192x3840 at 32 rows on the GEMM, 13.8 vs 19.9).
 constexpr int kGemmMinRows = 32;
 constexpr double kDecodeMaxSlabWork = 5.5e7;
+// The slab bound was fitted on the Gemma shapes at 32-256 rows (the full-attention k,
+// 512 x 3840, stays on decode to 448 rows); beyond 64 slabs the GEMM takes any shape.
+constexpr long kDecodeMaxRows = 1024;
 inline bool use_decode(long rows, const Layout& l, int gemm_min_rows) {
     if (gemm_min_rows > 0) return rows < gemm_min_rows;
-    return rows < kGemmMinRows || (double)((rows + 15) / 16) * (double)l.n * (double)l.k <= kDecodeMaxSlabWork;
+    return rows < kGemmMinRows ||
+           (rows <= kDecodeMaxRows && (double)((rows + 15) / 16) * (double)l.n * (double)l.k <= kDecodeMaxSlabWork);
 }
 
 }  // namespace q4

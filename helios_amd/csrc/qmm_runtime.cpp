@@ -140,8 +140,9 @@ hipError_t static_scratch(int device, char** out) {
 // Work on one stream runs in order, so consecutive calls can reuse it; `mu` is held
 // for a whole call (its scratch and its launches), so calls from several host threads
 // on one stream cannot interleave their launches.  It grows by allocating a larger
-// buffer when a call is not being captured into a graph; outgrown buffers are kept
-// until the process ends, since a graph captured earlier may still use them.  A
+// buffer when a call is not being captured into a graph.  An outgrown buffer that a
+// capture took pieces of is kept (a graph captured earlier may still use it) until
+// gemma4_qmm_release_scratch; one no capture used is freed once the stream is idle.  A
 // stream-ordered pool allocation per call (and, under capture, an allocation node per
 // call in the graph) cost 5-10 us per forward on the GPU: k_proj 2048x3840 at 512 rows,
 // split four ways, 31 us per forward in a graph against 22 us with the workspace.
@@ -151,7 +152,8 @@ struct StreamWorkspace {
     std::thread::id thread;  // hipStreamPerThread: a different stream in every thread
     char* buf = nullptr;
     size_t cap = 0;
-    std::vector<char*> retired;
+    bool buf_captured = false;    // a graph capture took pieces of buf
+    std::vector<char*> retired;  // outgrown buffers that captures used
     std::mutex mu;
 };
 std::mutex g_ws_mu;
@@ -206,25 +208,35 @@ struct Scratch {
             cap = ws->cap;
             used = 0;
         }
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        const bool capturing =
+            hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone;
         if (need <= cap - used) {
             *out = base + used;
             used += need;
+            if (capturing) ws->buf_captured = true;
             return hipSuccess;
         }
-        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(stream, &capture) == hipSuccess && capture == hipStreamCaptureStatusNone) {
-            // grow: a new buffer for this and later calls; pieces this call took from
-            // the old one stay valid, as does every graph that uses it.  (The pool for
-            // the fallback below is made here too, outside any capture.)
+        if (!capturing) {
+            // grow: a new buffer for this and later calls.  Pieces this call took from
+            // the old one stay valid (it is released only after this call's launches,
+            // see `finish`), as does every graph that used it.  (The pool for the
+            // fallback below is made here too, outside any capture.)
             hipMemPool_t pool = nullptr;
             (void)scratch_pool(device, &pool);
             size_t ncap = ws->cap * 2 > need ? ws->cap * 2 : need;
             ncap = (ncap + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
             char* nb = nullptr;
             if (hipMalloc(&nb, ncap) == hipSuccess) {
-                if (ws->buf != nullptr) ws->retired.push_back(ws->buf);
+                if (ws->buf != nullptr) {
+                    if (ws->buf_captured)
+                        ws->retired.push_back(ws->buf);
+                    else
+                        outgrown = ws->buf;
+                }
                 ws->buf = base = nb;
                 ws->cap = cap = ncap;
+                ws->buf_captured = false;
                 *out = base;
                 used = need;
                 return hipSuccess;
@@ -247,8 +259,18 @@ struct Scratch {
             if (first == hipSuccess) first = e;
         }
         n_owned = 0;
+        if (outgrown != nullptr) {
+            // an outgrown buffer no capture used: freed once the stream's work (this
+            // call's launches included) is done
+            hipError_t e = hipStreamSynchronize(stream);
+            if (e == hipSuccess) e = hipFree(outgrown);
+            outgrown = nullptr;
+            if (first == hipSuccess) first = e;
+        }
         return first;
     }
+
+    char* outgrown = nullptr;  // the stream's previous buffer, freed by release()
 };
 
 // Restores the caller's current device on scope exit.
@@ -551,6 +573,44 @@ uint32_t gemma4_qmm_set_gemm_min_rows(uint32_t rows) {
     return g_gemm_min_rows.exchange(rows > (uint32_t)INT_MAX ? (uint32_t)INT_MAX : rows);
 }
 
+Gemma4Status gemma4_qmm_release_scratch(void* stream) {
+    try {
+        int device = 0;
+        hipError_t e = hipGetDevice(&device);
+        if (e != hipSuccess) return hip_fail("gemma4_qmm_release_scratch: hipGetDevice", e);
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        const std::thread::id thread = st == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+        StreamWorkspace* ws = nullptr;
+        {
+            std::lock_guard<std::mutex> lock(g_ws_mu);
+            for (auto& w : g_ws)
+                if (w->device == device && w->stream == st && w->thread == thread) ws = w.get();
+        }
+        if (ws == nullptr) return ok();
+        // the entry itself stays (a call in another thread may hold it); its memory goes
+        std::lock_guard<std::mutex> lock(ws->mu);
+        e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail("gemma4_qmm_release_scratch: hipStreamSynchronize", e);
+        hipError_t first = hipSuccess;
+        for (char* p : ws->retired) {
+            const hipError_t ef = hipFree(p);
+            if (first == hipSuccess) first = ef;
+        }
+        ws->retired.clear();
+        if (ws->buf != nullptr) {
+            const hipError_t ef = hipFree(ws->buf);
+            if (first == hipSuccess) first = ef;
+        }
+        ws->buf = nullptr;
+        ws->cap = 0;
+        ws->buf_captured = false;
+        if (first != hipSuccess) return hip_fail("gemma4_qmm_release_scratch: hipFree", first);
+        return ok();
+    } catch (...) {
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qmm_release_scratch: unexpected native exception");
+    }
+}
+
 uint32_t gemma4_qmm_set_decode_kernel(uint32_t variant) {
     return (uint32_t)q4::set_decode_variant(variant > 2u ? 0 : (int)variant);
 }
@@ -662,6 +722,22 @@ Gemma4Status gemma4_qlinear_info(const Gemma4QLinear* linear, Gemma4QLinearInfo*
         return ok();
     } catch (...) {
         return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_info: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qlinear_scratch_bytes(const Gemma4QLinear* linear, uint32_t rows, uint64_t* out) {
+    try {
+        if (out == nullptr)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_scratch_bytes requires a non-null out pointer");
+        if (!valid_handle(linear))
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, "gemma4_qlinear_scratch_bytes received an invalid handle");
+        *out = 0;
+        if (rows == 0 || q4::use_decode(rows, linear->layout, (int)g_gemm_min_rows.load(std::memory_order_relaxed)))
+            return ok();
+        *out = q4::gemm_workspace_bytes((int)rows, linear->layout);
+        return ok();
+    } catch (...) {
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_scratch_bytes: unexpected native exception");
     }
 }
 

@@ -103,6 +103,8 @@ def load_library(path: str | None = None):
         "gemma4_qmm_get_last_error": [ctypes.c_char_p, ctypes.c_size_t],
         "gemma4_qmm_set_gemm_min_rows": [ctypes.c_uint32],
         "gemma4_qmm_set_decode_kernel": [ctypes.c_uint32],
+        "gemma4_qmm_release_scratch": [vp],
+        "gemma4_qlinear_scratch_bytes": [vp, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint64)],
         "gemma4_qlinear_create": [ctypes.POINTER(_Desc), vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qlinear_create_device": [ctypes.POINTER(_Desc), vp, vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qlinear_free": [vp],
@@ -156,6 +158,14 @@ def set_gemm_min_rows(rows: int) -> int:
     if not 0 <= int(rows) < 2 ** 32:
         raise ValueError(f"rows must be in [0, 2**32), got {rows}")
     return int(load_library().gemma4_qmm_set_gemm_min_rows(int(rows)))
+
+
+def release_scratch(stream=None) -> None:
+    """Frees the device memory the library keeps for the scratch of calls on `stream`
+    (default: torch's current stream) on the current device, after waiting for the
+    stream.  Graphs captured on it that used that memory must not be replayed after."""
+    lib = load_library()
+    check(lib.gemma4_qmm_release_scratch(_stream_ptr(stream)), lib)
 
 
 def set_decode_kernel(variant: int) -> int:
@@ -271,6 +281,13 @@ class _Handle:
         info = _Info()
         check(self._lib.gemma4_qlinear_info(self._handle, ctypes.byref(info)), self._lib)
         return {f: getattr(info, f) for f, _ in _Info._fields_}
+
+    def scratch_bytes(self, rows: int) -> int:
+        """Scratch bytes a forward of `rows` rows takes (0 on the decode path); at most
+        64 MiB means forward_noalloc runs the same plan (identical bits)."""
+        out = ctypes.c_uint64(0)
+        check(self._lib.gemma4_qlinear_scratch_bytes(self._handle, int(rows), ctypes.byref(out)), self._lib)
+        return int(out.value)
 
     @property
     def device(self):

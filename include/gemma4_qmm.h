@@ -41,11 +41,14 @@
  * device work is asynchronous on that stream.  A handle is immutable after
  * create, so forward/dequantize may run concurrently on several streams and
  * threads; create and free must not overlap use.  Scratch (split-K partial sums,
- * the greedy head's keys, LoRA's x.A^T) comes from device memory the library keeps
- * per (device, stream) and reuses call after call in stream order.  A HIP graph that
- * captured a call uses its capture stream's memory, so replays of graphs captured on
- * one stream must not overlap one another or calls on that stream (replay them on
- * one stream, or serialize).  The memory is held until the process ends.
+ * the 256-row GEMM tile's group sums, the greedy head's keys, LoRA's x.A^T) comes
+ * from device memory the library keeps per (device, stream) and reuses call after
+ * call in stream order.  A HIP graph that captured a call uses its capture stream's
+ * memory, so replays of graphs captured on one stream must not overlap one another
+ * or calls on that stream (replay them on one stream, or serialize).  When a call
+ * needs more, the stream's memory grows; the outgrown buffer is freed unless a
+ * capture used it.  The memory is held until gemma4_qmm_release_scratch or the end
+ * of the process.
  */
 #ifndef GEMMA4_QMM_H
 #define GEMMA4_QMM_H
@@ -140,6 +143,14 @@ uint32_t gemma4_qmm_set_gemm_min_rows(uint32_t rows);
  * it returns. */
 uint32_t gemma4_qmm_set_decode_kernel(uint32_t variant);
 
+/* Releases the device memory the library keeps for the scratch of calls on `stream`
+ * on the current device (for hipStreamPerThread, the calling thread's), after waiting
+ * for the stream's work.  No counterpart in the reference (MLX frees per call); for
+ * long-running hosts that retire streams.  Graphs captured on that stream that used
+ * the memory must not be replayed afterwards; later calls on the stream allocate
+ * again.  A stream the library never used is a no-op. */
+Gemma4Status gemma4_qmm_release_scratch(void* stream);
+
 /* Load one projection's weight triple from HOST memory in MLX layout onto the
  * current HIP device (the per-prefix tensors the reference keeps in Impl::tensors,
  * native_model.cc:84-104, :3550-3566).  The host arrays may be freed on return. */
@@ -167,17 +178,26 @@ Gemma4Status gemma4_qlinear_info(const Gemma4QLinear* linear, Gemma4QLinearInfo*
 Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
                                     uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype);
 
+/* Scratch bytes gemma4_qlinear_forward (or gemma4_qgeglu_forward, for a pair) takes
+ * for `rows` rows under the current path choice: 0 on the decode path, else the GEMM
+ * plan's group sums and split-K partial sums.  No counterpart in the reference.  When
+ * it is at most 64 MiB, gemma4_qlinear_forward_noalloc runs the same plan, so the two
+ * calls give identical bits. */
+Gemma4Status gemma4_qlinear_scratch_bytes(const Gemma4QLinear* linear, uint32_t rows, uint64_t* out);
+
 /* gemma4_qlinear_forward for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, hosts that forbid allocation): the same
  * arguments, results and kernels, with every scratch buffer taken from a static
  * 64 MiB device array that the library holds on each GPU it runs on until the
  * process ends.  No counterpart in the reference (its MLX ops allocate per call).
  * It calls no hipMalloc, hipFree or allocating library routine.  Scratch needs:
- * none on the decode path (gemma4_qmm_set_gemm_min_rows); on the GEMM path split-K
- * partial sums only as far as the array has room (fewer splits than
+ * none on the decode path (gemma4_qmm_set_gemm_min_rows); on the GEMM path the
+ * 256-row tile's table of x's group sums (1 KiB per 16 rows, rounded up to 256, and
+ * per 512 columns of K) and split-K partial
+ * sums, only as far as the array has room (a cheaper tile or fewer splits than
  * gemma4_qlinear_forward may choose, so the fp32 summation order, and with it the
- * last bits of some outputs, can differ from that call's; an unsplit GEMM needs
- * none), so no call is refused for want of scratch.  Every call
+ * last bits of some outputs, can differ from that call's; unsplit plans on the 64-
+ * and 128-row tiles need none), so no call is refused for want of scratch.  Every call
  * on a GPU shares that GPU's array: calls that overlap in time on one GPU (other
  * streams, other threads) race and must be serialized by the caller. */
 Gemma4Status gemma4_qlinear_forward_noalloc(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,

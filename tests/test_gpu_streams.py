@@ -13,10 +13,11 @@ split order), so concurrent results must equal the serial ones bit for bit:
     rewritten by eager work between replays: every replay equals the eager result
     for its inputs.  Captured on a stream whose scratch memory is too small, the
     calls' scratch becomes allocation nodes of the graph; captured on a stream warmed
-    up first, they use that stream's memory (no allocation nodes); no memset nodes
-    either way;
+    up first, they use that stream's memory (no allocation nodes: asserted on the
+    graph's node types); no memset nodes either way;
   * hipStreamPerThread from two threads at once: each thread's own stream and
-    scratch.
+    scratch;
+  * gemma4_qmm_release_scratch returns a stream's memory.
 """
 
 import threading
@@ -207,5 +208,81 @@ def test_graph_on_warmed_stream_matches_eager(gpu_lib):
         for i, (a, b) in enumerate(zip(outs, want)):
             assert _same(a, b), f"replay {rep}: output {i} differs from the eager result"
     del g
+    for h in (lin, pair, head):
+        h.close()
+
+
+def test_release_scratch(gpu_lib):
+    """gemma4_qmm_release_scratch frees a stream's scratch memory (the device's free
+    memory grows by at least what the split plan took), later calls on the stream
+    allocate again and give the same bits, and a stream the library never used is a
+    no-op."""
+    import torch
+
+    import hip_graph_nodes as G
+
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*random_triple(N, K, 31)))
+    x = dev_x(A.make_activations(512, K, seed=32))
+    need = lin.scratch_bytes(512)
+    assert need > 0
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        y1 = lin.forward(x)
+    torch.cuda.synchronize()
+    free0 = G.free_device_bytes()
+    gpu_lib.release_scratch(s)
+    assert G.free_device_bytes() >= free0 + need
+    with torch.cuda.stream(s):
+        y2 = lin.forward(x)
+    torch.cuda.synchronize()
+    assert _same(y1, y2)
+    gpu_lib.release_scratch(s)
+    gpu_lib.release_scratch(torch.cuda.Stream())
+    lin.close()
+
+
+def test_warmed_stream_capture_node_types(gpu_lib):
+    """The node types behind the graph tests' claims: on a stream whose workspace was
+    grown by the same calls, a capture of the decode path, the split-K GEMM, the pair
+    and the greedy head holds kernel nodes only; on a cold stream the scratch-taking
+    calls add allocation and free nodes; never a memset node."""
+    import ctypes
+
+    import torch
+
+    import hip_graph_nodes as G
+
+    lin, pair, head = _handles(gpu_lib)
+    xs = _inputs(6500)
+    lib = gpu_lib.load_library()
+    outs = []
+    for x in xs:
+        m = x.shape[0]
+        outs.append((x, torch.empty((m, N), dtype=torch.bfloat16, device="cuda"),
+                     torch.empty((m, F), dtype=torch.bfloat16, device="cuda"),
+                     torch.empty((m,), dtype=torch.int32, device="cuda"),
+                     torch.empty((m,), dtype=torch.float32, device="cuda")))
+
+    def issue(s):
+        for x, y, h, tok, val in outs:
+            m = x.shape[0]
+            lin.forward(x, out=y, stream=s)
+            pair.forward(x, out=h, stream=s)
+            if m <= 16:
+                st = lib.gemma4_qlinear_forward_greedy(head._handle, ctypes.c_void_p(s.cuda_stream),
+                                                       ctypes.c_void_p(x.data_ptr()), m, 30.0, None,
+                                                       gpu_lib.DTYPE_BF16, ctypes.c_void_p(tok.data_ptr()),
+                                                       ctypes.c_void_p(val.data_ptr()))
+                assert st == 0, gpu_lib.last_error()
+
+    cold = torch.cuda.Stream()
+    types_cold = G.capture_node_types(cold, lambda: issue(cold))
+    assert G.MEM_ALLOC in types_cold and G.MEM_FREE in types_cold, types_cold
+    assert G.MEMSET not in types_cold, types_cold
+    warm = torch.cuda.Stream()
+    issue(warm)
+    torch.cuda.synchronize()
+    types_warm = G.capture_node_types(warm, lambda: issue(warm))
+    assert types_warm and all(t == G.KERNEL for t in types_warm), types_warm
     for h in (lin, pair, head):
         h.close()

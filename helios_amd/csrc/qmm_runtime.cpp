@@ -159,6 +159,7 @@ struct StreamWorkspace {
 std::mutex g_ws_mu;
 std::vector<std::unique_ptr<StreamWorkspace>> g_ws;
 
+
 StreamWorkspace* stream_workspace(int device, hipStream_t stream) {
     const std::thread::id thread = stream == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
     std::lock_guard<std::mutex> lock(g_ws_mu);
@@ -722,6 +723,44 @@ Gemma4Status gemma4_qlinear_info(const Gemma4QLinear* linear, Gemma4QLinearInfo*
         return ok();
     } catch (...) {
         return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_info: unexpected native exception");
+    }
+}
+
+Gemma4Status gemma4_qmlp_forward(const Gemma4QLinear* gate_up, const Gemma4QLinear* down, void* stream,
+                                 const uint16_t* x_dev, uint32_t rows, uint16_t* h_dev, void* y_dev,
+                                 Gemma4QmmDtype y_dtype) {
+    try {
+        const std::string name("gemma4_qmlp_forward");
+        if (!valid_handle(gate_up) || !valid_handle(down))
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " received an invalid handle");
+        if (gate_up->pair_rows == 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": the first handle must be a gate|up pair "
+                                                            "(gemma4_qgeglu_create)");
+        if (down->pair_rows != 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": the second handle must be one projection (down_proj)");
+        if (down->desc.in_features != (uint32_t)gate_up->pair_rows)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": down's in_features (" +
+                                                         std::to_string(down->desc.in_features) +
+                                                         ") must equal the pair's F (" +
+                                                         std::to_string(gate_up->pair_rows) + ")");
+        if (down->device != gate_up->device)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": the two handles live on different devices");
+        if (y_dtype != GEMMA4_QMM_BF16)
+            return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, name + ": the MLP block runs in the bf16 model dtype "
+                                                              "(h is bf16; under the float32 override call "
+                                                              "gemma4_qgeglu_forward and gemma4_qlinear_forward)");
+        if (rows == 0) return ok();
+        if (x_dev == nullptr || h_dev == nullptr || y_dev == nullptr)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " requires non-null x, h and y");
+        if ((reinterpret_cast<uintptr_t>(h_dev) & 15u) != 0)
+            return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + ": h must be 16-byte aligned (it is down's x)");
+        // the pair's launch, then down's: the two separate calls' kernels
+        const Gemma4Status st = run_forward(gate_up, stream, x_dev, rows, h_dev, GEMMA4_QMM_BF16, true, false,
+                                            "gemma4_qmlp_forward (gate|up)");
+        if (st != GEMMA4_OK) return st;
+        return run_forward(down, stream, h_dev, rows, y_dev, y_dtype, false, false, "gemma4_qmlp_forward (down)");
+    } catch (...) {
+        return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qmlp_forward: unexpected native exception");
     }
 }
 

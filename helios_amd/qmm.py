@@ -105,6 +105,7 @@ def load_library(path: str | None = None):
         "gemma4_qmm_set_decode_kernel": [ctypes.c_uint32],
         "gemma4_qmm_release_scratch": [vp],
         "gemma4_qlinear_scratch_bytes": [vp, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint64)],
+        "gemma4_qmlp_forward": [vp, vp, vp, vp, ctypes.c_uint32, vp, vp, ctypes.c_uint32],
         "gemma4_qlinear_create": [ctypes.POINTER(_Desc), vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qlinear_create_device": [ctypes.POINTER(_Desc), vp, vp, vp, vp, ctypes.POINTER(vp)],
         "gemma4_qlinear_free": [vp],
@@ -457,6 +458,29 @@ class QuantizedGeGLU(_Handle):
                             self.out_features, out, out_dtype, stream)
 
     __call__ = forward
+
+    def forward_mlp(self, down, x, out=None, h=None, stream=None):
+        """The MLP block through gemma4_qmlp_forward: h = geglu(x . Wg^T, x . Wu^T) and
+        y = h . Wd^T on the projection `down` (in_features = F), bf16 throughout (the
+        reference's decode MLP, ``native_model.cc:1318-1321``).  One launch at one
+        row.  Returns (y [..., N_down], h [..., F]); `out` and `h` may be given."""
+        import torch
+
+        if x.dtype != torch.bfloat16 or x.shape[-1] != self.in_features:
+            raise Gemma4Error(Status.INVALID_ARGUMENT, f"x must be bfloat16 [..., {self.in_features}]")
+        lead = tuple(x.shape[:-1])
+        x2 = x.reshape(-1, self.in_features).contiguous()
+        rows = x2.shape[0]
+        if h is None:
+            h = torch.empty(lead + (self.out_features,), dtype=torch.bfloat16, device=x.device)
+        if out is None:
+            out = torch.empty(lead + (down.out_features,), dtype=torch.bfloat16, device=x.device)
+        for t, n, what in ((h, self.out_features, "h"), (out, down.out_features, "out")):
+            if t.dtype != torch.bfloat16 or tuple(t.shape) != lead + (n,) or not t.is_contiguous():
+                raise Gemma4Error(Status.INVALID_ARGUMENT, f"{what} has the wrong dtype, shape or layout")
+        check(self._lib.gemma4_qmlp_forward(self._handle, down._handle, _stream_ptr(stream), _dev_ptr(x2), rows,
+                                            _dev_ptr(h), _dev_ptr(out), DTYPE_BF16), self._lib)
+        return out, h
 
     def forward_raw(self, x_ptr: int, rows: int, h_ptr: int, f32: bool = False, stream_ptr: int = 0) -> None:
         """Direct C-ABI call on raw device pointers (benchmark loops)."""

@@ -203,6 +203,20 @@ Gemma4Status gemma4_qlinear_scratch_bytes(const Gemma4QLinear* linear, uint32_t 
 Gemma4Status gemma4_qlinear_forward_noalloc(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,
                                             uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype);
 
+/* The MLP block in one call — replaces the decode MLP's gate and up quantized_linear,
+ * geglu and down quantized_linear (native_model.cc:1318-1321; prefill :934-949):
+ *     h = geglu(x . Wg^T, x . Wu^T)   (bf16 [rows, F], written to h_dev)
+ *     y = h . Wd^T                    (bf16 [rows, N_down])
+ * gate_up is a pair from gemma4_qgeglu_create, down a projection whose in_features is
+ * the pair's F, on the same device.  It queues the pair's launch and then down's (the
+ * kernels of gemma4_qgeglu_forward and gemma4_qlinear_forward, so the same bits).
+ * y_dtype must be BF16 (the bf16 model dtype; under the float32 override h is fp32,
+ * which these kernels do not take as x): GEMMA4_ERR_UNSUPPORTED_CONFIG otherwise.
+ * h_dev is 16-byte aligned. */
+Gemma4Status gemma4_qmlp_forward(const Gemma4QLinear* gate_up, const Gemma4QLinear* down, void* stream,
+                                 const uint16_t* x_dev, uint32_t rows, uint16_t* h_dev, void* y_dev,
+                                 Gemma4QmmDtype y_dtype);
+
 /* Writes the fp32 dequantized weight W[N,K] = s*q + b (row-major) to w_dev —
  * mlx::core::dequantize (native_model.cc:364-376) with a float32 result.  Bit-exact:
  * the product s*q is exact in fp32, so the value is unique.  For a gate|up pair the

@@ -47,7 +47,7 @@ def test_decoder_48_layers_chained_m1(gpu_lib):
         assert chk["graph_equals_eager"], "graph replays differ from the eager forward"
         assert chk["token_stable"], f"token changed across replays: {chk}"
         assert 0 <= chk["token"] < 262144
-        assert 0.1 < chk["final_rms"] < 1e4
+        assert 0.1 < chk["final_rms"] < 1e6
 
         # layer 0 fed its own chain values, against float64 products
         L = net[0]

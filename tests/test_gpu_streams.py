@@ -221,8 +221,9 @@ def test_release_scratch(gpu_lib):
 
     import hip_graph_nodes as G
 
-    lin = gpu_lib.QuantizedLinear(*dev_triple(*random_triple(N, K, 31)))
-    x = dev_x(A.make_activations(512, K, seed=32))
+    # k_proj's shape at 512 rows: 64-row tiles with K split four ways (partial planes)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*random_triple(2048, 3840, 31)))
+    x = dev_x(A.make_activations(512, 3840, seed=32))
     need = lin.scratch_bytes(512)
     assert need > 0
     s = torch.cuda.Stream()

@@ -709,8 +709,11 @@ int decode_variant() { return g_decode_variant.load(std::memory_order_relaxed); 
 
 hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x, const OutParams& op, int m,
                          const Layout& l, hipStream_t stream) {
-    if (m == 1 && decode_variant() != 2 && limb_lds_bytes(l) <= kLdsPerCu)
-        return launch_decode_limbs(tiles, x, op, l, stream);
+    const int variant = decode_variant();
+    if (m == 1 && variant != 2 && limb_lds_bytes(l) <= kLdsPerCu) return launch_decode_limbs(tiles, x, op, l, stream);
+    if (m >= 2 && m <= 8 && variant != 2 && (variant == 1 || limb_rows_preferred(l, m)) &&
+        limb_rows_lds_bytes(l, m) <= kLdsPerCu)
+        return launch_decode_limb_rows(tiles, x, op, m, l, stream);
     if (m == 1) return launch_mt<1>(tiles, sb, x, op, m, l, stream);
     if (m == 2) return launch_mt<2>(tiles, sb, x, op, m, l, stream);
     if (m <= 4) return launch_mt<4>(tiles, sb, x, op, m, l, stream);

@@ -87,7 +87,7 @@ hipError_t launch_decode(const uint4* tiles, const uint2* sb, const uint16_t* x,
                          const Layout& l, hipStream_t stream);
 
 // Decode kernel family (a process-wide choice for tests and benchmarks): 0 automatic,
-// 1 the int8-limb kernel wherever it applies (one row of x), 2 the bf16 kernels only.
+// 1 the int8-limb kernels wherever they apply (1-8 rows of x), 2 the bf16 kernels only.
 // set_decode_variant returns the previous choice (an atomic exchange).
 int set_decode_variant(int v);
 int decode_variant();
@@ -98,6 +98,13 @@ int decode_variant();
 size_t limb_lds_bytes(const Layout& l);
 hipError_t launch_decode_limbs(const uint4* tiles, const uint16_t* x, const OutParams& op, const Layout& l,
                                hipStream_t stream);
+// 2-8 rows of x on the int8 matrix cores (rows padded to 2, 4 or 8); the launch fails
+// (hipErrorInvalidValue) where limb_rows_lds_bytes exceeds the CU's LDS.
+size_t limb_rows_lds_bytes(const Layout& l, int m);
+// whether the automatic choice takes them for m rows of this layout (measured per shape)
+bool limb_rows_preferred(const Layout& l, int m);
+hipError_t launch_decode_limb_rows(const uint4* tiles, const uint16_t* x, const OutParams& op, int m,
+                                   const Layout& l, hipStream_t stream);
 
 // token[m] (and value[m] when not null) = argmax over the keys part[m][0..nb) left by
 // the greedy modes, for m < rows.

@@ -286,6 +286,265 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_kernel(const uint4* __
     }
 }
 
+// Rows 2-8 of x (MT = 2, 4 or 8, the rows padded with zeros) on the int8 matrix cores,
+// the same limb split per (row, group).  The A rows of one MFMA are (group, row, limb)
+// triples with a zero row after each (row, group)'s three limbs:
+//   MT <= 4: the MFMA of group j of a chunk feeds accumulator j / (4 / MT); within it
+//            rows 4 MT (j % (4 / MT)) + 4m + l hold limb l of row m, so lane
+//            (quarter q, column n) ends with C_0..C_2 of group (q / MT) of that
+//            accumulator and row q % MT;
+//   MT = 8:  two MFMAs per group j on the same B operand, accumulators 2j and 2j + 1,
+//            rows 4m' + l of row 4h + m' (h = 0, 1), so lane (q, n) holds row 4h + q.
+// A lane accumulates one row (MT <= 4) or two (MT = 8); its scale words are those of
+// the groups it holds, two 4- or 8-byte loads per chunk.  Per chunk: 4 MFMAs (8 at
+// MT = 8) and MT scale steps per lane.
+template <int MT, int NBUF, int WAVES, bool STRIDED>
+__global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint4* __restrict__ tiles,
+                                                                      const uint16_t* __restrict__ x, OutParams op,
+                                                                      int m_rows, int n_rows, int k, int kx,
+                                                                      int gpairs, int nblocks) {
+    static_assert(MT == 2 || MT == 4 || MT == 8, "rows");
+    constexpr int kGpa = MT <= 4 ? 4 / MT : 1;  // groups per accumulator
+    constexpr int kAcc = MT;                     // accumulators per chunk
+    constexpr int kMfma = MT <= 4 ? 4 : 8;       // MFMAs per chunk
+    constexpr int kRows = MT <= 4 ? 1 : 2;       // rows a lane accumulates
+    constexpr int kChunkBytes = 4 * MT * 3 * kLimbUnitBytes * 4;  // [group][row][limb][quarter] x 16 B
+    constexpr int kChunkStride = kChunkBytes + kLimbUnitBytes;    // then one zero unit
+    extern __shared__ uint4 lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15;
+    const int quarter = lane >> 4;
+    const int groups = k >> 6;
+    const int nch = (gpairs + 1) >> 1;
+    const int rb0 = STRIDED ? (int)blockIdx.x : (int)(((uint32_t)blockIdx.x * (uint32_t)nblocks) / gridDim.x);
+    const int nrb = STRIDED ? (nblocks - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x
+                            : (int)(((uint32_t)blockIdx.x * (uint32_t)nblocks + (uint32_t)nblocks) / gridDim.x) - rb0;
+    const int rbs = STRIDED ? (int)gridDim.x : 1;
+    const int total = nrb * nch;
+    char* const limbs = reinterpret_cast<char*>(lds);
+    float2* const tab = reinterpret_cast<float2*>(limbs + nch * kChunkStride);  // [nch][4][MT] (2^(e-135), 8 X 2^(132-e))
+    float* const slots = reinterpret_cast<float*>(tab + nch * 4 * MT);          // [nrb][WAVES][MT][16]
+
+    // scale words: MT = 2: groups q/2 (record 0) and 2 + q/2 (record 1), 4 bytes each;
+    // MT >= 4: all four groups, 8 bytes of each record
+    const uint32_t sb0 = (uint32_t)(kRecSbBytes + col * 8 + (MT == 2 ? (quarter >> 1) * 4 : 0));
+    uint4 t0[NBUF], t1[NBUF];
+    uint32_t sw[NBUF][4];
+    int i_f = wave, i_rb = 0, i_c = wave;
+    while (i_c >= nch) {
+        i_c -= nch;
+        ++i_rb;
+    }
+    auto issue = [&](int b) {
+        const bool live = i_f < total;
+        const int left = gpairs - 2 * i_c;
+        const int nrec = !live ? 0 : left < 2 ? left : 2;
+        const long first = live ? (long)(rb0 + i_rb * rbs) * gpairs + 2 * i_c : 0;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(tiles + first * kRecU4, (uint32_t)nrec * kRecBytes);
+        t0[b] = buffer_load16<kNonTemporal>(rs, (uint32_t)(lane * 16));
+        t1[b] = buffer_load16<kNonTemporal>(rs, (uint32_t)(kRecBytes + lane * 16));
+        if constexpr (MT == 2) {
+            sw[b][0] = buffer_load4(rs, sb0);
+            sw[b][1] = buffer_load4(rs, kRecBytes + sb0);
+        } else {
+            const uint2 a = buffer_load8<kNonTemporal>(rs, sb0);
+            const uint2 c = buffer_load8<kNonTemporal>(rs, kRecBytes + sb0);
+            sw[b][0] = a.x;
+            sw[b][1] = a.y;
+            sw[b][2] = c.x;
+            sw[b][3] = c.y;
+        }
+        i_f += WAVES;
+        i_c += WAVES;
+        while (i_c >= nch) {
+            i_c -= nch;
+            ++i_rb;
+        }
+    };
+
+    // x' rows -> limbs; unit f = m * (nch * 32) + u, u the 16-byte unit of row m's x'
+    // (group u / 8, half (u / 4) % 2, k-quarter u % 4): the eight units of a (row,
+    // group) are eight consecutive lanes.  Rows >= m_rows and groups past K stage zeros.
+    constexpr int nthr = WAVES * 64;
+    const int runits = nch * 32;
+    const int units = MT * runits;
+    const int xunits = groups * 8;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)kx * 2u);
+    auto load_unit = [&](int f) {
+        const int m = f / runits, u = f - m * runits;
+        const bool ok = m < m_rows && u < xunits;
+        return buffer_load16(xrs, ok ? (uint32_t)m * (uint32_t)kx * 2u + xprime_offset(u, k, kx) : kOutOfRange);
+    };
+    auto stage = [&](const uint4 v, int f) {
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+        uint32_t mb = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t lo = w4[j] & 0x7FFFu, hi = (w4[j] >> 16) & 0x7FFFu;
+            mb = mb > lo ? mb : lo;
+            mb = mb > hi ? mb : hi;
+        }
+#pragma unroll
+        for (int d = 1; d < 8; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_xor((int)mb, d);
+            mb = mb > o ? mb : o;
+        }
+        const int ex = (int)(mb >> 7);
+        const int e = ex < 19 ? 19 : ex > 254 ? 254 : ex;
+        const float scale = __uint_as_float((uint32_t)(273 - e) << 23);  // 2^(146 - e)
+        const float unit = __uint_as_float((uint32_t)(259 - e) << 23);   // 2^(132 - e)
+        float sum = 0.f;
+        uint32_t l0[8], l1[8], l2[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float xv = (i & 1) ? bf16_hi(w4[i >> 1]) : bf16_lo(w4[i >> 1]);
+            sum += xv * unit;
+            const uint32_t bits = __float_as_uint(__builtin_fmaf(xv, scale, 12582912.0f));
+            l2[i] = bits;
+            l1[i] = bits >> 7;
+            l0[i] = (uint32_t)__builtin_amdgcn_sbfe((int)bits, 14, 8);
+        }
+#pragma unroll
+        for (int d = 1; d < 8; d <<= 1) sum += __shfl_xor(sum, d);
+        const uint2 p0 = make_uint2(pack_bytes(l0[0], l0[4], l0[1], l0[5]), pack_bytes(l0[2], l0[6], l0[3], l0[7]));
+        const uint2 p1 = make_uint2(pack_bytes(l1[0], l1[4], l1[1], l1[5]) & 0x7F7F7F7Fu,
+                                    pack_bytes(l1[2], l1[6], l1[3], l1[7]) & 0x7F7F7F7Fu);
+        const uint2 p2 = make_uint2(pack_bytes(l2[0], l2[4], l2[1], l2[5]) & 0x7F7F7F7Fu,
+                                    pack_bytes(l2[2], l2[6], l2[3], l2[7]) & 0x7F7F7F7Fu);
+        if (f < units) {
+            const int m = f / runits, u = f - m * runits;
+            const int g = u >> 3, h = (u >> 2) & 1, kq = u & 3;
+            char* const base = limbs + (g >> 2) * kChunkStride + (((g & 3) * MT + m) * 3) * 64 + kq * 16 + h * 8;
+            *reinterpret_cast<uint2*>(base) = p0;
+            *reinterpret_cast<uint2*>(base + 64) = p1;
+            *reinterpret_cast<uint2*>(base + 128) = p2;
+            if ((u & 7) == 0) {
+                const float fs = ex == 255 ? __uint_as_float(0x7FC00000u) : __uint_as_float((uint32_t)(e - 8) << 23);
+                tab[(g >> 2) * 4 * MT + (g & 3) * MT + m] = make_float2(fs, 8.0f * sum);
+            }
+        }
+    };
+    const uint4 xa = load_unit((int)threadIdx.x);
+    const uint4 xb = load_unit(nthr + (int)threadIdx.x);
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) issue(b);
+    stage(xa, (int)threadIdx.x);
+    if (nthr < units) stage(xb, nthr + (int)threadIdx.x);
+    for (int f0 = 2 * nthr; f0 < units; f0 += nthr) stage(load_unit(f0 + (int)threadIdx.x), f0 + (int)threadIdx.x);
+    for (int c = (int)threadIdx.x; c < nch; c += nthr)
+        *reinterpret_cast<uint4*>(limbs + c * kChunkStride + kChunkBytes) = make_uint4(0, 0, 0, 0);
+    for (int t = (int)threadIdx.x; t < nrb * WAVES * MT * 16; t += nthr) slots[t] = 0.f;
+    __syncthreads();
+
+    // A operand address of MFMA i of a chunk for this lane (row r = col, k-quarter)
+    uint32_t a_off[kMfma];
+#pragma unroll
+    for (int i = 0; i < kMfma; ++i) {
+        const int r = col, l = r & 3;
+        int j, m;
+        bool on;
+        if constexpr (MT <= 4) {
+            j = i;
+            m = (r % (4 * MT)) >> 2;
+            on = (r / (4 * MT)) == (i % kGpa) && l < 3;
+        } else {
+            j = i >> 1;
+            m = 4 * (i & 1) + (r >> 2);
+            on = l < 3;
+        }
+        a_off[i] = on ? (uint32_t)(((j * MT + m) * 3 + l) * 64 + quarter * 16) : (uint32_t)kChunkBytes;
+    }
+
+    float acc[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) acc[r] = 0.f;
+    int c_f = wave, c_rb = 0, c_c = wave;
+    while (c_c >= nch) {
+        c_c -= nch;
+        ++c_rb;
+    }
+    auto compute = [&](int b) {
+        const char* const cl = limbs + c_c * kChunkStride;
+        i32x4 C[kAcc];
+#pragma unroll
+        for (int a = 0; a < kAcc; ++a) C[a] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < kMfma; ++i) {
+            const int j = MT <= 4 ? i : i >> 1;
+            const int a = MT <= 4 ? i / kGpa : i;
+            const uint4 t = (j >> 1) ? t1[b] : t0[b];
+            const i32x4 B = (j & 1) ? expand_i8(t.z, t.w) : expand_i8(t.x, t.y);
+            const i32x4 A = *reinterpret_cast<const i32x4*>(cl + a_off[i]);
+            C[a] = mfma_i8(A, B, C[a]);
+        }
+        const float2* const tc = tab + c_c * 4 * MT;
+#pragma unroll
+        for (int a = 0; a < kAcc; ++a) {
+            // the lane's (group, row) in accumulator a, and its scale word
+            const int j = MT <= 4 ? a * kGpa + quarter / MT : a >> 1;
+            const int m = MT <= 4 ? quarter % MT : 4 * (a & 1) + quarter;
+            const uint32_t w = MT == 2 ? sw[b][a] : MT == 4 ? sw[b][a] : sw[b][a >> 1];
+            const float2 tv = tc[j * MT + m];
+            const float p = __builtin_fmaf(__builtin_fmaf((float)C[a][2], 0x1p-7f, (float)C[a][1]), 0x1p-7f,
+                                           (float)C[a][0]);
+            float& r = acc[MT <= 4 ? 0 : (a & 1)];
+            r = __builtin_fmaf(bf16_lo(w) * tv.x, p, r);
+            r = __builtin_fmaf(bf16_hi(w) * tv.x, tv.y, r);
+        }
+        const int rb = c_rb;
+        c_f += WAVES;
+        c_c += WAVES;
+        while (c_c >= nch) {
+            c_c -= nch;
+            ++c_rb;
+        }
+        if (c_rb != rb || c_f >= total) {
+            float* const sl = slots + (rb * WAVES + wave) * MT * 16;
+            if constexpr (MT == 2) {
+                const float v = acc[0] + __shfl_xor(acc[0], 32);
+                if (quarter < 2) sl[quarter * 16 + col] = v;
+            } else if constexpr (MT == 4) {
+                sl[quarter * 16 + col] = acc[0];
+            } else {
+                sl[quarter * 16 + col] = acc[0];
+                sl[(4 + quarter) * 16 + col] = acc[1];
+            }
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) acc[r] = 0.f;
+        }
+    };
+
+    const int mine = wave < total ? (total - wave + WAVES - 1) / WAVES : 0;
+    int i = 0;
+    for (; i + NBUF <= mine; i += NBUF) {
+#pragma unroll
+        for (int b = 0; b < NBUF; ++b) {
+            compute(b);
+            issue(b);
+        }
+    }
+#pragma unroll
+    for (int b = 0; b + 1 < NBUF; ++b)
+        if (i + b < mine) compute(b);
+
+    __syncthreads();
+    // every (row block, row)'s 16 outputs: the waves' slots summed in wave order; a
+    // 16-lane row of a wave holds one (row block, row) (the GeGLU and greedy stages
+    // work within it)
+    for (int t0 = 0; t0 < nrb * MT * 16; t0 += nthr) {
+        const int t = t0 + (int)threadIdx.x;
+        const bool live = t < nrb * MT * 16;
+        const int r = t / (MT * 16), m = (t >> 4) % MT;
+        float v = 0.f;
+        if (live) {
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) v += slots[((r * WAVES + w) * MT + m) * 16 + col];
+        }
+        store_out(op, live ? m : MT, m_rows, rb0 + (live ? r : 0) * rbs, col, n_rows, v);
+    }
+}
+
 }  // namespace
 
 namespace {
@@ -328,6 +587,103 @@ size_t limb_lds_bytes(const Layout& l) {
     const int grid = limb_grid(l, c);
     const size_t nrb = ((size_t)l.nb + grid - 1) / grid;
     return nch * kLimbChunkStride + nch * 4 * sizeof(float2) + nrb * c.waves * 16 * sizeof(float);
+}
+
+namespace {
+// Rows 2-8.  Launch shapes from a sweep at 4 and 8 rows (us per launch, graph replays
+// of back-to-back launches; the bf16 kernels in brackets), 16-wave workgroups for the
+// padded rows' longer scale steps:
+//  * up to four row blocks per CU: one workgroup per CU, two chunks in flight,
+//    contiguous runs: gate 15360x3840 9.5 / 11.6 (12.3 / 13.5);
+//  * more, up to 16 per CU: two workgroups per CU, one chunk in flight, blocks dealt
+//    round the grid: the gate|up pair 14.6 / 18.4 (19.1 / 20.4);
+//  * more still (the lm_head): 8 waves, two per CU, two chunks in flight, dealt round
+//    the grid: 95.6 / 119.6 (101.6 / 119.5).
+// At 2 rows the one-row kernel's shapes.  Workgroups per CU are capped by what LDS
+// admits (the per-(row block, wave) sums take MT times the one-row kernel's room), and
+// the grid grows (more, shorter row-block runs) until one workgroup fits.
+struct LimbRowsPlan {
+    LimbConfig c;
+    int grid;
+    size_t lds;
+};
+size_t limb_rows_lds(const Layout& l, int mt, int waves, int grid) {
+    const size_t nch = (size_t)(l.gp + 1) / 2;
+    const size_t nrb = ((size_t)l.nb + grid - 1) / grid;
+    return nch * ((size_t)4 * mt * 3 * 64 + kLimbUnitBytes) + nch * 4 * mt * sizeof(float2) +
+           nrb * waves * mt * 16 * sizeof(float);
+}
+LimbRowsPlan limb_rows_plan(const Layout& l, int mt) {
+    LimbRowsPlan p;
+    const int cus = device_cus();
+    if (mt == 2)
+        p.c = limb_config(l);
+    else if (l.nb <= 4 * cus)
+        p.c = {16, 1, 2, false};
+    else if (l.nb <= 16 * cus)
+        p.c = {16, 2, 1, true};
+    else
+        p.c = {8, 2, 2, true};
+    int per_cu = p.c.per_cu;
+    for (;;) {
+        p.grid = l.nb < cus * per_cu ? l.nb : cus * per_cu;
+        p.lds = limb_rows_lds(l, mt, p.c.waves, p.grid);
+        const int fit = (int)(((size_t)160 * 1024) / p.lds);
+        if (fit >= per_cu || per_cu == 1) break;
+        per_cu = fit > 1 ? fit : 1;
+    }
+    while (p.lds > (size_t)160 * 1024 && p.grid < l.nb) {
+        p.grid = p.grid * 2 < l.nb ? p.grid * 2 : l.nb;
+        p.lds = limb_rows_lds(l, mt, p.c.waves, p.grid);
+    }
+    return p;
+}
+int rows_mt(int m) { return m <= 2 ? 2 : m <= 4 ? 4 : 8; }
+}  // namespace
+
+size_t limb_rows_lds_bytes(const Layout& l, int m) { return limb_rows_plan(l, rows_mt(m)).lds; }
+
+bool limb_rows_preferred(const Layout& l, int m) {
+    if (m == 2) return true;
+    // 3-8 rows: only wide 4-bit outputs gain (qkv and o lose at 8 rows, the lm_head
+    // ties there); the two-plane 8-bit handles were not measured on these shapes
+    const int cus = device_cus();
+    return l.kx == l.k && l.nb >= 3 * cus && (m <= 4 || l.nb <= 16 * cus);
+}
+
+hipError_t launch_decode_limb_rows(const uint4* tiles, const uint16_t* x, const OutParams& op, int m,
+                                   const Layout& l, hipStream_t stream) {
+    const int mt = rows_mt(m);
+    const LimbRowsPlan p = limb_rows_plan(l, mt);
+    if (m < 2 || m > 8 || p.lds > (size_t)160 * 1024) return hipErrorInvalidValue;
+    const dim3 grid(p.grid), block(64 * p.c.waves);
+#define Q4_LR(MT, NB, W, ST)                                                                                     \
+    hipLaunchKernelGGL((decode_limb_rows_kernel<MT, NB, W, ST>), grid, block, p.lds, stream, tiles, x, op, m, l.n, \
+                       l.k, l.kx, l.gp, l.nb)
+    if (mt == 2) {
+        if (p.c.waves == 16)
+            Q4_LR(2, 3, 16, false);
+        else if (!p.c.strided)
+            Q4_LR(2, 2, 8, false);
+        else
+            Q4_LR(2, 1, 8, true);
+    } else if (mt == 4) {
+        if (!p.c.strided)
+            Q4_LR(4, 2, 16, false);
+        else if (p.c.waves == 16)
+            Q4_LR(4, 1, 16, true);
+        else
+            Q4_LR(4, 2, 8, true);
+    } else {
+        if (!p.c.strided)
+            Q4_LR(8, 2, 16, false);
+        else if (p.c.waves == 16)
+            Q4_LR(8, 1, 16, true);
+        else
+            Q4_LR(8, 2, 8, true);
+    }
+#undef Q4_LR
+    return hipGetLastError();
 }
 
 hipError_t launch_decode_limbs(const uint4* tiles, const uint16_t* x, const OutParams& op, const Layout& l,

@@ -468,3 +468,142 @@ def test_decode_limb_accesses(n, k):
 @pytest.mark.parametrize("n,k", [(15360, 3840), (48, 576), (130, 1088), (3840, 15360), (262144, 3840)])
 def test_decode_limb_accesses_two_plane(n, k):
     audit_decode_limbs(n, 2 * k, kx=k)
+
+
+def limb_rows_plan(nb, gp, mt, cus=256):
+    """q4_limbs.hip limb_rows_plan: at 2 rows the one-row launch shape, at 4 and 8 the
+    swept shapes; workgroups per CU capped by the LDS, then the grid doubled (up to one
+    workgroup per row block) until one fits.  Returns (waves, nbuf, strided, grid, lds)."""
+    if mt == 2:
+        waves, per_cu, nbuf, strided = limb_config(nb, gp, cus)
+    elif nb <= 4 * cus:
+        waves, per_cu, nbuf, strided = 16, 1, 2, False
+    elif nb <= 16 * cus:
+        waves, per_cu, nbuf, strided = 16, 2, 1, True
+    else:
+        waves, per_cu, nbuf, strided = 8, 2, 2, True
+    nch = (gp + 1) // 2
+
+    def lds(g):
+        nrb = (nb + g - 1) // g
+        return nch * (4 * mt * 3 * 64 + 16) + nch * 4 * mt * 8 + nrb * waves * mt * 16 * 4
+
+    while True:
+        grid = min(nb, cus * per_cu)
+        fit = LDS_BYTES // lds(grid)
+        if fit >= per_cu or per_cu == 1:
+            break
+        per_cu = max(fit, 1)
+    while lds(grid) > LDS_BYTES and grid < nb:
+        grid = min(2 * grid, nb)
+    return waves, nbuf, strided, grid, lds(grid)
+
+
+def audit_decode_limb_rows(m_rows, n, k, kx=None, cus=256):
+    """decode_limb_rows_kernel (2-8 rows of x): the chunk walk as in the one-row kernel;
+    the scale-word loads; the staging of m_rows x' rows into [chunk][group][row][limb]
+    [quarter] limb units, the (chunk, group, row) table and the zero unit; the A operand
+    reads of every MFMA; the (row block, wave, row) slots and the final stores."""
+    kx = k if kx is None else kx
+    mt = 2 if m_rows <= 2 else 4 if m_rows <= 4 else 8
+    L = layout(n, k)
+    nb, gp = L["nb"], L["gp"]
+    waves, nbuf, strided, grid, lds = limb_rows_plan(nb, gp, mt, cus)
+    if lds > LDS_BYTES:
+        return None  # the launcher refuses it (the bf16 kernels run)
+    nch = (gp + 1) // 2
+    chunk_bytes = 4 * mt * 3 * 64
+    stride = chunk_bytes + 16
+    lane = np.arange(64)
+    col, quarter = lane & 15, lane >> 4
+    sb0 = REC_SB + col * 8 + ((quarter >> 1) * 4 if mt == 2 else 0)
+    sw_size = 4 if mt == 2 else 8
+    seen = np.zeros((nb, nch), np.int64)
+    stored = np.zeros((nb, mt), np.int64)
+    nrb_max = 0
+    for b in range(grid):
+        if strided:
+            rb0, nrb, rbs = b, (nb - b + grid - 1) // grid, grid
+        else:
+            rb0 = b * nb // grid
+            nrb, rbs = (b * nb + nb) // grid - rb0, 1
+        nrb_max = max(nrb_max, nrb)
+        total = nrb * nch
+        for w in range(waves):
+            mine = (total - w + waves - 1) // waves if w < total else 0
+            for i in range(mine + nbuf):
+                f = w + i * waves
+                live = f < total
+                i_rb, c = divmod(f, nch)
+                nrec = min(2, gp - 2 * c) if live else 0
+                base = ((rb0 + i_rb * rbs) * gp + 2 * c) * REC if live else 0
+                for off, size in ((lane * 16, 16), (REC + lane * 16, 16), (sb0, sw_size), (REC + sb0, sw_size)):
+                    inr = off < nrec * REC
+                    assert (off[inr] + size <= nrec * REC).all()
+                    assert (base + off[inr] + size <= L["rec_bytes"]).all()
+                if live:
+                    seen[rb0 + i_rb * rbs, c] += 1
+                    # the lane's slot rows and the chunk's table entries
+                    assert ((i_rb * waves + w) * mt + mt - 1) * 16 + 15 < nrb * waves * mt * 16
+                    assert (c * 4 * mt + 3 * mt + mt - 1) < nch * 4 * mt
+        for r in range(nrb):
+            stored[rb0 + r * rbs] += 1
+    assert (seen == 1).all() and (stored == 1).all()
+    assert nch * stride + nch * 4 * mt * 8 + nrb_max * waves * mt * 16 * 4 == lds
+    # staging: flat unit f -> (row m, unit u); writes inside the chunk's limb region
+    runits = nch * 32
+    f = np.arange(mt * runits)
+    m, u = f // runits, f % runits
+    g, h, kq = u >> 3, (u >> 2) & 1, u & 3
+    base = (g >> 2) * stride + (((g & 3) * mt + m) * 3) * 64 + kq * 16 + h * 8
+    assert (base + 128 + 8 <= nch * stride).all() and ((base % stride) + 128 + 8 <= chunk_bytes).all()
+    assert (((g >> 2) * 4 * mt + (g & 3) * mt + m) < nch * 4 * mt).all()
+    ok = (m < m_rows) & (u < (k // 64) * 8)
+    assert (m[ok] * kx * 2 + xprime_offset(u[ok], k, kx) + 16 <= m_rows * kx * 2).all()
+    # every unit of a (row, group) lies in one 8-lane run (the max and sum shuffles)
+    assert ((f // 8) == (m * runits + (u // 8) * 8) // 8).all()
+    # A operands: MFMA i of a chunk, lane (row r = col, quarter)
+    mfmas = 4 if mt <= 4 else 8
+    gpa = 4 // mt if mt <= 4 else 1
+    hits = np.zeros((4, mt, 3, 4), np.int64)
+    for i in range(mfmas):
+        for r in range(16):
+            for q in range(4):
+                l = r & 3
+                if mt <= 4:
+                    j, mm, on = i, (r % (4 * mt)) >> 2, (r // (4 * mt)) == (i % gpa) and l < 3
+                else:
+                    j, mm, on = i >> 1, 4 * (i & 1) + (r >> 2), l < 3
+                off = ((j * mt + mm) * 3 + l) * 64 + q * 16 if on else chunk_bytes
+                assert off + 16 <= stride
+                if on:
+                    hits[j, mm, l, q] += 1
+    assert (hits == 1).all()  # every (group, row, limb, quarter) unit read by exactly one MFMA lane
+    # final stores: t -> (row block run index, row, column) covers every output once
+    t = np.arange(nrb_max * mt * 16)
+    r, mm = t // (mt * 16), (t >> 4) % mt
+    assert (((r * waves + waves - 1) * mt + mm) * 16 + 15 < nrb_max * waves * mt * 16).all()
+    return lds
+
+
+# the largest shapes (thousands of row blocks per launch) at 8 rows only, where the
+# slots press hardest on the LDS
+ROWS_SHAPES = [(40, 384), (64, 320), (16, 64), (4096, 3840), (2048, 3840), (3840, 4096), (15360, 3840),
+               (3840, 15360), (33, 640), (8192, 3840), (40, 192), (1000, 192)]
+
+
+@pytest.mark.parametrize("m", [2, 5, 8])
+@pytest.mark.parametrize("n,k", ROWS_SHAPES)
+def test_decode_limb_rows_accesses(m, n, k):
+    audit_decode_limb_rows(m, n, k)
+
+
+@pytest.mark.parametrize("n,k", [(30720, 3840), (262144, 3840), (70000, 3840), (131072 + 48, 128)])
+def test_decode_limb_rows_accesses_wide(n, k):
+    audit_decode_limb_rows(8, n, k)
+
+
+@pytest.mark.parametrize("m", [2, 4, 8])
+@pytest.mark.parametrize("n,k", [(15360, 3840), (48, 576), (3840, 15360)])
+def test_decode_limb_rows_accesses_two_plane(m, n, k):
+    audit_decode_limb_rows(m, n, 2 * k, kx=k)

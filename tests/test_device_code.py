@@ -118,3 +118,18 @@ def test_limb_register_budgets():
         nbuf, waves = map(int, re.search(r"decode_limb_kernelILi(\d+)ELi(\d+)E", name).groups())
         limit = 85 if nbuf == 1 else (128 if waves == 16 else 256)
         assert vgprs <= limit, f"{name}: {vgprs} VGPRs"
+
+
+def test_limb_rows_register_budgets():
+    """decode_limb_rows_kernel: no scratch; the 16-wave instance dealt round the grid at
+    4 rows runs two workgroups per CU (8 waves per SIMD: at most 64 VGPRs); the rest
+    run one 16-wave workgroup per CU (at most 128) or 8-wave ones."""
+    asm = hbuild.device_asm("q4_limbs.hip")
+    meta = [(n, v, p) for n, v, p in _kernel_meta(asm) if "decode_limb_rows_kernel" in n]
+    assert len(meta) == 9
+    for name, vgprs, private in meta:
+        assert private == 0, f"{name} spills to scratch"
+        mt, nbuf, waves = map(int, re.search(r"decode_limb_rows_kernelILi(\d+)ELi(\d+)ELi(\d+)E", name).groups())
+        limit = 64 if (mt == 4 and nbuf == 1 and waves == 16) else 128 if waves == 16 else 256
+        assert vgprs <= limit, f"{name}: {vgprs} VGPRs"
+

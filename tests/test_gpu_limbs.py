@@ -1,4 +1,4 @@
-"""GPU parity of the int8-limb decode kernel (q4_limbs.hip, one row of x).
+"""GPU parity of the int8-limb decode kernels (q4_limbs.hip: one row of x, and 2-8 rows).
 
 The kernel splits every 64-column group of x into three int8 limbs relative to the
 group's largest magnitude (exact for every x within 2^12 of it, rounded at 2^-21 of
@@ -170,3 +170,108 @@ def test_deterministic_and_agrees_with_bf16_kernels(gpu_lib):
     rms = c.pow(2).mean().sqrt().item()
     assert (a - c).abs().max().item() <= 2 * ACC_REL * rms
     lin.close()
+
+
+# ---- 2-8 rows (decode_limb_rows_kernel, pinned with gemma4_qmm_set_decode_kernel(1)) ----
+# Rows pad to 2, 4 or 8; where the limbs of x and the slots do not fit a CU's LDS (down
+# at more than 2 rows) the pinned family falls back to the bf16 kernels, so every case
+# still holds the bars.
+
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 8])
+@pytest.mark.parametrize("proj", sorted(PROJ) + ["qkv_proj"])
+def test_rows_projections(gpu_lib, proj, m):
+    if proj == "qkv_proj":
+        parts = [A.make_weights(*PROJ[p], seed=4300 + i) for i, p in enumerate(("q_proj", "k_proj", "v_proj"))]
+        wq, s, b = (np.concatenate([p[j] for p in parts]) for j in range(3))
+        k = 3840
+    else:
+        n, k = PROJ[proj]
+        wq, s, b = A.make_weights(n, k, seed=4400 + sorted(PROJ).index(proj))
+    x = A.make_activations(m, k, seed=4500 + m, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    y_exact = C.qmm_f64(x, wq, s, b)
+    y_f = run(lin, x, True, 1, gpu_lib)
+    assert assert_close(y_f, y_exact, f"{proj} m={m} f32") < ACC_REL
+    y_b = run(lin, x, False, 1, gpu_lib)
+    assert_rounded(y_b, y_exact, f"{proj} m={m} bf16")
+    lin.close()
+
+
+@pytest.mark.parametrize("m", [2, 3, 6, 7])
+@pytest.mark.parametrize("n,k", [(40, 320), (1000, 192), (16, 64), (33, 640), (4096 + 8, 3840), (20000, 576),
+                                 (70000 + 40, 384), (3840, 15360)])
+def test_rows_launch_shapes(gpu_lib, n, k, m):
+    wq, s, b = random_triple(n, k, seed=n + 5 * k + m)
+    x = A.make_activations(m, k, seed=n + m, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    y_exact = C.qmm_f64(x, wq, s, b)
+    y_f = run(lin, x, True, 1, gpu_lib)
+    assert assert_close(y_f, y_exact, f"{n}x{k} m={m} f32") < ACC_REL
+    lin.close()
+
+
+@pytest.mark.parametrize("m", [2, 4, 8])
+def test_rows_wide_dynamic_range_and_non_finite(gpu_lib, m):
+    """Rows whose groups span the bf16 exponent range (each row its own exponents), and
+    a row holding inf: that row's outputs are non-finite, the others unaffected."""
+    import torch
+
+    n, k = 15360, 3840
+    wq, s, b = random_triple(n, k, seed=80 + m)
+    x = np.concatenate([_wide_range_x(k, seed=k + r, group_spread=100 * (r % 2)) for r in range(m)])
+    y_exact = C.qmm_f64(x, wq, s, b)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    y_f = run(lin, x, True, 1, gpu_lib)
+    assert assert_close(y_f, y_exact, f"wide range m={m} f32") < ACC_REL
+    xi = A.bf16_bits_to_f32(x).copy()
+    xi[m - 1, 77] = np.inf
+    y_i = host_bits(run(lin, A.f32_to_bf16_bits(xi), True, 1, gpu_lib))
+    assert not np.isfinite(y_i[m - 1]).any() and np.isfinite(y_i[: m - 1]).all()
+    lin.close()
+    del torch
+
+
+@pytest.mark.parametrize("m", [2, 4, 8])
+def test_rows_gate_up_pair(gpu_lib, m):
+    from test_gpu_geglu import _check, _exact_gu
+
+    gate = A.make_weights(15360, 3840, seed=4600)
+    up = A.make_weights(15360, 3840, seed=4601)
+    x = A.make_activations(m, 3840, seed=4700 + m, outliers=True)
+    pair = gpu_lib.QuantizedGeGLU(dev_triple(*gate), dev_triple(*up))
+    import torch
+
+    with gpu_lib.decode_kernel(1):
+        h = pair.forward(dev_x(x))
+        hf = pair.forward(dev_x(x), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    g_exact, u_exact = _exact_gu(x, gate, up)
+    _check(h, g_exact, u_exact, f"pair m={m} bf16")
+    _check(hf, g_exact, u_exact, f"pair m={m} f32")
+    pair.close()
+
+
+@pytest.mark.parametrize("m", [2, 8])
+def test_rows_lm_head_and_greedy(gpu_lib, m):
+    """The lm_head at 2 and 8 rows (every output against the oracle) and its greedy
+    head under the int8 kernels."""
+    import torch
+
+    from test_gpu_greedy import _check_token, _oracle
+    from test_gpu_parity import lm_head_triple
+
+    wq, s, b = lm_head_triple()
+    x = A.make_activations(m, 3840, seed=4800 + m)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    y_exact = C.qmm_f64(x, wq, s, b)
+    y_f = run(lin, x, True, 1, gpu_lib)
+    assert assert_close(y_f, y_exact, f"lm_head m={m} f32") < ACC_REL
+    with gpu_lib.decode_kernel(1):
+        tok, val, logits = lin.forward_greedy(dev_x(x), softcap=30.0, return_logits=True)
+    torch.cuda.synchronize()
+    sc = A.softcap_ops(y_exact.astype(np.float32), 30.0, bf16=True)
+    _check_token(tok.cpu().numpy(), sc, True)
+    lg = host_bits(logits)
+    assert np.array_equal(A.bf16_bits_to_f32(lg[np.arange(m), tok.cpu().numpy()]), val.cpu().numpy())
+    lin.close()
+    del _oracle

@@ -141,6 +141,19 @@ enum OutMode : int {
     kOutGegluF32 = 3,    // h fp32 [M, F], the float32 override's GeGLU
     kOutGreedyBf16 = 4,  // lm_head: softcap in bf16 ops, optional logits, best (value, index) per block
     kOutGreedyF32 = 5,   // the same in fp32
+    kOutLoraBf16 = 6,    // GEMM only: y bf16 = base + the LoRA delta (LoraEpilogue), bf16 ops
+    kOutLoraF32 = 7,     // the same in fp32
+};
+
+// The LoRA delta a GEMM epilogue adds to its outputs (kOutLora*): t = x . A^T as
+// `slices` fp32 partial planes [slices][M][rank] (summed in slice order), B [N][rank]
+// fp32, the adapter's scale; rank a multiple of 4, at most 32.
+struct LoraEpilogue {
+    const float* part;
+    const float* b;
+    int rank;
+    int slices;
+    float scale;
 };
 
 // Where and how a decode kernel writes its outputs.

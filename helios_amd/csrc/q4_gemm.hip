@@ -131,6 +131,103 @@ __device__ __forceinline__ void tile_of(int id, int nwg, int mtiles, int ntiles,
     nt = r / bm;
 }
 
+// t = x . A^T of a workgroup's BM rows into LDS (`ts`, [BM][rank] floats: the x ring's
+// first slot, BM x 128 bytes, so rank <= 32), each entry summed over its slices in
+// slice order; rows past the output read as zeros.  All of the workgroup's threads,
+// one barrier after.
+template <int BM>
+__device__ __forceinline__ void lora_stage_t(const LoraEpilogue& lo, float* ts, int row0, int m_rows, int nthr) {
+    const int q4s = lo.rank >> 2;  // float4s per row
+    for (int t = (int)threadIdx.x; t < BM * q4s; t += nthr) {
+        const int row = t / q4s, r = 4 * (t - row * q4s);
+        const int m = row0 + row;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (m < m_rows) {
+            v = *reinterpret_cast<const float4*>(lo.part + (long)m * lo.rank + r);
+            for (int sl = 1; sl < lo.slices; ++sl) {
+                const float4 u = *reinterpret_cast<const float4*>(lo.part + ((long)sl * m_rows + m) * lo.rank + r);
+                v.x = v.x + u.x;
+                v.y = v.y + u.y;
+                v.z = v.z + u.z;
+                v.w = v.w + u.w;
+            }
+        }
+        *reinterpret_cast<float4*>(ts + row * lo.rank + r) = v;
+    }
+    __syncthreads();
+}
+
+// Eight fp32 values as bf16 high parts and the bf16 roundings of what is left
+// (v = hi + lo to about 2^-16 relative).
+__device__ __forceinline__ void split_bf16x8(const float4 a, const float4 b, bf16x8& hi, bf16x8& lo) {
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const __bf16 h = (__bf16)v[e];
+        hi[e] = h;
+        lo[e] = (__bf16)(v[e] - (float)h);
+    }
+}
+
+// The LoRA delta of a wave's output tiles and the combined store, in lora_up's
+// rounding steps (q4_lora.hip): d[m, n] = sum_r t[m, r] B[n, r] on the bf16 matrix
+// cores, t and B each split into bf16 high and low parts, d = th.bh + th.bl + tl.bh
+// (three 16x16x32 MFMAs per tile cover every rank up to 32; the dropped tl.bl term and
+// the parts' roundings leave d within about 2^-16 of the fp32 sum, far below the bf16
+// rounding of the delta that follows); then y = bf16(bf16(acc) + bf16(d * bf16(scale)))
+// in bf16, acc + d * scale in fp32.  Lane (row or column, kq) holds ranks 8kq..8kq+7;
+// columns past the output and ranks past the adapter's read zeros.
+template <bool F32, int kMT, int kNT>
+__device__ __forceinline__ void lora_store(const f32x4 (&acc)[kMT][kNT], const LoraEpilogue& lo, const float* ts,
+                                           void* y, int row0, int rb0, int m_rows, int n_rows, int lane) {
+#pragma clang fp contract(off)
+    const int col = lane & 15, kq = lane >> 4;
+    const int r0 = 8 * kq;
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    bf16x8 bh[kNT], bl[kNT];
+#pragma unroll
+    for (int j = 0; j < kNT; ++j) {
+        const int n = (rb0 + j) * 16 + col;
+        const bool ok = n < n_rows;
+        const float* bp = lo.b + (long)(ok ? n : 0) * lo.rank + r0;
+        const float4 b0 = ok && r0 < lo.rank ? *reinterpret_cast<const float4*>(bp) : zero4;
+        const float4 b1 = ok && r0 + 4 < lo.rank ? *reinterpret_cast<const float4*>(bp + 4) : zero4;
+        split_bf16x8(b0, b1, bh[j], bl[j]);
+    }
+    const float sc = F32 ? lo.scale : (float)(__bf16)lo.scale;
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) {
+        const float* tp = ts + (16 * i + col) * lo.rank + r0;
+        const float4 t0 = r0 < lo.rank ? *reinterpret_cast<const float4*>(tp) : zero4;
+        const float4 t1 = r0 + 4 < lo.rank ? *reinterpret_cast<const float4*>(tp + 4) : zero4;
+        bf16x8 th, tl;
+        split_bf16x8(t0, t1, th, tl);
+#pragma unroll
+        for (int j = 0; j < kNT; ++j) {
+            f32x4 d = mfma16x16x32(th, bh[j], zero);
+            d = mfma16x16x32(th, bl[j], d);
+            d = mfma16x16x32(tl, bh[j], d);
+            const int n = (rb0 + j) * 16 + col;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int mr = row0 + 16 * i + 4 * kq + e;
+                if (mr < m_rows && n < n_rows) {
+                    const long o = (long)mr * n_rows + n;
+                    if constexpr (F32) {
+                        const float delta = d[e] * lo.scale;
+                        static_cast<float*>(y)[o] = acc[i][j][e] + delta;
+                    } else {
+                        const float base = (float)(__bf16)acc[i][j][e];
+                        const float delta = (float)(__bf16)(d[e] * sc);
+                        static_cast<uint16_t*>(y)[o] = f32_to_bf16(base + delta);
+                    }
+                }
+            }
+        }
+    }
+}
+
 // LDS rings (declared per instantiation inside the kernel, sized by its tile).
 // x: three slots of one group each (group g in slot g % 3; the loads for g+2 are in
 // flight while g is multiplied).  Weights: two slots of one group pair each (pair p
@@ -148,7 +245,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
                                                    void* __restrict__ y, int m_rows, int n_rows, int kx, int groups,
                                                    int gpairs, int mtiles, int ntiles, int octets, uint32_t rec_bytes,
                                                    int g_split, long split_stride, int n_out,
-                                                   const uint16_t* __restrict__ gelu_table) {
+                                                   const uint16_t* __restrict__ gelu_table, LoraEpilogue lora) {
     // BN / 32 waves of BM x 32: BM = 256; BM = 128 (more workgroups for small M
     // without splitting K); BM = 64 (fewest K splits for narrow outputs)
     static_assert(BM == 256 || BM == 128 || BM == 64, "tile rows");
@@ -493,6 +590,16 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     // its own stays live across the main loop (some 200 VGPRs in the 256-row tile).
     const int slane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
 
+    if constexpr (OUT == kOutLoraBf16 || OUT == kOutLoraF32) {
+        // t of the tile's rows into the x ring's first slot, free now
+        float* ts = reinterpret_cast<float*>(g_xs0);
+        wait_lds();  // this wave's operand reads have returned
+        lds_barrier();
+        lora_stage_t<BM>(lora, ts, mt * BM, m_rows, 64 * kWaves);
+        lora_store<OUT == kOutLoraF32>(acc, lora, ts, y, mt * BM, rbw + wave * kNT, m_rows, n_rows, slane);
+        return;
+    }
+
     // bf16 GeGLU: the gelu table (5.5 KiB) into the x ring's first slot, free now
     const uint16_t* gtab = reinterpret_cast<const uint16_t*>(g_xs0);
     if constexpr (OUT == kOutGegluBf16) {
@@ -717,11 +824,19 @@ hipError_t launch_gelu_table(uint16_t* table, hipStream_t stream) {
     return hipGetLastError();
 }
 
+bool gemm_lora_epilogue(int m, const Layout& l, int rank, size_t workspace_bytes) {
+    return rank >= 4 && rank <= 32 && rank % 4 == 0 && plan_gemm(m, l, workspace_bytes).splits == 1;
+}
+
 hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, int out_mode,
                        int n_out, const Layout& l, void* workspace, size_t workspace_bytes,
-                       const uint16_t* gelu_table, hipStream_t stream) {
+                       const uint16_t* gelu_table, hipStream_t stream, const LoraEpilogue* lora) {
     const GemmPlan plan = plan_gemm(m, l, workspace_bytes);
     if (plan.xaug_bytes + plan.part_bytes > workspace_bytes) return hipErrorInvalidValue;
+    const LoraEpilogue lo = lora != nullptr ? *lora : LoraEpilogue{nullptr, nullptr, 0, 0, 0.0f};
+    if (lora != nullptr && (plan.splits != 1 || out_mode > kOutF32 || lo.rank % 4 != 0 || lo.rank < 4 ||
+                            lo.rank > 32 || lo.slices < 1 || lo.part == nullptr || lo.b == nullptr))
+        return hipErrorInvalidValue;
     const int octets = (l.g + 7) / 8;
     const int mtiles = (m + plan.bm - 1) / plan.bm;
     const int ntiles = (l.n + plan.bn - 1) / plan.bn;
@@ -744,15 +859,15 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
         if (plan.bm == 64)                                                                                       \
             hipLaunchKernelGGL((gemm_kernel<MODE, 64, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,   \
                                l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split, STRIDE, n_out, \
-                               gelu_table);                                                                      \
+                               gelu_table, lo);                                                                  \
         else if (plan.bm == 256)                                                                                 \
             hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,  \
                                l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split, STRIDE, n_out, \
-                               gelu_table);                                                                      \
+                               gelu_table, lo);                                                                  \
         else                                                                                                     \
             hipLaunchKernelGGL((gemm_kernel<MODE, 128, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,  \
                                l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split, STRIDE, n_out, \
-                               gelu_table);                                                                      \
+                               gelu_table, lo);                                                                  \
     } while (0)
     if (plan.splits > 1) {
         Q4_GEMM_LAUNCH(kOutF32, (void*)part, elems);
@@ -776,6 +891,13 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
         else
             hipLaunchKernelGGL((split_reduce_kernel<false>), dim3(rgrid), dim3(rblock), 0, stream, part, y, elems,
                                plan.splits);
+        return hipGetLastError();
+    }
+    if (lora != nullptr) {
+        if (out_mode == kOutF32)
+            Q4_GEMM_LAUNCH(kOutLoraF32, y, 0L);
+        else
+            Q4_GEMM_LAUNCH(kOutLoraBf16, y, 0L);
         return hipGetLastError();
     }
     switch (out_mode) {

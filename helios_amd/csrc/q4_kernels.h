@@ -136,7 +136,10 @@ int device_cus();
 // LDS by the bf16 GeGLU epilogue (out_mode 2); may be null for the other modes.
 hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, void* y, int m, int out_mode,
                        int n_out, const Layout& l, void* workspace, size_t workspace_bytes,
-                       const uint16_t* gelu_table, hipStream_t stream);
+                       const uint16_t* gelu_table, hipStream_t stream, const LoraEpilogue* lora = nullptr);
+// Whether launch_gemm can add a LoRA delta of this rank in its epilogue for m rows
+// within `workspace_bytes` (an unsplit plan; rank a multiple of 4 up to 32).
+bool gemm_lora_epilogue(int m, const Layout& l, int rank, size_t workspace_bytes);
 
 // Fills table[kGeluTable] with gelu of the bf16 patterns that need a table, in the
 // bf16 op sequence.
@@ -152,6 +155,10 @@ int lora_slices(int k, int m);
 bool lora_fused(int m, int rank);
 hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float* part, void* y, int m, int n, int k,
                        int rank, float scale, bool out_f32, hipStream_t stream);
+// Only the first step, part[slice][m][r] = x . A^T over lora_slices(k, m) slices of K
+// (for a GEMM whose epilogue adds the delta).
+hipError_t launch_lora_down(const uint16_t* x, const float* a, float* part, int m, int k, int rank,
+                            hipStream_t stream);
 
 // Forward path choice (automatic mode): the decode kernels below kGemmMinRows rows,
 // and beyond that while 16-row slabs x N x K stays at most kDecodeMaxSlabWork (K' = 2K

@@ -347,6 +347,16 @@ int lora_slices(int k, int m) {
 
 bool lora_fused(int m, int rank) { return m <= kFusedRows && rank <= kFusedMaxRank; }
 
+hipError_t launch_lora_down(const uint16_t* x, const float* a, float* part, int m, int k, int rank,
+                            hipStream_t stream) {
+    const int slices = lora_slices(k, m);
+    const int slice_chunks = (k / 8 + slices - 1) / slices;
+    const dim3 dgrid((unsigned)((m + kDownRows - 1) / kDownRows), (unsigned)((rank + kRankBlock - 1) / kRankBlock),
+                     (unsigned)slices);
+    hipLaunchKernelGGL(lora_down_kernel, dgrid, dim3(256), 0, stream, x, a, part, m, rank, k, slice_chunks);
+    return hipGetLastError();
+}
+
 hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float* part, void* y, int m, int n, int k,
                        int rank, float scale, bool out_f32, hipStream_t stream) {
     static_assert(kWaveRanks * 4 == kRankBlock, "four waves per lora_down workgroup");

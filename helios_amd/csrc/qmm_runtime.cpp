@@ -463,8 +463,12 @@ Gemma4Status create_from_device(const Gemma4QLinearDesc* desc, const Triple& mai
 }
 
 // Launches one forward (checked arguments, device current) with its scratch from sc.
+// With an adapter (`lora`) whose delta the GEMM's epilogue can add (an unsplit plan,
+// rank a multiple of 4 up to 32), x . A^T is launched first and the GEMM adds the delta
+// (*lora_done set); otherwise the caller adds it after.
 Gemma4Status dispatch_forward(const Gemma4QLinear* linear, const uint16_t* x_dev, uint32_t rows, void* y_dev,
-                              Gemma4QmmDtype y_dtype, bool geglu, Scratch& sc, const std::string& name) {
+                              Gemma4QmmDtype y_dtype, bool geglu, Scratch& sc, const std::string& name,
+                              const Gemma4QLora* lora = nullptr, bool* lora_done = nullptr) {
     const bool f32 = y_dtype == GEMMA4_QMM_F32;
     const int mode = geglu ? (f32 ? q4::kOutGegluF32 : q4::kOutGegluBf16) : (f32 ? q4::kOutF32 : q4::kOutBf16);
     const int n_out = linear->pair_rows;
@@ -495,15 +499,31 @@ Gemma4Status dispatch_forward(const Gemma4QLinear* linear, const uint16_t* x_dev
     if (sc.fixed) ws = sc.base + sc.used;
     if (e != hipSuccess)
         return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
+    q4::LoraEpilogue lo{};
+    const bool with_lora = lora != nullptr && !geglu && !sc.fixed &&
+                           q4::gemm_lora_epilogue((int)rows, linear->layout, (int)lora->rank, ws_bytes);
+    if (with_lora) {
+        const int slices = q4::lora_slices((int)linear->desc.in_features, (int)rows);
+        void* part = nullptr;
+        e = sc.take((size_t)slices * rows * lora->rank * 4, &part);
+        if (e != hipSuccess)
+            return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
+        e = q4::launch_lora_down(x_dev, lora->a, static_cast<float*>(part), (int)rows, (int)linear->desc.in_features,
+                                 (int)lora->rank, sc.stream);
+        if (e != hipSuccess) return hip_fail((name + ": lora_down launch").c_str(), e);
+        lo = q4::LoraEpilogue{static_cast<const float*>(part), lora->b, (int)lora->rank, slices, lora->scale};
+    }
     e = q4::launch_gemm(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, mode, n_out, linear->layout, ws, ws_bytes,
-                        linear->gelu_table, sc.stream);
+                        linear->gelu_table, sc.stream, with_lora ? &lo : nullptr);
     if (e != hipSuccess) return hip_fail((name + ": gemm launch").c_str(), e);
+    if (lora_done != nullptr) *lora_done = with_lora;
     return GEMMA4_OK;
 }
 
 // Checks and dispatch shared by the plain, the GeGLU and the allocation-free forward.
 Gemma4Status run_forward(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev, uint32_t rows,
-                         void* y_dev, Gemma4QmmDtype y_dtype, bool geglu, bool no_alloc, const char* fn) {
+                         void* y_dev, Gemma4QmmDtype y_dtype, bool geglu, bool no_alloc, const char* fn,
+                         const Gemma4QLora* lora = nullptr, bool* lora_done = nullptr) {
     const std::string name(fn);
     if (!valid_handle(linear)) return fail(GEMMA4_ERR_INVALID_ARGUMENT, name + " received an invalid handle");
     if (geglu && linear->pair_rows == 0)
@@ -535,7 +555,7 @@ Gemma4Status run_forward(const Gemma4QLinear* linear, void* stream, const uint16
         sc.fixed = true;
         sc.cap = kStaticScratchBytes;
     }
-    const Gemma4Status st = dispatch_forward(linear, x_dev, rows, y_dev, y_dtype, geglu, sc, name);
+    const Gemma4Status st = dispatch_forward(linear, x_dev, rows, y_dev, y_dtype, geglu, sc, name, lora, lora_done);
     const hipError_t er = sc.release();
     if (st != GEMMA4_OK) return st;
     if (er != hipSuccess) return hip_fail((name + ": workspace release").c_str(), er);
@@ -928,8 +948,12 @@ Gemma4Status gemma4_qlinear_forward_lora(const Gemma4QLinear* linear, const Gemm
             if (valid_handle(linear) && lora->device != linear->device)
                 return fail(GEMMA4_ERR_ADAPTER, name + ": adapter and projection are on different devices");
         }
-        Gemma4Status st = run_forward(linear, stream, x_dev, rows, y_dev, y_dtype, false, false, name.c_str());
-        if (st != GEMMA4_OK || lora == nullptr || rows == 0) return st;
+        // the GEMM adds the delta in its epilogue where it can (unsplit plans, rank a
+        // multiple of 4 up to 32); otherwise the LoRA kernels add it after the forward
+        bool done = false;
+        Gemma4Status st = run_forward(linear, stream, x_dev, rows, y_dev, y_dtype, false, false, name.c_str(), lora,
+                                      &done);
+        if (st != GEMMA4_OK || lora == nullptr || rows == 0 || done) return st;
         DeviceGuard guard;
         hipError_t e = guard.enter(linear->device);
         if (e != hipSuccess) return hip_fail((name + ": hipSetDevice").c_str(), e);

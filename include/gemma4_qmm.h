@@ -239,9 +239,12 @@ Gemma4Status gemma4_qlora_free(Gemma4QLora* lora);
 
 /* gemma4_qlinear_forward plus the adapter's delta; lora NULL is the plain forward.
  * The adapter must match the projection's K and N and live on its device.  Up to 4
- * rows with rank up to 64: one fused launch and no scratch; otherwise a stream-ordered
- * scratch of at most 8 * rows * rank * 4 bytes (x . A^T summed over up to eight
- * slices of K). */
+ * rows with rank up to 64: one fused launch and no scratch; otherwise scratch of at
+ * most 8 * rows * rank * 4 bytes (x . A^T summed over up to eight slices of K).  Where
+ * the forward runs on an unsplit GEMM plan and the rank is a multiple of 4 up to 32,
+ * x . A^T is formed first and the GEMM's epilogue adds the delta (t . B^T on the bf16
+ * matrix cores from high and low bf16 parts of t and B, within about 2^-16 of the fp32
+ * sum, then the same roundings); otherwise the delta is added after the forward. */
 Gemma4Status gemma4_qlinear_forward_lora(const Gemma4QLinear* linear, const Gemma4QLora* lora, void* stream,
                                          const uint16_t* x_dev, uint32_t rows, void* y_dev, Gemma4QmmDtype y_dtype);
 

@@ -43,7 +43,9 @@ def gemm_asm():
 
 def test_lds_dma_sgpr_hazards_covered(gemm_asm):
     kernels = list(_kernels(gemm_asm))
-    assert len(kernels) == 12  # bf16 / fp32 outputs, bf16 / fp32 GeGLU pairs; 256, 128 and 64 x 256 tiles
+    # bf16 / fp32 outputs, bf16 / fp32 GeGLU pairs, bf16 / fp32 outputs with a LoRA
+    # delta; 256, 128 and 64 x 256 tiles
+    assert len(kernels) == 18
     for name, lines in kernels:
         dmas = 0
         for i, line in enumerate(lines):
@@ -79,7 +81,7 @@ def test_no_spills_and_lds_budget(gemm_asm):
         if "gemm_kernelILi" in m.group(2) and "ELi64ELi256E" in m.group(2):
             small += 1
             assert int(m.group(1)) <= 80 * 1024 and int(m.group(3)) <= 128, m.group(2)
-    assert small == 4
+    assert small == 6
 
 
 def _kernel_meta(asm: str):

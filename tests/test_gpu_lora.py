@@ -94,3 +94,42 @@ def test_lora_adapter_directory(gpu_lib, tmp_path):
         L.load_lora_adapter(str(ad), r + 1, 8.0, ["q_proj"], ck, cfg)
     lin.close()
     mods[prefix].close()
+
+
+# Prefill shapes whose GEMM plan is unsplit (gate at 2048 rows on 256-row tiles, k at
+# 2048 and the full-attention q at 512 on 64-row tiles): the GEMM's epilogue adds the
+# delta (t staged in LDS, fp32 matrix cores for t . B^T, then lora_up's rounding
+# steps).  Ranks that are multiples of 4 up to 32 take it; 48 and 64 (past 32) and 6
+# (not a multiple of 4) the LoRA kernels after the forward.  Sampled rows against the
+# oracle, same bars.
+@pytest.mark.parametrize("n,k,m,r,bits", [(15360, 3840, 2048, 16, 4), (2048, 3840, 2048, 4, 4),
+                                          (8192, 3840, 512, 32, 4), (8192, 3840, 512, 12, 4),
+                                          (2048, 3840, 2048, 28, 8), (2048, 3840, 2048, 48, 4),
+                                          (8192, 3840, 512, 64, 4), (2048, 3840, 2048, 6, 4)])
+@pytest.mark.parametrize("f32", [False, True])
+def test_lora_prefill_epilogue(gpu_lib, n, k, m, r, bits, f32):
+    import torch
+
+    rng = np.random.default_rng(n + k + m + r)
+    w = A.round_to_bf16((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    tri = C.quantize(w, bits=bits)
+    a = (rng.standard_normal((r, k)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal((n, r)) * 0.02).astype(np.float32)
+    x = A.make_activations(m, k, seed=m + r, outliers=True)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*tri), bits=bits)
+    lora = gpu_lib.LoraAdapter(a, b, 2.0)
+    dt = torch.float32 if f32 else torch.bfloat16
+    y = lin.forward_lora(dev_x(x), lora, out_dtype=dt)
+    torch.cuda.synchronize()
+    rows = np.unique(np.linspace(0, m - 1, 8).astype(np.int64))
+    xs = np.ascontiguousarray(x[rows])
+    base = C.qmm_f64(xs, *tri, bits=bits).astype(np.float32)
+    want = A.lora_ops(xs, a, b, 2.0, base, bf16=not f32).astype(np.float64)
+    got = host_bits(y[torch.from_numpy(rows).cuda()])
+    if f32:
+        ok, worst = A.check_f32_output(got, want, F32_REL)
+    else:
+        ok, worst = check_bf16_two_roundings(got, want)
+    assert ok, f"LoRA N={n} K={k} M={m} r={r} bits={bits}: worst error / RMS = {worst:.3e}"
+    lin.close()
+    lora.close()

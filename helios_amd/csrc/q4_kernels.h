@@ -153,12 +153,15 @@ constexpr int kLoraSlices = 8;
 int lora_slices(int k, int m);
 // Small M and rank: one fused launch that needs no part scratch (part may be null).
 bool lora_fused(int m, int rank);
-hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float* part, void* y, int m, int n, int k,
-                       int rank, float scale, bool out_f32, hipStream_t stream);
+// a_hi, a_lo: A as bf16 high and low parts [ceil(rank / 16) * 16][k] (rows past rank
+// zero), for the matrix-core x . A^T.
+hipError_t launch_lora(const uint16_t* x, const float* a, const uint16_t* a_hi, const uint16_t* a_lo, const float* b,
+                       float* part, void* y, int m, int n, int k, int rank, float scale, bool out_f32,
+                       hipStream_t stream);
 // Only the first step, part[slice][m][r] = x . A^T over lora_slices(k, m) slices of K
 // (for a GEMM whose epilogue adds the delta).
-hipError_t launch_lora_down(const uint16_t* x, const float* a, float* part, int m, int k, int rank,
-                            hipStream_t stream);
+hipError_t launch_lora_down(const uint16_t* x, const uint16_t* a_hi, const uint16_t* a_lo, float* part, int m,
+                            int k, int rank, hipStream_t stream);
 
 // Forward path choice (automatic mode): the decode kernels below kGemmMinRows rows,
 // and beyond that while 16-row slabs x N x K stays at most kDecodeMaxSlabWork (K' = 2K

@@ -3,17 +3,15 @@
 // A [rank, K] and B [N, rank] are fp32 (the adapter's tensors cast to float32,
 // native_model.cc:3420-3426).  Two passes after the base qmm, which has already
 // written base (bf16 in the bf16 model dtype, else fp32) into y:
-//   lora_down: t[m, r] = sum_k x[m, k] A[r, k]     (fp32)
+//   lora_down: t[m, r] = sum_k x[m, k] A[r, k]     (fp32 accumulation)
 //   lora_up:   y[m, n] = y[m, n] + delta,  delta = (sum_r t[m, r] B[n, r]) * scale
 // In bf16 the scale is bf16 (model_scalar) and delta is rounded to bf16 before the
 // bf16 add, as the reference's array ops round.
 //
-// lora_down: K is cut into lora_slices(k, m) slices (up to 8; fewer when the rows
-// alone give enough workgroups); a 256-thread workgroup per (4 rows of x, 16 ranks,
-// slice) has wave w take ranks 4w..4w+3 and lane l an 8-column chunk of the slice per
-// step (one 16-byte x load per row, two 16-byte A loads per rank, all in flight
-// together), then each wave sums its 4 x 4 partials by shuffles and writes them to
-// part[slice][m][r].  No atomics: lora_up adds the slices in a fixed order.
+// lora_down: on the matrix cores from A's bf16 high and low parts (below); K is cut
+// into lora_slices(k, m) slices (up to 8) until the workgroups fill the CUs, each
+// writing its partial sums to part[slice][m][r].  No atomics: lora_up (or the GEMM's
+// LoRA epilogue) adds the slices in a fixed order.
 // lora_up: a 256-thread workgroup per (256 columns, 16 or 32 rows); t[m, r] (the
 // slices summed in order, all of them requested at once) and the workgroup's rows of
 // B are staged in LDS 16 ranks at a time (B with coalesced loads), and each thread
@@ -28,68 +26,63 @@
 namespace q4 {
 namespace {
 
-constexpr int kDownRows = 4;    // rows of x per lora_down workgroup
-constexpr int kWaveRanks = 4;   // ranks per lora_down wave
-constexpr int kRankBlock = 16;  // ranks per lora_down workgroup / per lora_up register block
+constexpr int kDownWaves = 4;   // waves per lora_down workgroup (16 rows x 16 ranks x one slice of K)
+constexpr int kRankBlock = 16;  // ranks per lora_up register block
 constexpr int kUpRows = 16;     // rows of y per lora_up workgroup (M <= 16)
 constexpr int kUpRowsLarge = 32;  // rows of y per lora_up workgroup (M > 16)
 constexpr int kFusedRows = 4;      // M up to this with rank up to kFusedMaxRank: one fused launch
 constexpr int kFusedMaxRank = 64;
 
-__global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restrict__ x, const float* __restrict__ a,
-                                                        float* __restrict__ part, int m_rows, int rank, int k,
-                                                        int slice_chunks) {
-    const int m0 = (int)blockIdx.x * kDownRows;
+// lora_down on the matrix cores: A is held as bf16 high and low parts [rank_pad][K]
+// (A = Ah + Al to about 2^-17 relative, split once when the adapter is created), x is
+// bf16, so t = x . Ah^T + x . Al^T is two 16x16x32 MFMAs per 32 columns of K with exact
+// products and fp32 accumulation: within about 2^-17 of the fp32 product.  A 4-wave
+// workgroup per (16 rows of x, 16 ranks, slice of K): the waves split the slice's
+// 32-column steps, then their sums are added in wave order and written to
+// part[slice][m][r].  Each lane reads 16 contiguous bytes of x (row l%16) and of Ah and
+// Al (rank l%16) per step, so x is read once per 16 ranks.
+__global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ ah,
+                                                        const uint16_t* __restrict__ al, float* __restrict__ part,
+                                                        int m_rows, int rank, int k, int slice_steps) {
     const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-    const int r0 = (int)blockIdx.y * kRankBlock + wave * kWaveRanks;
-    const int slice = (int)blockIdx.z;
-    const int chunks = k >> 3;  // 8-column chunks (K is a multiple of 64)
-    const int c_end = (slice + 1) * slice_chunks < chunks ? (slice + 1) * slice_chunks : chunks;
-    float acc[kDownRows][kWaveRanks];
+    const int col = lane & 15, kq = lane >> 4;
+    const int steps = k >> 5;
+    const int s0 = (int)blockIdx.z * slice_steps;
+    const int left = steps - s0;
+    const int n_s = left < 0 ? 0 : left < slice_steps ? left : slice_steps;
+    const int w0 = s0 + wave * n_s / kDownWaves, w1 = s0 + (wave + 1) * n_s / kDownWaves;
+    const int m = (int)blockIdx.x * 16 + col;
+    const int r = (int)blockIdx.y * 16 + col;  // rows of Ah / Al past rank are zero
+    const uint16_t* xp = x + (long)(m < m_rows ? m : m_rows - 1) * k + 8 * kq;  // rows past M: never stored
+    const uint16_t* hp = ah + (long)r * k + 8 * kq;
+    const uint16_t* lp = al + (long)r * k + 8 * kq;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int st = w0; st < w1; ++st) {
+        const bf16x8 xa = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xp + 32 * st));
+        const bf16x8 bh = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(hp + 32 * st));
+        const bf16x8 bl = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(lp + 32 * st));
+        acc = mfma16x16x32(xa, bh, acc);
+        acc = mfma16x16x32(xa, bl, acc);
+    }
+    __shared__ f32x4 red[kDownWaves][64];
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    f32x4 v = red[0][lane];
 #pragma unroll
-    for (int i = 0; i < kDownRows; ++i)
-#pragma unroll
-        for (int r = 0; r < kWaveRanks; ++r) acc[i][r] = 0.f;
-    for (int c = slice * slice_chunks + lane; c < c_end; c += 64) {
-        uint4 xu[kDownRows];
-        float4 av[kWaveRanks][2];
-#pragma unroll
-        for (int i = 0; i < kDownRows; ++i) {
-            const int m = m0 + i < m_rows ? m0 + i : m_rows - 1;  // rows past M: any row, never stored
-            xu[i] = *reinterpret_cast<const uint4*>(x + (long)m * k + 8 * c);
-        }
-#pragma unroll
-        for (int r = 0; r < kWaveRanks; ++r) {
-            const int rr = r0 + r < rank ? r0 + r : rank - 1;  // ranks past the adapter's: never stored
-            const float4* ap = reinterpret_cast<const float4*>(a + (long)rr * k + 8 * c);
-            av[r][0] = ap[0];
-            av[r][1] = ap[1];
-        }
-#pragma unroll
-        for (int i = 0; i < kDownRows; ++i) {
-            const uint32_t w[4] = {xu[i].x, xu[i].y, xu[i].z, xu[i].w};
-#pragma unroll
-            for (int r = 0; r < kWaveRanks; ++r) {
-                const float av8[8] = {av[r][0].x, av[r][0].y, av[r][0].z, av[r][0].w,
-                                      av[r][1].x, av[r][1].y, av[r][1].z, av[r][1].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    acc[i][r] = __builtin_fmaf(bf16_lo(w[j]), av8[2 * j], acc[i][r]);
-                    acc[i][r] = __builtin_fmaf(bf16_hi(w[j]), av8[2 * j + 1], acc[i][r]);
-                }
-            }
-        }
+    for (int w = 1; w < kDownWaves; ++w) {
+        const f32x4 u = red[w][lane];
+        v[0] += u[0];
+        v[1] += u[1];
+        v[2] += u[2];
+        v[3] += u[3];
     }
 #pragma unroll
-    for (int i = 0; i < kDownRows; ++i)
-#pragma unroll
-        for (int r = 0; r < kWaveRanks; ++r) {
-            float v = acc[i][r];
-#pragma unroll
-            for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
-            if (lane == 0 && m0 + i < m_rows && r0 + r < rank)
-                part[((long)slice * m_rows + m0 + i) * rank + r0 + r] = v;
-        }
+    for (int e = 0; e < 4; ++e) {
+        const int row = (int)blockIdx.x * 16 + 4 * kq + e;
+        if (row < m_rows && r < rank) part[((long)blockIdx.z * m_rows + row) * rank + r] = v[e];
+    }
 }
 
 template <bool F32, int ROWS>
@@ -336,41 +329,37 @@ __global__ __launch_bounds__(1024) void lora_fused_kernel_f(const uint16_t* __re
 }  // namespace
 
 int lora_slices(int k, int m) {
-    const int chunks = k / 8;
-    int s = chunks >= kLoraSlices * 64 ? kLoraSlices : (chunks + 63) / 64;
-    // the rows alone give enough workgroups: fewer slices (fewer shuffle reductions and
-    // partial planes; M = 2048 at K = 3840 runs 2 slices of 1024 workgroups)
-    const int wgs = (m + kDownRows - 1) / kDownRows;
-    while (s > 1 && wgs * (s / 2) >= 1024) s /= 2;
+    // slices of K until the (16-row block, slice) workgroups fill the CUs, each wave
+    // keeping at least four 32-column steps
+    const int steps = k / 32;
+    const int wgs = (m + 15) / 16;
+    int s = 1;
+    while (s < kLoraSlices && wgs * s < 256 && steps / (2 * s * kDownWaves) >= 4) s *= 2;
     return s;
 }
 
 bool lora_fused(int m, int rank) { return m <= kFusedRows && rank <= kFusedMaxRank; }
 
-hipError_t launch_lora_down(const uint16_t* x, const float* a, float* part, int m, int k, int rank,
-                            hipStream_t stream) {
+hipError_t launch_lora_down(const uint16_t* x, const uint16_t* a_hi, const uint16_t* a_lo, float* part, int m,
+                            int k, int rank, hipStream_t stream) {
     const int slices = lora_slices(k, m);
-    const int slice_chunks = (k / 8 + slices - 1) / slices;
-    const dim3 dgrid((unsigned)((m + kDownRows - 1) / kDownRows), (unsigned)((rank + kRankBlock - 1) / kRankBlock),
-                     (unsigned)slices);
-    hipLaunchKernelGGL(lora_down_kernel, dgrid, dim3(256), 0, stream, x, a, part, m, rank, k, slice_chunks);
+    const int slice_steps = (k / 32 + slices - 1) / slices;
+    const dim3 dgrid((unsigned)((m + 15) / 16), (unsigned)((rank + 15) / 16), (unsigned)slices);
+    hipLaunchKernelGGL(lora_down_kernel, dgrid, dim3(64 * kDownWaves), 0, stream, x, a_hi, a_lo, part, m, rank, k,
+                       slice_steps);
     return hipGetLastError();
 }
 
-hipError_t launch_lora(const uint16_t* x, const float* a, const float* b, float* part, void* y, int m, int n, int k,
-                       int rank, float scale, bool out_f32, hipStream_t stream) {
-    static_assert(kWaveRanks * 4 == kRankBlock, "four waves per lora_down workgroup");
+hipError_t launch_lora(const uint16_t* x, const float* a, const uint16_t* a_hi, const uint16_t* a_lo, const float* b,
+                       float* part, void* y, int m, int n, int k, int rank, float scale, bool out_f32,
+                       hipStream_t stream) {
     if (lora_fused(m, rank)) {
         hipLaunchKernelGGL(lora_fused_kernel_f, dim3((unsigned)((n + 255) / 256)), dim3(1024), 0, stream, x, a, b, y, m,
                            n, k, rank, scale, out_f32 ? 1 : 0);
         return hipGetLastError();
     }
     const int slices = lora_slices(k, m);
-    const int slice_chunks = (k / 8 + slices - 1) / slices;
-    const dim3 dgrid((unsigned)((m + kDownRows - 1) / kDownRows), (unsigned)((rank + kRankBlock - 1) / kRankBlock),
-                     (unsigned)slices);
-    hipLaunchKernelGGL(lora_down_kernel, dgrid, dim3(256), 0, stream, x, a, part, m, rank, k, slice_chunks);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_lora_down(x, a_hi, a_lo, part, m, k, rank, stream);
     if (e != hipSuccess) return e;
     // 16 rows per workgroup for decode-sized M, 64 (B read a quarter as often) beyond
     const int rows = m <= kUpRows ? kUpRows : kUpRowsLarge;

@@ -274,6 +274,21 @@ struct Scratch {
     char* outgrown = nullptr;  // the stream's previous buffer, freed by release()
 };
 
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet), and back.
+uint16_t host_bf16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu) != 0) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+float host_f32(uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
 // Restores the caller's current device on scope exit.
 struct DeviceGuard {
     int saved = -1;
@@ -312,6 +327,8 @@ struct Gemma4QLora {
     int device = 0;
     float* a = nullptr;  // [rank, K] fp32
     float* b = nullptr;  // [N, rank] fp32
+    uint16_t* a_hi = nullptr;  // A as bf16 high and low parts [ceil(rank / 16) * 16, K], rows past rank zero
+    uint16_t* a_lo = nullptr;
 };
 
 namespace {
@@ -508,8 +525,8 @@ Gemma4Status dispatch_forward(const Gemma4QLinear* linear, const uint16_t* x_dev
         e = sc.take((size_t)slices * rows * lora->rank * 4, &part);
         if (e != hipSuccess)
             return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
-        e = q4::launch_lora_down(x_dev, lora->a, static_cast<float*>(part), (int)rows, (int)linear->desc.in_features,
-                                 (int)lora->rank, sc.stream);
+        e = q4::launch_lora_down(x_dev, lora->a_hi, lora->a_lo, static_cast<float*>(part), (int)rows,
+                                 (int)linear->desc.in_features, (int)lora->rank, sc.stream);
         if (e != hipSuccess) return hip_fail((name + ": lora_down launch").c_str(), e);
         lo = q4::LoraEpilogue{static_cast<const float*>(part), lora->b, (int)lora->rank, slices, lora->scale};
     }
@@ -900,13 +917,25 @@ Gemma4Status gemma4_qlora_create(const float* a, const float* b, uint32_t rank, 
         h->scale = scale;
         hipError_t e = hipGetDevice(&h->device);
         const size_t abytes = (size_t)rank * in_features * 4, bbytes = (size_t)out_features * rank * 4;
+        // A as bf16 high and low parts for the matrix-core x . A^T (rank padded to 16)
+        const size_t rpad = ((size_t)rank + 15) / 16 * 16;
+        std::vector<uint16_t> hi(rpad * in_features, 0), lo(rpad * in_features, 0);
+        for (size_t i = 0; i < (size_t)rank * in_features; ++i) {
+            hi[i] = host_bf16(a[i]);
+            lo[i] = host_bf16(a[i] - host_f32(hi[i]));
+        }
+        const size_t sbytes = rpad * in_features * 2;
         if (e == hipSuccess) e = hipMalloc(&h->a, abytes);
         if (e == hipSuccess) e = hipMalloc(&h->b, bbytes);
+        if (e == hipSuccess) e = hipMalloc(&h->a_hi, sbytes);
+        if (e == hipSuccess) e = hipMalloc(&h->a_lo, sbytes);
         if (e == hipSuccess) e = hipMemcpy(h->a, a, abytes, hipMemcpyHostToDevice);
         if (e == hipSuccess) e = hipMemcpy(h->b, b, bbytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(h->a_hi, hi.data(), sbytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(h->a_lo, lo.data(), sbytes, hipMemcpyHostToDevice);
         if (e != hipSuccess) {
-            if (h->a) (void)hipFree(h->a);
-            if (h->b) (void)hipFree(h->b);
+            for (void* p : {(void*)h->a, (void*)h->b, (void*)h->a_hi, (void*)h->a_lo})
+                if (p) (void)hipFree(p);
             delete h;
             return fail(GEMMA4_ERR_ADAPTER, name + ": device copy failed: " + hipGetErrorString(e));
         }
@@ -927,6 +956,8 @@ Gemma4Status gemma4_qlora_free(Gemma4QLora* lora) {
         (void)guard.enter(lora->device);
         (void)hipFree(lora->a);
         (void)hipFree(lora->b);
+        (void)hipFree(lora->a_hi);
+        (void)hipFree(lora->a_lo);
         lora->magic = 0;
         delete lora;
         return ok();
@@ -970,7 +1001,7 @@ Gemma4Status gemma4_qlinear_forward_lora(const Gemma4QLinear* linear, const Gemm
             if (e != hipSuccess)
                 return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
         }
-        e = q4::launch_lora(x_dev, lora->a, lora->b, static_cast<float*>(t), y_dev, (int)rows,
+        e = q4::launch_lora(x_dev, lora->a, lora->a_hi, lora->a_lo, lora->b, static_cast<float*>(t), y_dev, (int)rows,
                             (int)linear->desc.out_features, (int)linear->desc.in_features, (int)lora->rank, lora->scale,
                             y_dtype == GEMMA4_QMM_F32, sc.stream);
         const hipError_t ef = sc.release();

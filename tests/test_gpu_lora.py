@@ -1,6 +1,8 @@
 """GPU parity of LoRA on a quantized projection (gemma4_qlinear_forward_lora) against
 the oracle (lora_ops over the exact base product), plus loading an adapter directory
-against a checkpoint.  Bars: fp32 max |y - y_ref| <= 2e-3 * RMS; bf16 max |y - y_ref|
+against a checkpoint.  x . A^T runs on the matrix cores from A's bf16 high and low
+parts (within ~2^-17 of the fp32 product) except in the one-launch path for up to 4
+rows; t . B^T in the GEMM's epilogue likewise from bf16 parts (~2^-16).  Bars: fp32 max |y - y_ref| <= 2e-3 * RMS; bf16 max |y - y_ref|
 <= 1e-2 * RMS + two ulps of y_ref.  The bf16 bar allows two ulps (not the plain
 output's half): the base product is rounded to bf16 before the delta is added (the
 reference's order), so the fp32 accumulation can move that first rounding by an ulp,

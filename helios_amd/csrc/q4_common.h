@@ -115,6 +115,32 @@ __device__ __forceinline__ bf16x8 expand_word(uint32_t u) {
     return __builtin_bit_cast(bf16x8, d);
 }
 
+// The GEMM's fp16 form.  q - 8 lies in [-8, 7] and a bf16 scale has an 8-bit
+// significand, so s' (q - 8) has at most 11 significant bits (255 * 8 < 2^11): it is
+// exact in fp16 whenever s' lies in [2^-14, 2^13) or is zero.  Eight nibbles of one
+// tiled word -> the eight fp16 values s' (q - 8) in element order: the mask puts q in
+// mantissa bits 3..6 under the exponent of 128, giving 128 + q; minus 136 is q - 8
+// (exact), times s' (exact).
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+constexpr uint32_t kF16x2Of128 = 0x58005800u;
+__device__ __forceinline__ f16x8 expand_word_f16(uint32_t u, f16x2 s) {
+    const f16x2 off = {(_Float16)-136.0f, (_Float16)-136.0f};
+    f16x2 v[4];
+    v[0] = __builtin_bit_cast(f16x2, and_or(u, kNibMask, kF16x2Of128));
+    v[1] = __builtin_bit_cast(f16x2, and_or(rotr(u, 4), kNibMask, kF16x2Of128));
+    v[2] = __builtin_bit_cast(f16x2, and_or(rotr(u, 8), kNibMask, kF16x2Of128));
+    v[3] = __builtin_bit_cast(f16x2, and_or(rotr(u, 12), kNibMask, kF16x2Of128));
+    f16x8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const f16x2 w = (v[i] + off) * s;
+        r[2 * i] = w[0];
+        r[2 * i + 1] = w[1];
+    }
+    return r;
+}
+
 // q[2p] and q[2p+1] of a tiled word, for the dequantize kernel.
 __device__ __forceinline__ uint32_t word_nibble(uint32_t u, int i) {
     const uint32_t r = rotr(u, 4 * (i >> 1));
@@ -369,6 +395,9 @@ __device__ __forceinline__ int geglu2_col(int col, int rb) { return rb * 8 + (co
 
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------

@@ -16,6 +16,21 @@
 //   pre-pass's launch (gate 15360x3840 at 2048 rows 228.5 -> 232.4 us).
 // Every product is exact; rounding is fp32 accumulation only.
 //
+// The fp16 form (256-row tiles, when the handle's scales allow it): with
+// s' = s 2^p and x scaled per row to x16 = fp16(x 2^k) by a pre-pass (xprep_kernel),
+//   y 2^(k + p) = sum_k x16 * s'(q - 8) + sum_g X_g 2^p (b + 8 s),   X_g = sum of x16,
+// where s'(q - 8) is exact in fp16 (q4_common.h) and every product is again exact:
+// the matrix cores (v_mfma_f32_16x16x32_f16) accumulate straight into the outputs and
+// the per-group scale FMAs go away (two per MFMA; with the expansion's four extra ops
+// per word, 81 VALU ops per group step instead of ~240).  The bias term is the same
+// MFMA with A = [Xh, Xl, 8Xh, 8Xl] (X_g 2^p).  x16 is exact for every x within 2^32 of
+// its row's largest; smaller ones are rounded at 2^-39 of it.  The outputs are scaled
+// back by 2^-(k + p) before any store.  Measured on gate 15360x3840 at 2048 rows
+// (rocprof, steady clock): the GEMM kernel 210-215 us against 218-223 in the bf16
+// form, but the pre-pass, which now writes x16 (15.7 MB), 12 us against 5; so the plan
+// takes the form only where its cost model says the kernel's gain is larger (the
+// widest outputs: the gate|up pair, gate and up from ~1024 rows).
+//
 // Tiling: a 512-thread workgroup computes a 256 (M) x 256 (N) tile as eight waves
 // side by side along N, each all 256 rows x 32 columns (two waves per SIMD, so one's
 // MFMA and LDS latencies are covered by the other's work); or 128 x 256, or 64 x 256
@@ -45,8 +60,9 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // The bias MFMA's A operand for one 16-row tile and one octet, as 64 lanes of 16 B:
 // lane (m = l%16, kq = l/16), element e -> group 8*octet + 2*kq + e/4, term e%4 in
-// {Xh, Xl, -16 Xh, -16 Xl}.  Lane (m, kq) packs it from X of row m for groups 2kq and
-// 2kq + 1.
+// {Xh, Xl, c Xh, c Xl} (c = -16, or 8 in the fp16 form).  Lane (m, kq) packs it from X
+// of row m for groups 2kq and 2kq + 1.
+template <int C = -16>
 __device__ __forceinline__ uint4 bias_a_operand(float x0, float x1) {
     uint32_t w[4];
     const float xs[2] = {x0, x1};
@@ -54,8 +70,8 @@ __device__ __forceinline__ uint4 bias_a_operand(float x0, float x1) {
     for (int gi = 0; gi < 2; ++gi) {
         const uint16_t xh = f32_to_bf16(xs[gi]);
         const uint16_t xl = f32_to_bf16(xs[gi] - __uint_as_float((uint32_t)xh << 16));
-        const uint16_t nxh = f32_to_bf16(-16.0f * __uint_as_float((uint32_t)xh << 16));
-        const uint16_t nxl = f32_to_bf16(-16.0f * __uint_as_float((uint32_t)xl << 16));
+        const uint16_t nxh = f32_to_bf16((float)C * __uint_as_float((uint32_t)xh << 16));
+        const uint16_t nxl = f32_to_bf16((float)C * __uint_as_float((uint32_t)xl << 16));
         w[2 * gi] = (uint32_t)xh | ((uint32_t)xl << 16);
         w[2 * gi + 1] = (uint32_t)nxh | ((uint32_t)nxl << 16);
     }
@@ -104,6 +120,154 @@ __global__ __launch_bounds__(512) void xaug_kernel(const uint16_t* __restrict__ 
     if (t >= 64) return;
     const int kq = t >> 4;
     xaug[(long)unit * 64 + t] = bias_a_operand(gsum[2 * kq][t & 15], gsum[2 * kq + 1][t & 15]);
+}
+
+// ---------------------------------------------------------------------------
+// The fp16 form's pre-pass: one wave per row m of the tiles, four rows per workgroup
+// (rows past M write zero bias operands only):
+//  * k = 142 - e, e the largest biased exponent of the row's finite |x|, so that the
+//    largest |x| 2^k lies in [2^15, 2^16), with 8 significant bits below 65504 (k = 0
+//    for a row of zeros; inf and NaN stay inf and NaN and reach y so);
+//  * x16[m] = fp16(x 2^k), exact for every x within 2^32 of the largest;
+//  * X_g = the fp32 sum of the group's x16 values (in element order, then over the
+//    group's eight 16-byte units in a fixed tree), and the 256-row tile's bias A
+//    operands from X_g 2^p, in xaug_kernel's layout;
+//  * rowexp[m] = k + p: the GEMM's sums of row m are y 2^(k + p).
+// A lane keeps up to kPrepCache 16-byte units of its row between the two passes (rows
+// of up to 4096 values are read once); longer rows are read again from L2.
+// ---------------------------------------------------------------------------
+constexpr int kPrepRows = 4;    // rows (waves) per workgroup
+constexpr int kPrepCache = 8;
+
+// largest bf16 magnitude bits of eight values, inf and NaN left out
+__device__ __forceinline__ uint32_t finite_max_bits(uint4 v) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t mb = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = w[j] & 0x7FFFu, hi = (w[j] >> 16) & 0x7FFFu;
+        mb = (lo < 0x7F80u && lo > mb) ? lo : mb;
+        mb = (hi < 0x7F80u && hi > mb) ? hi : mb;
+    }
+    return mb;
+}
+
+__global__ __launch_bounds__(64 * kPrepRows) void xprep_kernel(const uint16_t* __restrict__ x,
+                                                               uint16_t* __restrict__ x16, uint4* __restrict__ xaug,
+                                                               int* __restrict__ rowexp, int m_rows, int kx, int groups,
+                                                               int octets, int p) {
+    extern __shared__ float gsum_all[];  // [kPrepRows][kx / 64]
+    const int wave = (int)(threadIdx.x >> 6);
+    const int lane = (int)(threadIdx.x & 63);
+    const int m = (int)blockIdx.x * kPrepRows + wave;
+    const int gx = kx >> 6;     // groups of a row of x (a two-plane handle's group g >= gx is g - gx)
+    const int units = kx >> 3;  // 16-byte units of the row (a multiple of 8)
+    float* const gsum = gsum_all + wave * gx;
+    if (m < m_rows) {
+        const uint4* xr = reinterpret_cast<const uint4*>(x + (long)m * kx);
+        uint4* yr = reinterpret_cast<uint4*>(x16 + (long)m * kx);
+        const uint4 zero = make_uint4(0, 0, 0, 0);
+        uint4 c[kPrepCache];
+#pragma unroll
+        for (int i = 0; i < kPrepCache; ++i) {
+            const int u = lane + 64 * i;
+            c[i] = u < units ? xr[u] : zero;
+        }
+        uint32_t mb = 0;
+#pragma unroll
+        for (int i = 0; i < kPrepCache; ++i) {
+            const uint32_t v = finite_max_bits(c[i]);
+            mb = v > mb ? v : mb;
+        }
+        for (int u = lane + 64 * kPrepCache; u < units; u += 64) {
+            const uint32_t v = finite_max_bits(xr[u]);
+            mb = v > mb ? v : mb;
+        }
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_xor((int)mb, d);
+            mb = o > mb ? o : mb;
+        }
+        const int e = (int)(mb >> 7);
+        const int k = e == 0 ? 0 : 142 - e;
+        // x16 of one 16-byte unit and its group's sum (the eight units of a group are
+        // eight consecutive lanes; every lane of the wave takes part in the shuffles)
+        auto conv = [&](uint4 v, int u) {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            uint32_t o[4];
+            float sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const _Float16 lo = (_Float16)__builtin_amdgcn_ldexpf(bf16_lo(w[j]), k);
+                const _Float16 hi = (_Float16)__builtin_amdgcn_ldexpf(bf16_hi(w[j]), k);
+                sum += (float)lo;
+                sum += (float)hi;
+                o[j] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+            }
+            sum += __shfl_xor(sum, 1);
+            sum += __shfl_xor(sum, 2);
+            sum += __shfl_xor(sum, 4);
+            if (u < units) {
+                yr[u] = make_uint4(o[0], o[1], o[2], o[3]);
+                if ((u & 7) == 0) gsum[u >> 3] = sum;
+            }
+        };
+#pragma unroll
+        for (int i = 0; i < kPrepCache; ++i)
+            if (64 * i < units) conv(c[i], lane + 64 * i);
+        for (int u0 = 64 * kPrepCache; u0 < units; u0 += 64) {
+            const int u = u0 + lane;
+            conv(u < units ? xr[u] : zero, u);
+        }
+        if (lane == 0) rowexp[m] = k + p;
+    }
+    __syncthreads();
+    // entry (octet o, kq) of row m: groups 8o + 2kq and 8o + 2kq + 1
+    const long m16 = m >> 4;
+    const int r = m & 15;
+    for (int i = lane; i < octets * 4; i += 64) {
+        const int o = i >> 2, kq = i & 3;
+        float xs[2];
+#pragma unroll
+        for (int gi = 0; gi < 2; ++gi) {
+            const int g = 8 * o + 2 * kq + gi;
+            xs[gi] = (m < m_rows && g < groups) ? __builtin_amdgcn_ldexpf(gsum[g >= gx ? g - gx : g], p) : 0.0f;
+        }
+        xaug[(m16 * octets + o) * 64 + kq * 16 + r] = bias_a_operand<8>(xs[0], xs[1]);
+    }
+}
+
+// Scale range of a handle: thread per (record, row), one atomic per wave.
+__global__ void scale_range_kernel(const uint2* __restrict__ sb, long records, int* __restrict__ out) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    int emax = 0, emin = 255, bad = 0;
+    if (i < records * 16) {
+        const uint2 w = sb[(i >> 4) * kRecU2 + (i & 15)];
+        const uint32_t mags[2] = {w.x & 0x7FFFu, w.y & 0x7FFFu};
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if (mags[j] == 0) continue;
+            const int e = (int)(mags[j] >> 7);
+            if (e == 255) {
+                ++bad;
+            } else {
+                emax = e > emax ? e : emax;
+                emin = e < emin ? e : emin;
+            }
+        }
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int a = __shfl_xor(emax, d), b = __shfl_xor(emin, d), c = __shfl_xor(bad, d);
+        emax = a > emax ? a : emax;
+        emin = b < emin ? b : emin;
+        bad += c;
+    }
+    if ((threadIdx.x & 63) == 0) {
+        atomicMax(&out[0], emax);
+        atomicMin(&out[1], emin);
+        if (bad) atomicAdd(&out[2], bad);
+    }
 }
 
 // B operand of the bias MFMA from one scale/bias word pair: [b0 b0 s0 s0 b1 b1 s1 s1]
@@ -239,17 +403,20 @@ __device__ __forceinline__ void lora_store(const f32x4 (&acc)[kMT][kNT], const L
 // (a shared array would make it wait for every DMA before every read); it tells apart
 // at most eight such objects.
 
-template <int OUT, int BM, int BN>
+template <int OUT, int BM, int BN, bool F16 = false>
 __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ tiles, const uint2* __restrict__ sb,
                                                    const uint16_t* __restrict__ x, const uint4* __restrict__ xaug,
                                                    void* __restrict__ y, int m_rows, int n_rows, int kx, int groups,
                                                    int gpairs, int mtiles, int ntiles, int octets, uint32_t rec_bytes,
                                                    int g_split, long split_stride, int n_out,
-                                                   const uint16_t* __restrict__ gelu_table, LoraEpilogue lora) {
+                                                   const uint16_t* __restrict__ gelu_table, LoraEpilogue lora,
+                                                   const int* __restrict__ rowexp, float s_pow) {
     // BN / 32 waves of BM x 32: BM = 256; BM = 128 (more workgroups for small M
-    // without splitting K); BM = 64 (fewest K splits for narrow outputs)
+    // without splitting K); BM = 64 (fewest K splits for narrow outputs).  F16: the fp16
+    // form (x is x16 then; rowexp and s_pow = 2^p from the pre-pass and the handle).
     static_assert(BM == 256 || BM == 128 || BM == 64, "tile rows");
     static_assert(BN == 256 || BN == 128, "tile columns");
+    static_assert(!F16 || BM == 256, "the fp16 form takes its group sums from the pre-pass");
     constexpr int kWaves = BN / kWN;              // side by side along N
     constexpr int kRB = BN / 16;                  // 16-row weight blocks per workgroup tile
     constexpr int kXChunks = BM * 8;              // 16-byte chunks of one x group tile (BM rows x 64 bf16)
@@ -419,6 +586,36 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
                 xsum[t] = mfma16x16x32(ones, b1, xsum[t]);
             }
         }
+        if constexpr (F16) {
+            // The fp16 form: each tile's two products accumulate straight into its
+            // outputs; row 0 expands each row block's words (s' (q - 8)) just before
+            // its first products, and the next row's A operands are read a row ahead.
+            f16x8 bq[kNT][2];
+            bf16x8 a0 = a_frag(0, 0), a1 = a_frag(0, 1), n0, n1;
+#pragma unroll
+            for (int t = 0; t < kMT * kNT; ++t) {
+                const int i = t / kNT, j = t % kNT;
+                if (i == 0) {
+                    const _Float16 sh = (_Float16)(bf16_lo(swv[j]) * s_pow);
+                    const f16x2 s2 = {sh, sh};
+                    bq[j][0] = expand_word_f16(tw[j].x, s2);
+                    bq[j][1] = expand_word_f16(tw[j].y, s2);
+                }
+                if (j == 0 && i + 1 < kMT) {
+                    n0 = a_frag(i + 1, 0);
+                    n1 = a_frag(i + 1, 1);
+                }
+                acc[i][j] = mfma16x16x32(__builtin_bit_cast(f16x8, a0), bq[j][0], acc[i][j]);
+                acc[i][j] = mfma16x16x32(__builtin_bit_cast(f16x8, a1), bq[j][1], acc[i][j]);
+                if (j == kNT - 1) {
+                    a0 = n0;
+                    a1 = n1;
+                }
+                hook(t);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            return;
+        }
         // The wave's 32 tiles in one stream, software-pipelined and kept in this order
         // (a scheduling fence after each tile): tile t's two products, then tile t-3's
         // scale FMAs, which do not wait for them; row 0 expands each row block's words
@@ -583,6 +780,27 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         wait_vm_lds<0>();
         lds_barrier();
         bias();
+    }
+    if constexpr (F16) {
+        // the fp16 form's sums are y 2^(k + p): rows 4kq + e of each row tile scaled back
+        // (exact: a power of two).  The row index is opaque here, so the exponent loads
+        // stay after the main loop (hoisted ahead of it, 64 values would stay live
+        // through it and spill).
+        int mrow = mt * BM + 4 * kq;
+        asm volatile("" : "+v"(mrow));
+#pragma unroll
+        for (int i = 0; i < kMT; ++i) {
+            const int m0 = mrow + 16 * i;
+            int re[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) re[e] = m0 + e < m_rows ? rowexp[m0 + e] : 0;
+#pragma unroll
+            for (int j = 0; j < kNT; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[i][j][e] = __builtin_amdgcn_ldexpf(acc[i][j][e], -re[e]);
+            // one row tile at a time (all 64 loads hoisted ahead would spill)
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 
     // store: lane holds rows 4*kq + e of column col of each 16x16 tile.  The GeGLU
@@ -777,7 +995,38 @@ constexpr double kRoundUs = 1.0;               // per round of workgroups: prolo
 constexpr double kSplitUs = 4.0;               // a split's reduction launch
 constexpr double kPartialBytesPerUs = 4.0e6;   // partial sums written and read back
 constexpr double kPrePassUs = 3.0;             // the 256-row tile's group-sum pre-pass
+// the fp16 form: its group step against the bf16 form's (gate 15360x3840 at 2048 rows,
+// the kernel alone, steady clock: 210-215 vs 218-223 us), and its pre-pass's extra
+// time per byte of x16 (12.3 us against the group-sum pre-pass's 5.0 for 15.7 MB)
+constexpr double kF16StepScale = 0.965;
+constexpr double kPrepBytesPerUs = 2.15e6;
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 }  // namespace
+
+void set_f16_form(Layout& l, const int range[3]) {
+    l.f16 = false;
+    l.f16_p = 0;
+    if (range[2] != 0 || l.kx / 64 > kPrepMaxGroups) return;
+    if (range[0] == 0) {  // every scale zero
+        l.f16 = true;
+        return;
+    }
+    // the largest scale times 2^p in [2^12, 2^13); the smallest nonzero then >= 2^-14
+    // when the exponents span at most 26
+    const int p = 12 - (range[0] - 127);
+    if (range[0] - range[1] > 26 || p > 64 || p < -64) return;
+    l.f16 = true;
+    l.f16_p = p;
+}
+
+hipError_t launch_scale_range(const uint2* sb, const Layout& l, int* out, hipStream_t stream) {
+    const long records = (long)l.nb * l.gp;
+    const long threads = records * 16;
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(scale_range_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, sb, records,
+                       out);
+    return hipGetLastError();
+}
 
 GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
     GemmPlan p;
@@ -788,36 +1037,46 @@ GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
         if (ts.max_m > 0 && m > ts.max_m) continue;
         const int bm = ts.bm, bn = ts.bn;
         const long tiles = (long)((m + bm - 1) / bm) * ((l.n + bn - 1) / bn);
-        for (int s = 1; s <= octets && s <= kMaxSplits; ++s) {
-            const int per = (octets + s - 1) / s;
-            const int used = (octets + per - 1) / per;  // splits that get work
-            if (used != s) continue;
-            const size_t part = s > 1 ? (size_t)s * m * l.n * 4 : 0;
-            if (part > kMaxPartialBytes) break;
-            // the 256-row tile's X_g pre-pass (bias A operands of every 16-row block and octet)
+        // the 256-row tile in the fp16 form (where the handle's scales allow it) and
+        // in the bf16 form
+        for (int form = (bm == 256 && l.f16) ? 1 : 0; form >= 0; --form) {
+            const bool f16 = form == 1;
+            // the 256-row tile's X_g pre-pass (bias A operands of every 16-row block and
+            // octet); the fp16 form's x16 and row exponents
             const size_t xa = bm == 256 ? ((size_t)m + bm - 1) / bm * (bm / 16) * octets * 1024 : 0;
-            if (xa + part > max_workspace) break;  // (more splits need more)
-            const double rounds = (double)((tiles * s + cus * ts.per_cu - 1) / (cus * ts.per_cu));
-            const double t = rounds * (per * 8 * ts.step_us + kRoundUs) +
-                             (s > 1 ? kSplitUs + part / kPartialBytesPerUs : 0.0) + (bm == 256 ? kPrePassUs : 0.0);
-            if (best < 0.0 || t < best) {
-                best = t;
-                p.bm = bm;
-                p.bn = bn;
-                p.splits = s;
-                p.g_split = per * 8;
-                p.part_bytes = part;
-                p.xaug_bytes = xa;
+            const size_t x16 = f16 ? round256((size_t)m * l.kx * 2) : 0;
+            const size_t rexp = f16 ? round256((size_t)m * 4) : 0;
+            for (int s = 1; s <= octets && s <= kMaxSplits; ++s) {
+                const int per = (octets + s - 1) / s;
+                const int used = (octets + per - 1) / per;  // splits that get work
+                if (used != s) continue;
+                const size_t part = s > 1 ? (size_t)s * m * l.n * 4 : 0;
+                if (part > kMaxPartialBytes) break;
+                if (xa + x16 + rexp + part > max_workspace) break;  // (more splits need more)
+                const double rounds = (double)((tiles * s + cus * ts.per_cu - 1) / (cus * ts.per_cu));
+                const double step = ts.step_us * (f16 ? kF16StepScale : 1.0);
+                const double t = rounds * (per * 8 * step + kRoundUs) +
+                                 (s > 1 ? kSplitUs + part / kPartialBytesPerUs : 0.0) +
+                                 (bm == 256 ? kPrePassUs + x16 / kPrepBytesPerUs : 0.0);
+                if (best < 0.0 || t < best) {
+                    best = t;
+                    p.bm = bm;
+                    p.bn = bn;
+                    p.splits = s;
+                    p.g_split = per * 8;
+                    p.part_bytes = part;
+                    p.xaug_bytes = xa;
+                    p.f16 = f16;
+                    p.x16_bytes = x16;
+                    p.rowexp_bytes = rexp;
+                }
             }
         }
     }
     return p;
 }
 
-size_t gemm_workspace_bytes(int m, const Layout& l) {
-    const GemmPlan p = plan_gemm(m, l);
-    return p.xaug_bytes + p.part_bytes;
-}
+size_t gemm_workspace_bytes(int m, const Layout& l) { return plan_gemm(m, l).total(); }
 
 hipError_t launch_gelu_table(uint16_t* table, hipStream_t stream) {
     hipLaunchKernelGGL(gelu_table_kernel, dim3((kGeluTable + 255) / 256), dim3(256), 0, stream, table);
@@ -832,7 +1091,7 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
                        int n_out, const Layout& l, void* workspace, size_t workspace_bytes,
                        const uint16_t* gelu_table, hipStream_t stream, const LoraEpilogue* lora) {
     const GemmPlan plan = plan_gemm(m, l, workspace_bytes);
-    if (plan.xaug_bytes + plan.part_bytes > workspace_bytes) return hipErrorInvalidValue;
+    if (plan.total() > workspace_bytes) return hipErrorInvalidValue;
     const LoraEpilogue lo = lora != nullptr ? *lora : LoraEpilogue{nullptr, nullptr, 0, 0, 0.0f};
     if (lora != nullptr && (plan.splits != 1 || out_mode > kOutF32 || lo.rank % 4 != 0 || lo.rank < 4 ||
                             lo.rank > 32 || lo.slices < 1 || lo.part == nullptr || lo.b == nullptr))
@@ -840,34 +1099,47 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     const int octets = (l.g + 7) / 8;
     const int mtiles = (m + plan.bm - 1) / plan.bm;
     const int ntiles = (l.n + plan.bn - 1) / plan.bn;
-    uint4* xaug = plan.xaug_bytes ? static_cast<uint4*>(workspace) : nullptr;
-    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.xaug_bytes);
+    // workspace: [group sums | x16 | row exponents | partial sums], each 256-byte aligned
+    char* const wsb = static_cast<char*>(workspace);
+    uint4* xaug = plan.xaug_bytes ? reinterpret_cast<uint4*>(wsb) : nullptr;
+    uint16_t* x16 = plan.f16 ? reinterpret_cast<uint16_t*>(wsb + plan.xaug_bytes) : nullptr;
+    int* rowexp = plan.f16 ? reinterpret_cast<int*>(wsb + plan.xaug_bytes + plan.x16_bytes) : nullptr;
+    float* part = reinterpret_cast<float*>(wsb + plan.xaug_bytes + plan.x16_bytes + plan.rowexp_bytes);
     if (l.rec_bytes() > kMaxBufferBytes || (size_t)m * l.kx * 2 > kMaxBufferBytes || plan.xaug_bytes > kMaxBufferBytes)
         return hipErrorInvalidValue;
-    if (plan.xaug_bytes) {
+    if (plan.f16) {
+        // one wave per row of the tiles
+        hipLaunchKernelGGL(xprep_kernel, dim3((unsigned)(mtiles * plan.bm / kPrepRows)), dim3(64 * kPrepRows),
+                           (size_t)kPrepRows * (l.kx / 64) * sizeof(float), stream, x, x16, xaug, rowexp, m, l.kx, l.g,
+                           octets, l.f16_p);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    } else if (plan.xaug_bytes) {
         const long units = (long)mtiles * (plan.bm / 16) * octets;  // 1 KiB blocks
         hipLaunchKernelGGL(xaug_kernel, dim3((unsigned)units), dim3(512), 0, stream, x, xaug, m, l.kx, l.g, octets);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
+    const uint16_t* const xin = plan.f16 ? x16 : x;
+    const float s_pow = plan.f16 ? __builtin_ldexpf(1.0f, l.f16_p) : 1.0f;
     const dim3 grid((unsigned)(mtiles * ntiles), (unsigned)plan.splits), block(2 * plan.bn);
     const uint32_t rec_bytes = (uint32_t)l.rec_bytes();
     const long elems = (long)m * l.n;
-    // one instantiation per (output mode, tile shape)
+    // one instantiation per (output mode, tile shape, form)
+#define Q4_GEMM_ARGS(YPTR, STRIDE)                                                                               \
+    tiles, sb, xin, xaug, YPTR, m, l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split, STRIDE, \
+        n_out, gelu_table, lo, rowexp, s_pow
 #define Q4_GEMM_LAUNCH(MODE, YPTR, STRIDE)                                                                       \
     do {                                                                                                         \
         if (plan.bm == 64)                                                                                       \
-            hipLaunchKernelGGL((gemm_kernel<MODE, 64, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,   \
-                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split, STRIDE, n_out, \
-                               gelu_table, lo);                                                                  \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 64, 256>), grid, block, 0, stream, Q4_GEMM_ARGS(YPTR, STRIDE));  \
+        else if (plan.bm == 256 && plan.f16)                                                                     \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256, true>), grid, block, 0, stream,                      \
+                               Q4_GEMM_ARGS(YPTR, STRIDE));                                                      \
         else if (plan.bm == 256)                                                                                 \
-            hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,  \
-                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split, STRIDE, n_out, \
-                               gelu_table, lo);                                                                  \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256>), grid, block, 0, stream, Q4_GEMM_ARGS(YPTR, STRIDE)); \
         else                                                                                                     \
-            hipLaunchKernelGGL((gemm_kernel<MODE, 128, 256>), grid, block, 0, stream, tiles, sb, x, xaug, YPTR, m,  \
-                               l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split, STRIDE, n_out, \
-                               gelu_table, lo);                                                                  \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 128, 256>), grid, block, 0, stream, Q4_GEMM_ARGS(YPTR, STRIDE)); \
     } while (0)
     if (plan.splits > 1) {
         Q4_GEMM_LAUNCH(kOutF32, (void*)part, elems);
@@ -907,6 +1179,7 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
         default: Q4_GEMM_LAUNCH(kOutBf16, y, 0L); break;
     }
 #undef Q4_GEMM_LAUNCH
+#undef Q4_GEMM_ARGS
     return hipGetLastError();
 }
 

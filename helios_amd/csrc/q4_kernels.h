@@ -33,6 +33,10 @@ struct Layout {
     int g = 0;   // groups per row (k / 64)
     int nb = 0;  // 16-row blocks
     int gp = 0;  // group pairs (ceil(g / 2))
+    // the GEMM's fp16 form applies (set when the handle is built, from its scales: every
+    // nonzero scale times 2^f16_p lies in [2^-14, 2^13))
+    bool f16 = false;
+    int f16_p = 0;
     size_t rec_bytes() const { return (size_t)nb * gp * kRecBytes; }
 };
 
@@ -111,10 +115,21 @@ hipError_t launch_decode_limb_rows(const uint4* tiles, const uint16_t* x, const 
 hipError_t launch_greedy_reduce(const unsigned long long* part, int nb, int rows, int32_t* token, float* value,
                                 hipStream_t stream);
 
+// The fp16 form's pre-pass keeps a row's group sums in LDS: rows of x of at most this
+// many groups.
+constexpr int kPrepMaxGroups = 8192;
+// Scale range of a built handle (the GEMM's fp16 form): out[0] the largest and out[1]
+// the smallest biased exponent of its nonzero scales, out[2] the count of inf or NaN
+// scales.  `out` is device memory the caller sets to {0, 255, 0} first.
+hipError_t launch_scale_range(const uint2* sb, const Layout& l, int* out, hipStream_t stream);
+// Sets l.f16 and l.f16_p from those three numbers.
+void set_f16_form(Layout& l, const int range[3]);
+
 // Prefill path: fp32-exact factored GEMM on the matrix cores.  `workspace` holds,
-// for the 256-row tile, the group sums of x and, when K is split over workgroups, the
-// fp32 partial sums (device memory, 256-byte aligned); an unsplit plan of 64- or
-// 128-row tiles needs none.  The plan is the cheapest whose workspace fits in
+// for the 256-row tile, the group sums of x (and in the fp16 form x as fp16 and each
+// row's power of two) and, when K is split over workgroups, the fp32 partial sums
+// (device memory, 256-byte aligned); an unsplit plan of 64- or 128-row tiles needs
+// none.  The plan is the cheapest whose workspace fits in
 // `workspace_bytes`; gemm_workspace_bytes(m, l) is what the unconstrained plan
 // needs, and with that much the launch runs the unconstrained plan.
 struct GemmPlan {
@@ -124,6 +139,10 @@ struct GemmPlan {
     int g_split = 0;         // groups per split (whole octets)
     size_t xaug_bytes = 0;   // group sums of x (256-row tiles)
     size_t part_bytes = 0;   // splits x M x N fp32 partial sums (0 when unsplit)
+    bool f16 = false;        // fp16 form (256-row tiles of a handle whose scales allow it)
+    size_t x16_bytes = 0;    // fp16 form: x scaled per row, as fp16 [M, kx]
+    size_t rowexp_bytes = 0; // fp16 form: each row's power of two
+    size_t total() const { return xaug_bytes + x16_bytes + rowexp_bytes + part_bytes; }
 };
 constexpr int kMaxSplits = 16;
 constexpr size_t kMaxPartialBytes = (size_t)1 << 30;

@@ -29,6 +29,8 @@ constexpr uint64_t kLoraMagic = 0x47454d344c4f5241ULL;  // "GEM4LORA"
 thread_local char g_last_error[512] = "";
 // forward path choice: 0 = automatic (q4::use_decode), r > 0 = the GEMM from r rows on
 std::atomic<uint32_t> g_gemm_min_rows{0};
+// GEMM form: 0 the fp16 form wherever a handle's scales allow it, 1 the bf16 form only
+std::atomic<uint32_t> g_gemm_form{0};
 
 // Records the message (truncated to the buffer) and returns status.  The const char*
 // forms build no std::string, so they cannot throw: catch blocks use them.
@@ -370,6 +372,31 @@ void release(Gemma4QLinear* h) {
 
 bool valid_handle(const Gemma4QLinear* h) { return h != nullptr && h->magic == kQLinearMagic; }
 
+// The layout the GEMM plans with: the handle's, without the fp16 form when the process
+// pins the bf16 form.
+q4::Layout gemm_layout(const Gemma4QLinear* h) {
+    q4::Layout l = h->layout;
+    if (g_gemm_form.load(std::memory_order_relaxed) != 0) l.f16 = false;
+    return l;
+}
+
+// Whether the handle's scales allow the GEMM's fp16 form (their exponent range, from
+// the device, once): sets h->layout.f16 and f16_p.
+hipError_t scale_form(Gemma4QLinear* h, hipStream_t stream) {
+    int* d = nullptr;
+    hipError_t e = hipMalloc(&d, 3 * sizeof(int));
+    if (e != hipSuccess) return e;
+    const int init[3] = {0, 255, 0};
+    int range[3] = {0, 0, 1};
+    e = hipMemcpyAsync(d, init, sizeof(init), hipMemcpyHostToDevice, stream);
+    if (e == hipSuccess) e = q4::launch_scale_range(h->sb, h->layout, d, stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(range, d, sizeof(range), hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    (void)hipFree(d);
+    if (e == hipSuccess) q4::set_f16_form(h->layout, range);
+    return e;
+}
+
 // One weight triple in MLX layout (device pointers).
 struct Triple {
     const uint32_t* w;
@@ -426,6 +453,12 @@ Gemma4Status build_handle(const Gemma4QLinearDesc* desc, const Triple& main, con
         release(h);
         delete h;
         return hip_fail("repack launch", e);
+    }
+    e = scale_form(h, stream);
+    if (e != hipSuccess) {
+        release(h);
+        delete h;
+        return hip_fail("scale range", e);
     }
     h->magic = kQLinearMagic;
     *out = h;
@@ -500,13 +533,14 @@ Gemma4Status dispatch_forward(const Gemma4QLinear* linear, const uint16_t* x_dev
     // workspace from the pool, or what the static scratch has left (the plan then takes
     // only tiles and splits that fit that room; an unsplit plan of 64- or 128-row tiles
     // needs none)
-    size_t ws_bytes = q4::gemm_workspace_bytes((int)rows, linear->layout);
+    const q4::Layout gl = gemm_layout(linear);
+    size_t ws_bytes = q4::gemm_workspace_bytes((int)rows, gl);
     if (sc.fixed) {
         ws_bytes = sc.room();
         // holds by construction (the plan takes only what fits the room); kept so that
         // a plan change can never overrun the array
-        const q4::GemmPlan plan = q4::plan_gemm((int)rows, linear->layout, ws_bytes);
-        if (plan.xaug_bytes + plan.part_bytes > ws_bytes)
+        const q4::GemmPlan plan = q4::plan_gemm((int)rows, gl, ws_bytes);
+        if (plan.total() > ws_bytes)
             return fail(GEMMA4_ERR_UNSUPPORTED_CONFIG, name + ": the GEMM's scratch needs more than the " +
                                                            std::to_string(kStaticScratchBytes) +
                                                            "-byte static scratch has left");
@@ -518,7 +552,7 @@ Gemma4Status dispatch_forward(const Gemma4QLinear* linear, const uint16_t* x_dev
         return fail(GEMMA4_ERR_MEMORY_GUARD, name + ": workspace allocation failed: " + hipGetErrorString(e));
     q4::LoraEpilogue lo{};
     const bool with_lora = lora != nullptr && !geglu && !sc.fixed &&
-                           q4::gemm_lora_epilogue((int)rows, linear->layout, (int)lora->rank, ws_bytes);
+                           q4::gemm_lora_epilogue((int)rows, gl, (int)lora->rank, ws_bytes);
     if (with_lora) {
         const int slices = q4::lora_slices((int)linear->desc.in_features, (int)rows);
         void* part = nullptr;
@@ -530,7 +564,7 @@ Gemma4Status dispatch_forward(const Gemma4QLinear* linear, const uint16_t* x_dev
         if (e != hipSuccess) return hip_fail((name + ": lora_down launch").c_str(), e);
         lo = q4::LoraEpilogue{static_cast<const float*>(part), lora->b, (int)lora->rank, slices, lora->scale};
     }
-    e = q4::launch_gemm(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, mode, n_out, linear->layout, ws, ws_bytes,
+    e = q4::launch_gemm(linear->tiles, linear->sb, x_dev, y_dev, (int)rows, mode, n_out, gl, ws, ws_bytes,
                         linear->gelu_table, sc.stream, with_lora ? &lo : nullptr);
     if (e != hipSuccess) return hip_fail((name + ": gemm launch").c_str(), e);
     if (lora_done != nullptr) *lora_done = with_lora;
@@ -652,6 +686,8 @@ Gemma4Status gemma4_qmm_release_scratch(void* stream) {
 uint32_t gemma4_qmm_set_decode_kernel(uint32_t variant) {
     return (uint32_t)q4::set_decode_variant(variant > 2u ? 0 : (int)variant);
 }
+
+uint32_t gemma4_qmm_set_gemm_form(uint32_t form) { return g_gemm_form.exchange(form > 1u ? 0u : form); }
 
 Gemma4Status gemma4_qlinear_create(const Gemma4QLinearDesc* desc, const uint32_t* weight,
                                    const uint16_t* scales, const uint16_t* biases, Gemma4QLinear** out) {
@@ -810,7 +846,7 @@ Gemma4Status gemma4_qlinear_scratch_bytes(const Gemma4QLinear* linear, uint32_t 
         *out = 0;
         if (rows == 0 || q4::use_decode(rows, linear->layout, (int)g_gemm_min_rows.load(std::memory_order_relaxed)))
             return ok();
-        *out = q4::gemm_workspace_bytes((int)rows, linear->layout);
+        *out = q4::gemm_workspace_bytes((int)rows, gemm_layout(linear));
         return ok();
     } catch (...) {
         return fail_nothrow(GEMMA4_ERR_RUNTIME, "gemma4_qlinear_scratch_bytes: unexpected native exception");

@@ -103,6 +103,7 @@ def load_library(path: str | None = None):
         "gemma4_qmm_get_last_error": [ctypes.c_char_p, ctypes.c_size_t],
         "gemma4_qmm_set_gemm_min_rows": [ctypes.c_uint32],
         "gemma4_qmm_set_decode_kernel": [ctypes.c_uint32],
+        "gemma4_qmm_set_gemm_form": [ctypes.c_uint32],
         "gemma4_qmm_release_scratch": [vp],
         "gemma4_qlinear_scratch_bytes": [vp, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint64)],
         "gemma4_qmlp_forward": [vp, vp, vp, vp, ctypes.c_uint32, vp, vp, ctypes.c_uint32],
@@ -176,6 +177,24 @@ def set_decode_kernel(variant: int) -> int:
     if int(variant) not in (0, 1, 2):
         raise ValueError(f"variant must be 0, 1 or 2, got {variant}")
     return int(load_library().gemma4_qmm_set_decode_kernel(int(variant)))
+
+
+def set_gemm_form(form: int) -> int:
+    """Pins the GEMM form for this process: 0 (the default) the fp16 form wherever a
+    handle's scales allow it, 1 the bf16 form only.  Returns the previous setting."""
+    if int(form) not in (0, 1):
+        raise ValueError(f"form must be 0 or 1, got {form}")
+    return int(load_library().gemma4_qmm_set_gemm_form(int(form)))
+
+
+@contextlib.contextmanager
+def gemm_form(form: int):
+    """set_gemm_form for the duration of a with-block."""
+    prev = set_gemm_form(form)
+    try:
+        yield
+    finally:
+        set_gemm_form(prev)
 
 
 @contextlib.contextmanager

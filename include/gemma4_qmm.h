@@ -143,6 +143,18 @@ uint32_t gemma4_qmm_set_gemm_min_rows(uint32_t rows);
  * it returns. */
 uint32_t gemma4_qmm_set_decode_kernel(uint32_t variant);
 
+/* GEMM (prefill) form of the forward calls in this process.  No counterpart in the
+ * reference; for tests and benchmarks that compare the two.
+ *   0 (the default): the fp16 form for 256-row tiles of handles whose scales allow it
+ *      (every nonzero scale within 2^26 of the largest, none inf or NaN): x scaled per
+ *      row by a power of two into fp16 and the weights expanded as s 2^p (q - 8),
+ *      exact fp16 products with no per-group scale step; the bf16 form elsewhere.
+ *   1: the bf16 form only (x as given, weights as 1 + q/16, scaled per group).
+ * Both meet the same accuracy contract and sum in different orders.  Values above 1
+ * are taken as 0.  Returns the previous setting; takes effect for calls issued after
+ * it returns. */
+uint32_t gemma4_qmm_set_gemm_form(uint32_t form);
+
 /* Releases the device memory the library keeps for the scratch of calls on `stream`
  * on the current device (for hipStreamPerThread, the calling thread's), after waiting
  * for the stream's work.  No counterpart in the reference (MLX frees per call); for

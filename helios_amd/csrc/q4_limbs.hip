@@ -298,7 +298,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_kernel(const uint4* __
 // A lane accumulates one row (MT <= 4) or two (MT = 8); its scale words are those of
 // the groups it holds, two 4- or 8-byte loads per chunk.  Per chunk: 4 MFMAs (8 at
 // MT = 8) and MT scale steps per lane.
-template <int MT, int NBUF, int WAVES, bool STRIDED>
+// BATCH = 0: the per-(row block, wave) sums of the whole run stay in LDS to the end.
+// BATCH > 0 (long runs, one workgroup per CU that stages x once): the run goes in
+// phases of BATCH row blocks whose sums take one half of a two-phase ring; at each
+// phase's end the waves meet at a barrier and sum (in wave order) and store that
+// phase's outputs, clearing its half for the phase after next, while the next phase's
+// loads stay in flight.
+template <int MT, int NBUF, int WAVES, bool STRIDED, int BATCH = 0>
 __global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint4* __restrict__ tiles,
                                                                       const uint16_t* __restrict__ x, OutParams op,
                                                                       int m_rows, int n_rows, int k, int kx,
@@ -324,7 +330,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint
     const int total = nrb * nch;
     char* const limbs = reinterpret_cast<char*>(lds);
     float2* const tab = reinterpret_cast<float2*>(limbs + nch * kChunkStride);  // [nch][4][MT] (2^(e-135), 8 X 2^(132-e))
-    float* const slots = reinterpret_cast<float*>(tab + nch * 4 * MT);          // [nrb][WAVES][MT][16]
+    // [nrb][WAVES][MT][16], or with BATCH the ring [2][BATCH][WAVES][MT][16]
+    float* const slots = reinterpret_cast<float*>(tab + nch * 4 * MT);
+    const int slot_rbs = BATCH ? 2 * BATCH : nrb;
 
     // scale words: MT = 2: groups q/2 (record 0) and 2 + q/2 (record 1), 4 bytes each;
     // MT >= 4: all four groups, 8 bytes of each record
@@ -434,8 +442,37 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint
     for (int f0 = 2 * nthr; f0 < units; f0 += nthr) stage(load_unit(f0 + (int)threadIdx.x), f0 + (int)threadIdx.x);
     for (int c = (int)threadIdx.x; c < nch; c += nthr)
         *reinterpret_cast<uint4*>(limbs + c * kChunkStride + kChunkBytes) = make_uint4(0, 0, 0, 0);
-    for (int t = (int)threadIdx.x; t < nrb * WAVES * MT * 16; t += nthr) slots[t] = 0.f;
+    for (int t = (int)threadIdx.x; t < slot_rbs * WAVES * MT * 16; t += nthr) slots[t] = 0.f;
     __syncthreads();
+
+    // BATCH: the end of phase ph (row blocks [ph BATCH, ph BATCH + BATCH) of the run):
+    // every wave's sums of it are in LDS after the barrier; each (row block, row)'s 16
+    // outputs are the waves' slots summed in wave order (a 16-lane row holds one, as the
+    // GeGLU and greedy stages need), and the slots read are cleared for phase ph + 2
+    int phase = 0;
+    auto end_phase = [&](int ph) {
+        wait_lds();
+        lds_barrier();
+        const int r0 = ph * BATCH;
+        const int half = (ph & 1) * BATCH;
+        for (int t0 = 0; t0 < BATCH * MT * 16; t0 += nthr) {
+            const int t = t0 + (int)threadIdx.x;
+            const int r = t / (MT * 16), m = (t >> 4) % MT;
+            const bool live = t < BATCH * MT * 16 && r0 + r < nrb;
+            float v = 0.f;
+            if (t < BATCH * MT * 16) {
+#pragma unroll
+                for (int w = 0; w < WAVES; ++w) {
+                    float* const sl = slots + (((half + r) * WAVES + w) * MT + m) * 16 + col;
+                    v += *sl;
+                    *sl = 0.f;
+                }
+            }
+            store_out(op, live ? m : MT, m_rows, rb0 + (live ? r0 + r : 0) * rbs, col, n_rows, v);
+        }
+    };
+    (void)phase;
+    (void)end_phase;
 
     // A operand address of MFMA i of a chunk for this lane (row r = col, k-quarter)
     uint32_t a_off[kMfma];
@@ -465,6 +502,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint
         ++c_rb;
     }
     auto compute = [&](int b) {
+        if constexpr (BATCH > 0) {
+            // the phases this wave's next chunk leaves behind end first
+            while (phase < c_rb / BATCH) end_phase(phase++);
+        }
         const char* const cl = limbs + c_c * kChunkStride;
         i32x4 C[kAcc];
 #pragma unroll
@@ -486,8 +527,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint
             const int m = MT <= 4 ? quarter % MT : 4 * (a & 1) + quarter;
             const uint32_t w = MT == 2 ? sw[b][a] : MT == 4 ? sw[b][a] : sw[b][a >> 1];
             const float2 tv = tc[j * MT + m];
-            const float p = __builtin_fmaf(__builtin_fmaf((float)C[a][2], 0x1p-7f, (float)C[a][1]), 0x1p-7f,
-                                           (float)C[a][0]);
+            // C_1 128 + C_2 is exact in int32 (|C_1|, |C_2| < 64 * 127 * 120 < 2^20)
+            const float p = __builtin_fmaf((float)(C[a][1] * 128 + C[a][2]), 0x1p-14f, (float)C[a][0]);
             float& r = acc[MT <= 4 ? 0 : (a & 1)];
             r = __builtin_fmaf(bf16_lo(w) * tv.x, p, r);
             r = __builtin_fmaf(bf16_hi(w) * tv.x, tv.y, r);
@@ -500,7 +541,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint
             ++c_rb;
         }
         if (c_rb != rb || c_f >= total) {
-            float* const sl = slots + (rb * WAVES + wave) * MT * 16;
+            const int srb = BATCH ? ((rb / (BATCH ? BATCH : 1)) & 1) * BATCH + rb % (BATCH ? BATCH : 1) : rb;
+            float* const sl = slots + (srb * WAVES + wave) * MT * 16;
             if constexpr (MT == 2) {
                 const float v = acc[0] + __shfl_xor(acc[0], 32);
                 if (quarter < 2) sl[quarter * 16 + col] = v;
@@ -528,6 +570,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint
     for (int b = 0; b + 1 < NBUF; ++b)
         if (i + b < mine) compute(b);
 
+    if constexpr (BATCH > 0) {
+        const int phases = (nrb + BATCH - 1) / BATCH;
+        while (phase < phases) end_phase(phase++);
+        // the loads issued past the run (zeros, no traffic) land before the end
+        __builtin_amdgcn_s_waitcnt(0);
+        return;
+    }
     __syncthreads();
     // every (row block, row)'s 16 outputs: the waves' slots summed in wave order; a
     // 16-lane row of a wave holds one (row block, row) (the GeGLU and greedy stages
@@ -597,8 +646,9 @@ namespace {
 //    contiguous runs: gate 15360x3840 9.5 / 11.6 (12.3 / 13.5);
 //  * more, up to 16 per CU: two workgroups per CU, one chunk in flight, blocks dealt
 //    round the grid: the gate|up pair 14.6 / 18.4 (19.1 / 20.4);
-//  * more still (the lm_head): 8 waves, two per CU, two chunks in flight, dealt round
-//    the grid: 95.6 / 119.6 (101.6 / 119.5).
+//  * more still (the lm_head): one 16-wave workgroup per CU, two chunks in flight,
+//    blocks dealt round the grid, the run walked in phases of two row blocks (the
+//    kernel's BATCH): 90.3-91.2 / 102-104.6 (98.2 / 114-119.5);
 // At 2 rows the one-row kernel's shapes.  Workgroups per CU are capped by what LDS
 // admits (the per-(row block, wave) sums take MT times the one-row kernel's room), and
 // the grid grows (more, shorter row-block runs) until one workgroup fits.
@@ -606,16 +656,30 @@ struct LimbRowsPlan {
     LimbConfig c;
     int grid;
     size_t lds;
+    int batch = 0;  // row blocks per phase (the kernel's BATCH), 0: none
 };
-size_t limb_rows_lds(const Layout& l, int mt, int waves, int grid) {
+constexpr int kLimbBatch = 2;
+size_t limb_rows_lds(const Layout& l, int mt, int waves, int grid, int batch = 0) {
     const size_t nch = (size_t)(l.gp + 1) / 2;
-    const size_t nrb = ((size_t)l.nb + grid - 1) / grid;
+    const size_t nrb = batch ? 2 * (size_t)batch : ((size_t)l.nb + grid - 1) / grid;
     return nch * ((size_t)4 * mt * 3 * 64 + kLimbUnitBytes) + nch * 4 * mt * sizeof(float2) +
            nrb * waves * mt * 16 * sizeof(float);
 }
 LimbRowsPlan limb_rows_plan(const Layout& l, int mt) {
     LimbRowsPlan p;
     const int cus = device_cus();
+    if (mt >= 4 && l.nb > 16 * cus) {
+        // the lm_head: one 16-wave workgroup per CU stages x once and walks its run in
+        // phases of two row blocks (4 / 8 rows: 91.2 / 104.6 us against 98.2 / 122.2 with
+        // a workgroup per few row blocks, each staging x; 8 waves and phases of 4 or 8
+        // row blocks, or 3 chunks in flight: 1-3% slower at 8 rows)
+        p.c = {16, 1, 2, true};
+        p.batch = kLimbBatch;
+        p.grid = cus;
+        p.lds = limb_rows_lds(l, mt, p.c.waves, p.grid, p.batch);
+        if (p.lds <= (size_t)160 * 1024) return p;
+        p.batch = 0;
+    }
     if (mt == 2)
         p.c = limb_config(l);
     else if (l.nb <= 4 * cus)
@@ -645,10 +709,11 @@ size_t limb_rows_lds_bytes(const Layout& l, int m) { return limb_rows_plan(l, ro
 
 bool limb_rows_preferred(const Layout& l, int m) {
     if (m == 2) return true;
-    // 3-8 rows: only wide 4-bit outputs gain (qkv and o lose at 8 rows, the lm_head
-    // ties there); the two-plane 8-bit handles were not measured on these shapes
+    // 3-8 rows: only wide 4-bit outputs gain (qkv and o lose at 8 rows; the lm_head at
+    // 8 rows 102-104.6 us phased against 114 for the bf16 kernels); the two-plane 8-bit
+    // handles were not measured on these shapes
     const int cus = device_cus();
-    return l.kx == l.k && l.nb >= 3 * cus && (m <= 4 || l.nb <= 16 * cus);
+    return l.kx == l.k && l.nb >= 3 * cus;
 }
 
 hipError_t launch_decode_limb_rows(const uint4* tiles, const uint16_t* x, const OutParams& op, int m,
@@ -667,6 +732,13 @@ hipError_t launch_decode_limb_rows(const uint4* tiles, const uint16_t* x, const 
             Q4_LR(2, 2, 8, false);
         else
             Q4_LR(2, 1, 8, true);
+    } else if (p.batch) {
+        if (mt == 4)
+            hipLaunchKernelGGL((decode_limb_rows_kernel<4, 2, 16, true, kLimbBatch>), grid, block, p.lds, stream, tiles,
+                               x, op, m, l.n, l.k, l.kx, l.gp, l.nb);
+        else
+            hipLaunchKernelGGL((decode_limb_rows_kernel<8, 2, 16, true, kLimbBatch>), grid, block, p.lds, stream, tiles,
+                               x, op, m, l.n, l.k, l.kx, l.gp, l.nb);
     } else if (mt == 4) {
         if (!p.c.strided)
             Q4_LR(4, 2, 16, false);

@@ -470,10 +470,21 @@ def test_decode_limb_accesses_two_plane(n, k):
     audit_decode_limbs(n, 2 * k, kx=k)
 
 
+LIMB_BATCH = 2
+
+
 def limb_rows_plan(nb, gp, mt, cus=256):
-    """q4_limbs.hip limb_rows_plan: at 2 rows the one-row launch shape, at 4 and 8 the
+    """q4_limbs.hip limb_rows_plan: at 4 and 8 rows with more than 16 row blocks per CU
+    one 16-wave workgroup per CU walking its run in phases of LIMB_BATCH row blocks (a
+    two-phase ring of sums); else at 2 rows the one-row launch shape, at 4 and 8 the
     swept shapes; workgroups per CU capped by the LDS, then the grid doubled (up to one
-    workgroup per row block) until one fits.  Returns (waves, nbuf, strided, grid, lds)."""
+    workgroup per row block) until one fits.  Returns (waves, nbuf, strided, grid, lds,
+    batch)."""
+    nch = (gp + 1) // 2
+    if mt >= 4 and nb > 16 * cus:
+        lds = nch * (4 * mt * 3 * 64 + 16) + nch * 4 * mt * 8 + 2 * LIMB_BATCH * 16 * mt * 16 * 4
+        if lds <= LDS_BYTES:
+            return 16, 2, True, cus, lds, LIMB_BATCH
     if mt == 2:
         waves, per_cu, nbuf, strided = limb_config(nb, gp, cus)
     elif nb <= 4 * cus:
@@ -496,19 +507,21 @@ def limb_rows_plan(nb, gp, mt, cus=256):
         per_cu = max(fit, 1)
     while lds(grid) > LDS_BYTES and grid < nb:
         grid = min(2 * grid, nb)
-    return waves, nbuf, strided, grid, lds(grid)
+    return waves, nbuf, strided, grid, lds(grid), 0
 
 
 def audit_decode_limb_rows(m_rows, n, k, kx=None, cus=256):
     """decode_limb_rows_kernel (2-8 rows of x): the chunk walk as in the one-row kernel;
     the scale-word loads; the staging of m_rows x' rows into [chunk][group][row][limb]
     [quarter] limb units, the (chunk, group, row) table and the zero unit; the A operand
-    reads of every MFMA; the (row block, wave, row) slots and the final stores."""
+    reads of every MFMA; the (row block, wave, row) slots and the final stores; with
+    phases, the ring of slots (two row blocks live at once never share a slot) and each
+    phase's stores."""
     kx = k if kx is None else kx
     mt = 2 if m_rows <= 2 else 4 if m_rows <= 4 else 8
     L = layout(n, k)
     nb, gp = L["nb"], L["gp"]
-    waves, nbuf, strided, grid, lds = limb_rows_plan(nb, gp, mt, cus)
+    waves, nbuf, strided, grid, lds, batch = limb_rows_plan(nb, gp, mt, cus)
     if lds > LDS_BYTES:
         return None  # the launcher refuses it (the bf16 kernels run)
     nch = (gp + 1) // 2
@@ -543,13 +556,31 @@ def audit_decode_limb_rows(m_rows, n, k, kx=None, cus=256):
                     assert (base + off[inr] + size <= L["rec_bytes"]).all()
                 if live:
                     seen[rb0 + i_rb * rbs, c] += 1
-                    # the lane's slot rows and the chunk's table entries
-                    assert ((i_rb * waves + w) * mt + mt - 1) * 16 + 15 < nrb * waves * mt * 16
+                    # the lane's slot rows (with phases: ring slot of the row block) and
+                    # the chunk's table entries
+                    srb = ((i_rb // batch) & 1) * batch + i_rb % batch if batch else i_rb
+                    slot_rbs = 2 * batch if batch else nrb
+                    assert ((srb * waves + w) * mt + mt - 1) * 16 + 15 < slot_rbs * waves * mt * 16
                     assert (c * 4 * mt + 3 * mt + mt - 1) < nch * 4 * mt
-        for r in range(nrb):
-            stored[rb0 + r * rbs] += 1
+        if batch:
+            # phase ph stores row blocks [ph batch, ph batch + batch) of the run from ring
+            # half ph % 2; the row blocks of phases ph and ph + 1 (live together) take
+            # different slots
+            for ph in range((nrb + batch - 1) // batch):
+                for r in range(batch):
+                    if ph * batch + r < nrb:
+                        stored[rb0 + (ph * batch + r) * rbs] += 1
+            for i_rb in range(nrb):
+                for j_rb in range(i_rb + 1, min(nrb, (i_rb // batch + 2) * batch)):
+                    a = ((i_rb // batch) & 1) * batch + i_rb % batch
+                    bb = ((j_rb // batch) & 1) * batch + j_rb % batch
+                    assert a != bb, (i_rb, j_rb)
+        else:
+            for r in range(nrb):
+                stored[rb0 + r * rbs] += 1
     assert (seen == 1).all() and (stored == 1).all()
-    assert nch * stride + nch * 4 * mt * 8 + nrb_max * waves * mt * 16 * 4 == lds
+    slot_rbs = 2 * batch if batch else nrb_max
+    assert nch * stride + nch * 4 * mt * 8 + slot_rbs * waves * mt * 16 * 4 == lds
     # staging: flat unit f -> (row m, unit u); writes inside the chunk's limb region
     runits = nch * 32
     f = np.arange(mt * runits)
@@ -580,9 +611,11 @@ def audit_decode_limb_rows(m_rows, n, k, kx=None, cus=256):
                     hits[j, mm, l, q] += 1
     assert (hits == 1).all()  # every (group, row, limb, quarter) unit read by exactly one MFMA lane
     # final stores: t -> (row block run index, row, column) covers every output once
-    t = np.arange(nrb_max * mt * 16)
+    # (with phases: t -> (row block of the phase, row, column) over a ring half)
+    t = np.arange((batch if batch else nrb_max) * mt * 16)
     r, mm = t // (mt * 16), (t >> 4) % mt
-    assert (((r * waves + waves - 1) * mt + mm) * 16 + 15 < nrb_max * waves * mt * 16).all()
+    for half in ((0, batch) if batch else (0,)):
+        assert ((((half + r) * waves + waves - 1) * mt + mm) * 16 + 15 < slot_rbs * waves * mt * 16).all()
     return lds
 
 

@@ -126,10 +126,12 @@ def test_limb_register_budgets():
 def test_limb_rows_register_budgets():
     """decode_limb_rows_kernel: no scratch; the 16-wave instance dealt round the grid at
     4 rows runs two workgroups per CU (8 waves per SIMD: at most 64 VGPRs); the rest
-    run one 16-wave workgroup per CU (at most 128) or 8-wave ones."""
+    run one 16-wave workgroup per CU (at most 128; the two phased ones, BATCH > 0,
+    among them) or 8-wave ones."""
     asm = hbuild.device_asm("q4_limbs.hip")
     meta = [(n, v, p) for n, v, p in _kernel_meta(asm) if "decode_limb_rows_kernel" in n]
-    assert len(meta) == 9
+    assert len(meta) == 11
+    assert sum(bool(re.search(r"ELb1ELi[1-9]\d*E", n)) for n, _, _ in meta) == 2
     for name, vgprs, private in meta:
         assert private == 0, f"{name} spills to scratch"
         mt, nbuf, waves = map(int, re.search(r"decode_limb_rows_kernelILi(\d+)ELi(\d+)ELi(\d+)E", name).groups())

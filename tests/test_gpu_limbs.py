@@ -251,10 +251,11 @@ def test_rows_gate_up_pair(gpu_lib, m):
     pair.close()
 
 
-@pytest.mark.parametrize("m", [2, 8])
+@pytest.mark.parametrize("m", [2, 4, 8])
 def test_rows_lm_head_and_greedy(gpu_lib, m):
-    """The lm_head at 2 and 8 rows (every output against the oracle) and its greedy
-    head under the int8 kernels."""
+    """The lm_head at 2, 4 and 8 rows (every output against the oracle; at 4 and 8 rows
+    the phased launch, one workgroup per CU) and its greedy head under the int8
+    kernels."""
     import torch
 
     from test_gpu_greedy import _check_token, _oracle

@@ -529,7 +529,8 @@ def summarize_trace(db_path: str, out_md: str, command: str) -> None:
     --kernel-trace database (rocpd SQLite).  Each shape's handles are created (repack
     launches) before its forwards, which split the trace into the sweep's shapes in
     order; a GEMM-path forward launches the GEMM (after xaug_kernel, the group-sum
-    pre-pass, for the 256-row tile) and, when K is split, the split-K reduction; a
+    pre-pass, or xprep_kernel, the fp16 form's, for the 256-row tile) and, when K is
+    split, the split-K reduction; a
     decode-path forward one decode kernel.  Reported: the median
     duration of each kernel and of the whole forward (first launch start to last
     launch end) over the shape's forwards."""
@@ -579,7 +580,7 @@ DECODE_PROFILE = [("k_proj", 1), ("q_proj", 1), ("o_proj", 1), ("qkv_proj", 1), 
 def _trace_forwards(rows, short):
     """Kernel launches of a trace in start order, grouped per shape (each shape's
     handles are created, with repack launches, before its forwards) and per forward (a
-    GEMM-path forward starts with the GEMM, or xaug_kernel for the 256-row tile; a
+    GEMM-path forward starts with the GEMM, or its pre-pass for the 256-row tile; a
     decode-path forward is one decode kernel)."""
     shapes = []
     for r in rows:
@@ -589,8 +590,9 @@ def _trace_forwards(rows, short):
         if s.startswith("repack"):
             if not shapes or shapes[-1]:
                 shapes.append([])
-        elif shapes and (s.startswith("xaug") or s.startswith("decode") or
-                         (s.startswith("gemm_kernel") and not (shapes[-1] and short(shapes[-1][-1][-1][0]).startswith("xaug")))):
+        elif shapes and (s.startswith(("xaug", "xprep")) or s.startswith("decode") or
+                         (s.startswith("gemm_kernel") and
+                          not (shapes[-1] and short(shapes[-1][-1][-1][0]).startswith(("xaug", "xprep"))))):
             shapes[-1].append([r])
         elif shapes and shapes[-1]:
             shapes[-1][-1].append(r)

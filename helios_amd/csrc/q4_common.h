@@ -141,6 +141,21 @@ __device__ __forceinline__ f16x8 expand_word_f16(uint32_t u, f16x2 s) {
     return r;
 }
 
+// 8-bit codes in one pass (a two-plane handle's GEMM): the high plane's word h and the
+// low plane's word l of the same (lane, group, half) hold q >> 4 and q & 15 of the same
+// eight codes.  -> the eight fp16 values 1024 + q (exact: 11 significant bits) in
+// element order: q_h from bits 3..6 shifted to 4..7, q_l rotated down to bits 0..3,
+// under the exponent of 1024.
+constexpr uint32_t kF16x2Of1024 = 0x64006400u;
+__device__ __forceinline__ f16x8 expand_word_q8(uint32_t h, uint32_t l) {
+    uint4 d;
+    d.x = ((h & kNibMask) << 1) | and_or(rotr(l, 3), 0x000F000Fu, kF16x2Of1024);
+    d.y = ((rotr(h, 4) & kNibMask) << 1) | and_or(rotr(l, 7), 0x000F000Fu, kF16x2Of1024);
+    d.z = ((rotr(h, 8) & kNibMask) << 1) | and_or(rotr(l, 11), 0x000F000Fu, kF16x2Of1024);
+    d.w = ((rotr(h, 12) & kNibMask) << 1) | and_or(rotr(l, 15), 0x000F000Fu, kF16x2Of1024);
+    return __builtin_bit_cast(f16x8, d);
+}
+
 // q[2p] and q[2p+1] of a tiled word, for the dequantize kernel.
 __device__ __forceinline__ uint32_t word_nibble(uint32_t u, int i) {
     const uint32_t r = rotr(u, 4 * (i >> 1));

@@ -46,6 +46,8 @@
 // operand reads are bank-conflict free), the group's weight words and scale words;
 // the bias operands once per 8 groups.  The rings have three slots, so each load has
 // two steps of arithmetic to arrive in.
+#include <type_traits>
+
 #include "q4_common.h"
 #include "q4_kernels.h"
 
@@ -152,6 +154,9 @@ __device__ __forceinline__ uint32_t finite_max_bits(uint4 v) {
     return mb;
 }
 
+// C: the bias operand's factor (8 for the fp16 form; -64 for one-pass 8-bit, whose
+// scale words hold 16 s: -64 * 16 s = -1024 s).
+template <int C>
 __global__ __launch_bounds__(64 * kPrepRows) void xprep_kernel(const uint16_t* __restrict__ x,
                                                                uint16_t* __restrict__ x16, uint4* __restrict__ xaug,
                                                                int* __restrict__ rowexp, int m_rows, int kx, int groups,
@@ -233,7 +238,7 @@ __global__ __launch_bounds__(64 * kPrepRows) void xprep_kernel(const uint16_t* _
             const int g = 8 * o + 2 * kq + gi;
             xs[gi] = (m < m_rows && g < groups) ? __builtin_amdgcn_ldexpf(gsum[g >= gx ? g - gx : g], p) : 0.0f;
         }
-        xaug[(m16 * octets + o) * 64 + kq * 16 + r] = bias_a_operand<8>(xs[0], xs[1]);
+        xaug[(m16 * octets + o) * 64 + kq * 16 + r] = bias_a_operand<C>(xs[0], xs[1]);
     }
 }
 
@@ -403,30 +408,40 @@ __device__ __forceinline__ void lora_store(const f32x4 (&acc)[kMT][kNT], const L
 // (a shared array would make it wait for every DMA before every read); it tells apart
 // at most eight such objects.
 
-template <int OUT, int BM, int BN, bool F16 = false>
+// FORM: 0 the bf16 form; 1 the fp16 form (x16 from the pre-pass, B = s' (q - 8));
+// 2 an 8-bit two-plane handle in one pass over K (x16 from the pre-pass, B = 1024 + q
+// from the two planes' words, the per-group scale step of the bf16 form).
+template <int OUT, int BM, int BN, int FORM = 0>
 __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ tiles, const uint2* __restrict__ sb,
                                                    const uint16_t* __restrict__ x, const uint4* __restrict__ xaug,
                                                    void* __restrict__ y, int m_rows, int n_rows, int kx, int groups,
                                                    int gpairs, int mtiles, int ntiles, int octets, uint32_t rec_bytes,
                                                    int g_split, long split_stride, int n_out,
                                                    const uint16_t* __restrict__ gelu_table, LoraEpilogue lora,
-                                                   const int* __restrict__ rowexp, float s_pow) {
+                                                   const int* __restrict__ rowexp, float s_pow, int lo_pairs) {
     // BN / 32 waves of BM x 32: BM = 256; BM = 128 (more workgroups for small M
-    // without splitting K); BM = 64 (fewest K splits for narrow outputs).  F16: the fp16
-    // form (x is x16 then; rowexp and s_pow = 2^p from the pre-pass and the handle).
+    // without splitting K); BM = 64 (fewest K splits for narrow outputs).  FORM 1 and 2:
+    // x is x16, rowexp from the pre-pass; FORM 1: s_pow = 2^p of the handle; FORM 2:
+    // groups and pairs count the original K (the high plane), the low plane's pair p
+    // is record lo_pairs + p.
     static_assert(BM == 256 || BM == 128 || BM == 64, "tile rows");
     static_assert(BN == 256 || BN == 128, "tile columns");
+    constexpr bool F16 = FORM == 1;
+    constexpr bool kQ8 = FORM == 2;
     static_assert(!F16 || BM == 256, "the fp16 form takes its group sums from the pre-pass");
+    static_assert(!kQ8 || BM == 128, "one-pass 8-bit: two planes' words per pair fit LDS beside 128-row x tiles");
     constexpr int kWaves = BN / kWN;              // side by side along N
     constexpr int kRB = BN / 16;                  // 16-row weight blocks per workgroup tile
     constexpr int kXChunks = BM * 8;              // 16-byte chunks of one x group tile (BM rows x 64 bf16)
-    constexpr int kWPair = kRB * 64;              // uint4: tiled words of the pair
+    constexpr int kWPair = kRB * 64;              // uint4: tiled words of the pair (of one plane)
+    constexpr int kWS = kQ8 ? 2 * kWPair : kWPair;  // uint4: a slot's words (both planes for FORM 2)
     constexpr int kSPair = kRB * 16 / 2;          // uint4: scale/bias words of the pair
     constexpr int kXaA = BM / 16 * 64;            // uint4: the bias A operands of the tile's rows
     constexpr int kMT = BM / 16;                  // 16x16 tiles per wave along M
     constexpr int kXParts = BM * 8 / (64 * kWaves);  // 16-byte x loads per wave per group
-    // X_g summed in the kernel (64 and 128 rows), or read from xaug (256 rows)
-    constexpr bool kXIn = BM < 256;
+    // X_g summed in the kernel (64 and 128 rows), or read from xaug (256 rows, and every
+    // tile of the pre-pass forms)
+    constexpr bool kXIn = BM < 256 && FORM == 0;
     // in the kernel: row tiles whose X_g a wave sums, tiles wave + 8t (BM = 64: waves
     // 0-3 one each, the rest none)
     constexpr int kXTiles = kXIn ? (kMT + kWaves - 1) / kWaves : 0;
@@ -440,8 +455,8 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     __shared__ uint4 g_xs0[kXChunks];             // x group tiles (BM rows x 64: 16 or 32 KiB)
     __shared__ uint4 g_xs1[kXChunks];
     __shared__ uint4 g_xs2[kXChunks];
-    __shared__ uint4 g_wp0[kWPair + kSPair];      // a pair's weights: 9 or 18 KiB
-    __shared__ uint4 g_wp1[kWPair + kSPair];
+    __shared__ uint4 g_wp0[kWS + kSPair];         // a pair's weights: 9 or 18 KiB (34 for FORM 2)
+    __shared__ uint4 g_wp1[kWS + kSPair];
     // one octet's bias operands: A side for the tile's rows [m16][lane] (written by the
     // waves, or DMA from xaug), then the scale/bias words as uint2 [row block][pair][column]
     // (DMA)
@@ -507,9 +522,12 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     };
     auto dma_w = [&](int p, int part, uint4* wdst) {
         dma16(p < p_end ? trs : zrs, wdst + (2 * wave + part) * 64, wv[part], (uint32_t)p * kRecBytes);
+        if constexpr (kQ8)  // the low plane's words of the same groups
+            dma16(p < p_end ? trs : zrs, wdst + kWPair + (2 * wave + part) * 64, wv[part],
+                  (uint32_t)(lo_pairs + p) * kRecBytes);
     };
     auto dma_s = [&](int p, uint4* wdst) {
-        dma16(p < p_end ? srs : zrs, wdst + kWPair + 64 * wave, sv, (uint32_t)p * kRecBytes);
+        dma16(p < p_end ? srs : zrs, wdst + kWS + 64 * wave, sv, (uint32_t)p * kRecBytes);
     };
     // bias operands of octet o: from xaug (256 rows) the A side, kXaParts 16-byte loads;
     // the scale/bias words of its four group pairs for row blocks 2w, 2w+1 (lane l: row
@@ -527,7 +545,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         }
         const int rb = rbw + 2 * wave + (ln >> 5);
         const int chunk = ln & 31;
-        const bool ok = (rb < nblocks) & (4 * o + (chunk >> 3) < gpairs);
+        const bool ok = (rb < nblocks) & (4 * o + (chunk >> 3) < (kQ8 ? lo_pairs : gpairs));
         const uint32_t raw = ((uint32_t)rb * (uint32_t)gpairs + 4u * (uint32_t)o + (uint32_t)(chunk >> 3)) * kRecBytes +
                              (uint32_t)(chunk & 7) * 16u;
         dma16(srs, g_xab + (kXaA + wave * 64), ok ? raw : kOutOfRange);
@@ -561,13 +579,15 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         int ln = threadIdx.x & 63;
         asm volatile("" : "+v"(ln));
         const int lcol = ln & 15, lkq = ln >> 4;
-        const uint2* sbl = reinterpret_cast<const uint2*>(wp + kWPair);
+        const uint2* sbl = reinterpret_cast<const uint2*>(wp + kWS);
         uint2 tw[kNT];      // this group's two tiled words of each row block
+        uint2 tl[kNT];      // FORM 2: the low plane's words of the same groups
         uint32_t swv[kNT];  // and its scale/bias word
 #pragma unroll
         for (int j = 0; j < kNT; ++j) {
             const int rbl = wave * kNT + j;
             tw[j] = reinterpret_cast<const uint2*>(wp + rbl * 64 + ln)[gpar];
+            if constexpr (kQ8) tl[j] = reinterpret_cast<const uint2*>(wp + kWPair + rbl * 64 + ln)[gpar];
             swv[j] = reinterpret_cast<const uint32_t*>(sbl + rbl * 16 + lcol)[gpar];
         }
         auto a_frag = [&](int i, int h) {
@@ -621,10 +641,12 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         // scale FMAs, which do not wait for them; row 0 expands each row block's words
         // just before its first products, and the next row's A operands are read one
         // row ahead.  Left to itself the compiler expands all words first and then
-        // issues long runs of products with no VALU work beside them.
+        // issues long runs of products with no VALU work beside them.  FORM 2 runs the
+        // same stream on fp16 operands: x16 against 1024 + q, scaled by s per group (the
+        // high plane's word holds 16 s).
         constexpr int kTiles = kMT * kNT;
         constexpr int kLag = 3;
-        bf16x8 bq[kNT][2];
+        typename std::conditional<kQ8, f16x8, bf16x8>::type bq[kNT][2];
         float s16[kNT];
         f32x4 p[kLag + 1];
         bf16x8 a0 = a_frag(0, 0), a1 = a_frag(0, 1), n0, n1;
@@ -633,16 +655,27 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
             if (t < kTiles) {
                 const int i = t / kNT, j = t % kNT;
                 if (i == 0) {
-                    bq[j][0] = expand_word(tw[j].x);
-                    bq[j][1] = expand_word(tw[j].y);
-                    s16[j] = bf16_lo(swv[j]) * 16.0f;
+                    if constexpr (kQ8) {
+                        bq[j][0] = expand_word_q8(tw[j].x, tl[j].x);
+                        bq[j][1] = expand_word_q8(tw[j].y, tl[j].y);
+                        s16[j] = bf16_lo(swv[j]) * 0.0625f;
+                    } else {
+                        bq[j][0] = expand_word(tw[j].x);
+                        bq[j][1] = expand_word(tw[j].y);
+                        s16[j] = bf16_lo(swv[j]) * 16.0f;
+                    }
                 }
                 if (j == 0 && i + 1 < kMT) {
                     n0 = a_frag(i + 1, 0);
                     n1 = a_frag(i + 1, 1);
                 }
-                p[t % (kLag + 1)] = mfma16x16x32(a0, bq[j][0], zero);
-                p[t % (kLag + 1)] = mfma16x16x32(a1, bq[j][1], p[t % (kLag + 1)]);
+                if constexpr (kQ8) {
+                    p[t % (kLag + 1)] = mfma16x16x32(__builtin_bit_cast(f16x8, a0), bq[j][0], zero);
+                    p[t % (kLag + 1)] = mfma16x16x32(__builtin_bit_cast(f16x8, a1), bq[j][1], p[t % (kLag + 1)]);
+                } else {
+                    p[t % (kLag + 1)] = mfma16x16x32(a0, bq[j][0], zero);
+                    p[t % (kLag + 1)] = mfma16x16x32(a1, bq[j][1], p[t % (kLag + 1)]);
+                }
                 if (j == kNT - 1) {
                     a0 = n0;
                     a1 = n1;
@@ -687,7 +720,8 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     // counts are fixed.
     auto issues_xa = [&](int g) { return (g & 7) == 1 && g > g_begin + 1; };
     auto issued = [&](int g) {  // loads this wave issues at step g
-        return kXParts + ((g & 1) == 0 ? 2 + (wave < kSWaves ? 1 : 0) : 0) + (issues_xa(g) ? 1 + (kXIn ? 0 : kXaParts) : 0);
+        return kXParts + ((g & 1) == 0 ? (kQ8 ? 4 : 2) + (wave < kSWaves ? 1 : 0) : 0) +
+               (issues_xa(g) ? 1 + (kXIn ? 0 : kXaParts) : 0);
     };
     // the octet's A operands of the wave's row tiles into the bias slot; X_g restarts.
     // (At the top of a step, before its barrier: written at the end of one, inlined in
@@ -781,8 +815,8 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         lds_barrier();
         bias();
     }
-    if constexpr (F16) {
-        // the fp16 form's sums are y 2^(k + p): rows 4kq + e of each row tile scaled back
+    if constexpr (F16 || kQ8) {
+        // the pre-pass forms' sums are y 2^(k + p): rows 4kq + e of each row tile scaled back
         // (exact: a power of two).  The row index is opaque here, so the exponent loads
         // stay after the main loop (hoisted ahead of it, 64 values would stay live
         // through it and spill).
@@ -1000,6 +1034,10 @@ constexpr double kPrePassUs = 3.0;             // the 256-row tile's group-sum p
 // time per byte of x16 (12.3 us against the group-sum pre-pass's 5.0 for 15.7 MB)
 constexpr double kF16StepScale = 0.965;
 constexpr double kPrepBytesPerUs = 2.15e6;
+// one-pass 8-bit (128-row tiles): its group step (over K, not 2K) against the 4-bit
+// 128-row tile's (8-bit gate 15360x3840 at 2048 rows: 325 us with the pre-pass, 240
+// steps per CU)
+constexpr double kQ8StepScale = 1.2;
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 }  // namespace
 
@@ -1030,22 +1068,28 @@ hipError_t launch_scale_range(const uint2* sb, const Layout& l, int* out, hipStr
 
 GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
     GemmPlan p;
-    const int octets = (l.g + 7) / 8;
     const long cus = device_cus();
+    // one-pass 8-bit: a two-plane handle whose low plane's group pairs line up with the
+    // high plane's (an even number of groups per plane)
+    const bool q8_ok = l.prepass_forms && l.k == 2 * l.kx && (l.g / 2) % 2 == 0 && l.kx / 64 <= kPrepMaxGroups;
     double best = -1.0;
     for (const TileShape& ts : kTileShapes) {
         if (ts.max_m > 0 && m > ts.max_m) continue;
         const int bm = ts.bm, bn = ts.bn;
         const long tiles = (long)((m + bm - 1) / bm) * ((l.n + bn - 1) / bn);
-        // the 256-row tile in the fp16 form (where the handle's scales allow it) and
-        // in the bf16 form
-        for (int form = (bm == 256 && l.f16) ? 1 : 0; form >= 0; --form) {
-            const bool f16 = form == 1;
-            // the 256-row tile's X_g pre-pass (bias A operands of every 16-row block and
-            // octet); the fp16 form's x16 and row exponents
-            const size_t xa = bm == 256 ? ((size_t)m + bm - 1) / bm * (bm / 16) * octets * 1024 : 0;
-            const size_t x16 = f16 ? round256((size_t)m * l.kx * 2) : 0;
-            const size_t rexp = f16 ? round256((size_t)m * 4) : 0;
+        // form 0: the bf16 form; 1: the fp16 form (256-row tiles of handles whose scales
+        // allow it); 2: one-pass 8-bit (128-row tiles)
+        for (int form = 2; form >= 0; --form) {
+            if ((form == 1 && !(bm == 256 && l.f16 && l.prepass_forms)) || (form == 2 && !(bm == 128 && q8_ok)))
+                continue;
+            const bool pre = form != 0;
+            const int groups = form == 2 ? l.g / 2 : l.g;
+            const int octets = (groups + 7) / 8;
+            // the X_g pre-pass (bias A operands of every 16-row block and octet) of the
+            // 256-row tile and of the pre-pass forms; their x16 and row exponents
+            const size_t xa = (bm == 256 || pre) ? ((size_t)m + bm - 1) / bm * (bm / 16) * octets * 1024 : 0;
+            const size_t x16 = pre ? round256((size_t)m * l.kx * 2) : 0;
+            const size_t rexp = pre ? round256((size_t)m * 4) : 0;
             for (int s = 1; s <= octets && s <= kMaxSplits; ++s) {
                 const int per = (octets + s - 1) / s;
                 const int used = (octets + per - 1) / per;  // splits that get work
@@ -1054,10 +1098,10 @@ GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
                 if (part > kMaxPartialBytes) break;
                 if (xa + x16 + rexp + part > max_workspace) break;  // (more splits need more)
                 const double rounds = (double)((tiles * s + cus * ts.per_cu - 1) / (cus * ts.per_cu));
-                const double step = ts.step_us * (f16 ? kF16StepScale : 1.0);
+                const double step = ts.step_us * (form == 1 ? kF16StepScale : form == 2 ? kQ8StepScale : 1.0);
                 const double t = rounds * (per * 8 * step + kRoundUs) +
                                  (s > 1 ? kSplitUs + part / kPartialBytesPerUs : 0.0) +
-                                 (bm == 256 ? kPrePassUs + x16 / kPrepBytesPerUs : 0.0);
+                                 ((bm == 256 || pre) ? kPrePassUs + x16 / kPrepBytesPerUs : 0.0);
                 if (best < 0.0 || t < best) {
                     best = t;
                     p.bm = bm;
@@ -1066,7 +1110,8 @@ GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
                     p.g_split = per * 8;
                     p.part_bytes = part;
                     p.xaug_bytes = xa;
-                    p.f16 = f16;
+                    p.f16 = form == 1;
+                    p.q8 = form == 2;
                     p.x16_bytes = x16;
                     p.rowexp_bytes = rexp;
                 }
@@ -1096,22 +1141,31 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
     if (lora != nullptr && (plan.splits != 1 || out_mode > kOutF32 || lo.rank % 4 != 0 || lo.rank < 4 ||
                             lo.rank > 32 || lo.slices < 1 || lo.part == nullptr || lo.b == nullptr))
         return hipErrorInvalidValue;
-    const int octets = (l.g + 7) / 8;
+    // one-pass 8-bit: groups and octets of K (the high plane), the low plane from pair
+    // groups / 2 of each row block's records
+    const int groups = plan.q8 ? l.g / 2 : l.g;
+    const int octets = (groups + 7) / 8;
+    const int lo_pairs = plan.q8 ? groups / 2 : 0;
     const int mtiles = (m + plan.bm - 1) / plan.bm;
     const int ntiles = (l.n + plan.bn - 1) / plan.bn;
     // workspace: [group sums | x16 | row exponents | partial sums], each 256-byte aligned
     char* const wsb = static_cast<char*>(workspace);
     uint4* xaug = plan.xaug_bytes ? reinterpret_cast<uint4*>(wsb) : nullptr;
-    uint16_t* x16 = plan.f16 ? reinterpret_cast<uint16_t*>(wsb + plan.xaug_bytes) : nullptr;
-    int* rowexp = plan.f16 ? reinterpret_cast<int*>(wsb + plan.xaug_bytes + plan.x16_bytes) : nullptr;
+    const bool pre = plan.f16 || plan.q8;
+    uint16_t* x16 = pre ? reinterpret_cast<uint16_t*>(wsb + plan.xaug_bytes) : nullptr;
+    int* rowexp = pre ? reinterpret_cast<int*>(wsb + plan.xaug_bytes + plan.x16_bytes) : nullptr;
     float* part = reinterpret_cast<float*>(wsb + plan.xaug_bytes + plan.x16_bytes + plan.rowexp_bytes);
     if (l.rec_bytes() > kMaxBufferBytes || (size_t)m * l.kx * 2 > kMaxBufferBytes || plan.xaug_bytes > kMaxBufferBytes)
         return hipErrorInvalidValue;
-    if (plan.f16) {
+    if (pre) {
         // one wave per row of the tiles
-        hipLaunchKernelGGL(xprep_kernel, dim3((unsigned)(mtiles * plan.bm / kPrepRows)), dim3(64 * kPrepRows),
-                           (size_t)kPrepRows * (l.kx / 64) * sizeof(float), stream, x, x16, xaug, rowexp, m, l.kx, l.g,
-                           octets, l.f16_p);
+        const dim3 pg((unsigned)(mtiles * plan.bm / kPrepRows)), pb(64 * kPrepRows);
+        const size_t plds = (size_t)kPrepRows * (l.kx / 64) * sizeof(float);
+        if (plan.q8)
+            hipLaunchKernelGGL(xprep_kernel<-64>, pg, pb, plds, stream, x, x16, xaug, rowexp, m, l.kx, groups, octets, 0);
+        else
+            hipLaunchKernelGGL(xprep_kernel<8>, pg, pb, plds, stream, x, x16, xaug, rowexp, m, l.kx, groups, octets,
+                               l.f16_p);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     } else if (plan.xaug_bytes) {
@@ -1120,21 +1174,24 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    const uint16_t* const xin = plan.f16 ? x16 : x;
+    const uint16_t* const xin = pre ? x16 : x;
     const float s_pow = plan.f16 ? __builtin_ldexpf(1.0f, l.f16_p) : 1.0f;
     const dim3 grid((unsigned)(mtiles * ntiles), (unsigned)plan.splits), block(2 * plan.bn);
     const uint32_t rec_bytes = (uint32_t)l.rec_bytes();
     const long elems = (long)m * l.n;
     // one instantiation per (output mode, tile shape, form)
 #define Q4_GEMM_ARGS(YPTR, STRIDE)                                                                               \
-    tiles, sb, xin, xaug, YPTR, m, l.n, l.kx, l.g, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split, STRIDE, \
-        n_out, gelu_table, lo, rowexp, s_pow
+    tiles, sb, xin, xaug, YPTR, m, l.n, l.kx, groups, l.gp, mtiles, ntiles, octets, rec_bytes, plan.g_split,      \
+        STRIDE, n_out, gelu_table, lo, rowexp, s_pow, lo_pairs
 #define Q4_GEMM_LAUNCH(MODE, YPTR, STRIDE)                                                                       \
     do {                                                                                                         \
         if (plan.bm == 64)                                                                                       \
             hipLaunchKernelGGL((gemm_kernel<MODE, 64, 256>), grid, block, 0, stream, Q4_GEMM_ARGS(YPTR, STRIDE));  \
         else if (plan.bm == 256 && plan.f16)                                                                     \
-            hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256, true>), grid, block, 0, stream,                      \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256, 1>), grid, block, 0, stream,                         \
+                               Q4_GEMM_ARGS(YPTR, STRIDE));                                                      \
+        else if (plan.bm == 128 && plan.q8)                                                                      \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 128, 256, 2>), grid, block, 0, stream,                         \
                                Q4_GEMM_ARGS(YPTR, STRIDE));                                                      \
         else if (plan.bm == 256)                                                                                 \
             hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256>), grid, block, 0, stream, Q4_GEMM_ARGS(YPTR, STRIDE)); \

@@ -37,6 +37,9 @@ struct Layout {
     // nonzero scale times 2^f16_p lies in [2^-14, 2^13))
     bool f16 = false;
     int f16_p = 0;
+    // the GEMM may plan its pre-pass forms (fp16, one-pass 8-bit); cleared to pin the
+    // bf16 form
+    bool prepass_forms = true;
     size_t rec_bytes() const { return (size_t)nb * gp * kRecBytes; }
 };
 
@@ -140,8 +143,9 @@ struct GemmPlan {
     size_t xaug_bytes = 0;   // group sums of x (256-row tiles)
     size_t part_bytes = 0;   // splits x M x N fp32 partial sums (0 when unsplit)
     bool f16 = false;        // fp16 form (256-row tiles of a handle whose scales allow it)
-    size_t x16_bytes = 0;    // fp16 form: x scaled per row, as fp16 [M, kx]
-    size_t rowexp_bytes = 0; // fp16 form: each row's power of two
+    bool q8 = false;         // one-pass 8-bit (128-row tiles of a two-plane handle)
+    size_t x16_bytes = 0;    // fp16 and one-pass 8-bit forms: x scaled per row, as fp16 [M, kx]
+    size_t rowexp_bytes = 0; // their rows' powers of two
     size_t total() const { return xaug_bytes + x16_bytes + rowexp_bytes + part_bytes; }
 };
 constexpr int kMaxSplits = 16;

@@ -29,7 +29,7 @@ constexpr uint64_t kLoraMagic = 0x47454d344c4f5241ULL;  // "GEM4LORA"
 thread_local char g_last_error[512] = "";
 // forward path choice: 0 = automatic (q4::use_decode), r > 0 = the GEMM from r rows on
 std::atomic<uint32_t> g_gemm_min_rows{0};
-// GEMM form: 0 the fp16 form wherever a handle's scales allow it, 1 the bf16 form only
+// GEMM form: 0 the pre-pass forms where the plan takes them, 1 the bf16 form only
 std::atomic<uint32_t> g_gemm_form{0};
 
 // Records the message (truncated to the buffer) and returns status.  The const char*
@@ -372,11 +372,11 @@ void release(Gemma4QLinear* h) {
 
 bool valid_handle(const Gemma4QLinear* h) { return h != nullptr && h->magic == kQLinearMagic; }
 
-// The layout the GEMM plans with: the handle's, without the fp16 form when the process
-// pins the bf16 form.
+// The layout the GEMM plans with: the handle's, without the pre-pass forms (fp16,
+// one-pass 8-bit) when the process pins the bf16 form.
 q4::Layout gemm_layout(const Gemma4QLinear* h) {
     q4::Layout l = h->layout;
-    if (g_gemm_form.load(std::memory_order_relaxed) != 0) l.f16 = false;
+    if (g_gemm_form.load(std::memory_order_relaxed) != 0) l.prepass_forms = false;
     return l;
 }
 

@@ -145,10 +145,13 @@ uint32_t gemma4_qmm_set_decode_kernel(uint32_t variant);
 
 /* GEMM (prefill) form of the forward calls in this process.  No counterpart in the
  * reference; for tests and benchmarks that compare the two.
- *   0 (the default): the fp16 form for 256-row tiles of handles whose scales allow it
- *      (every nonzero scale within 2^26 of the largest, none inf or NaN): x scaled per
- *      row by a power of two into fp16 and the weights expanded as s 2^p (q - 8),
- *      exact fp16 products with no per-group scale step; the bf16 form elsewhere.
+ *   0 (the default): the plan may take the pre-pass forms, which scale x per row by
+ *      a power of two into fp16: the fp16 form for 256-row tiles of handles whose
+ *      scales allow it (every nonzero scale within 2^26 of the largest, none inf or
+ *      NaN; weights expanded as s 2^p (q - 8), exact fp16 products with no per-group
+ *      scale step), and for 8-bit handles the one-pass form (weights as 1024 + q from
+ *      both planes, one pass over K instead of two 4-bit planes over 2K); the bf16
+ *      form elsewhere.
  *   1: the bf16 form only (x as given, weights as 1 + q/16, scaled per group).
  * Both meet the same accuracy contract and sum in different orders.  Values above 1
  * are taken as 0.  Returns the previous setting; takes effect for calls issued after

@@ -81,15 +81,18 @@ def xprime_offset(c, k, kx):
     return (row * (kx // 8) + np.where(cr >= kx // 8, cr - kx // 8, cr)) * 16
 
 
-def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
-    """kx: the row length of x (k, or k / 2 for a two-plane 8-bit handle)."""
+def audit_gemm(m, n, k, BM, splits, BN=256, kx=None, q8=False):
+    """kx: the row length of x (k, or k / 2 for a two-plane 8-bit handle).  q8: a
+    two-plane handle in one pass (FORM 2): groups of K, the high plane's pair p and the
+    low plane's pair G / 2 + p of each row block's records in one weight slot."""
     kx = kx or k
     L = layout(n, k)
+    assert not q8 or (k == 2 * kx and (L["g"] // 2) % 2 == 0)
     WAVES = BN // 32   # side by side along N, each all BM rows x 32 columns
     RB = BN // 16
     MT = BM // 16                 # 16-row tiles per wave
     XP = BM * 8 // (64 * WAVES)   # x DMA parts per wave per group
-    XIN = BM < 256                # X_g summed in the kernel, else DMA'd from the pre-pass
+    XIN = BM < 256 and not q8     # X_g summed in the kernel, else DMA'd from the pre-pass
     XT = (MT + WAVES - 1) // WAVES if XIN else 0  # row tiles whose X_g a wave sums: wave + WAVES t
     XA = 0 if XIN else MT // WAVES  # bias A-operand DMA parts per wave per octet
     SW = RB // 8                  # waves loading a pair's scale words
@@ -100,10 +103,12 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
     TILES = MT * 2
     TW = 9 if TILES >= 12 else 5
     assert 2 * XP - 1 < TILES and TW + 2 < TILES, (BM, TILES, TW)
-    KWP, KSP = RB * 64, RB * 16 // 2  # uint4 units of one weight slot
+    KWP, KSP = RB * 64, RB * 16 // 2  # uint4 units of one plane's words, and of the scale words
+    KWS = 2 * KWP if q8 else KWP      # a slot's words
     XAA = BM // 16 * 64               # uint4 units of the bias A operands
     BIAS_SLOT = XAA + RB * 4 * 16 // 2  # uint4 units: A operands, then the octet's scale/bias words
-    G = L["g"]
+    G = L["g"] // 2 if q8 else L["g"]
+    lo_pairs = G // 2 if q8 else 0
     octets = (G + 7) // 8
     mtiles = (m + BM - 1) // BM
     ntiles = (n + BN - 1) // BN
@@ -144,7 +149,8 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
             for part in range(2):
                 rb = rbw + 2 * wave + part
                 wv = np.where(rb < nblocks, rb * L["gp"] * REC + lane * 16, OOB)
-                for p in (0, L["gp"] - 1):
+                pairs = (0, G // 2 - 1, lo_pairs, lo_pairs + G // 2 - 1) if q8 else (0, L["gp"] - 1)
+                for p in pairs:
                     off = np.where(wv == OOB, OOB, wv + p * REC)
                     chk_buf("gemm w", off, 16, L["rec_bytes"], L["rec_bytes"])
                     assert in_tile_part(off[off != OOB], 16)
@@ -163,7 +169,7 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
                     chk_buf("gemm xa", off, 16, ws_bytes, ws_bytes)
                 rb = rbw + 2 * wave + (lane >> 5)
                 chunk = lane & 31
-                ok = (rb < nblocks) & (4 * o + (chunk >> 3) < L["gp"])
+                ok = (rb < nblocks) & (4 * o + (chunk >> 3) < (lo_pairs if q8 else L["gp"]))
                 raw = (rb * L["gp"] + 4 * o + (chunk >> 3)) * REC + (chunk & 7) * 16
                 chk_buf("gemm bias words", np.where(ok, raw, OOB), 16, L["sb_bytes"], L["sb_bytes"])
                 assert in_sb_part(raw[ok], 16)
@@ -173,6 +179,7 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
             for j in range(2):  # the wave's two row blocks
                 rbl = wave * 2 + j
                 assert rbl * 64 + 64 <= KWP and ((rbl * 16 + l16) < KSP * 2).all()
+                assert KWP + rbl * 64 + 64 <= KWS or not q8  # the low plane's words
                 assert ((((wave * 2 + j) * 4 + kq) * 16 + l16) < RB * 4 * 16).all()  # bias words, uint2
             for i in range(MT):  # the product stream's and the X_g sums' x fragments
                 r = 16 * i + l16
@@ -196,7 +203,7 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None):
         ge = min(G, gb + g_split)
         assert gb < ge and gb % 8 == 0
     # LDS: three x slots, two weight slots, the bias slot; two 128 x 128 workgroups per CU
-    lds = 3 * BM * 8 * 16 + 2 * (KWP + KSP) * 16 + BIAS_SLOT * 16
+    lds = 3 * BM * 8 * 16 + 2 * (KWS + KSP) * 16 + BIAS_SLOT * 16
     assert lds <= (LDS_BYTES if BN == 256 else LDS_BYTES // 2)
 
 
@@ -223,6 +230,17 @@ def test_gemm_accesses_two_plane(m, n, k, bm, bn):
         per = (octets + s - 1) // s
         if (octets + per - 1) // per == s:
             audit_gemm(m, n, 2 * k, bm, s, bn, kx=k)
+
+
+# two-plane 8-bit handles in one pass (128-row tiles): groups of K, both planes' words
+@pytest.mark.parametrize("m,n,k", [(2048, 15360, 3840), (300, 130, 1152), (33, 48, 256), (64, 96, 3840),
+                                   (2048, 3840, 15360)])
+def test_gemm_accesses_one_pass_eight_bit(m, n, k):
+    octets = (k // 64 + 7) // 8
+    for s in sorted({1, 2, min(8, octets), octets}):
+        per = (octets + s - 1) // s
+        if (octets + per - 1) // per == s:
+            audit_gemm(m, n, 2 * k, 128, s, 256, kx=k, q8=True)
 
 
 # ----------------------------------------------------------------------- decode

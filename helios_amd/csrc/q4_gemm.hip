@@ -429,7 +429,11 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     constexpr bool F16 = FORM == 1;
     constexpr bool kQ8 = FORM == 2;
     static_assert(!F16 || BM == 256, "the fp16 form takes its group sums from the pre-pass");
-    static_assert(!kQ8 || BM == 128, "one-pass 8-bit: two planes' words per pair fit LDS beside 128-row x tiles");
+    static_assert(!kQ8 || BM >= 128, "one-pass 8-bit: 128- and 256-row tiles");
+    // x ring slots: three (a group's x loaded two steps ahead), or two (one step ahead)
+    // where two planes' words per weight slot leave no room for a third 32 KiB slot
+    // (one-pass 8-bit at 256 rows: 156 KiB against 188)
+    constexpr int kXSlots = (kQ8 && BM == 256) ? 2 : 3;
     constexpr int kWaves = BN / kWN;              // side by side along N
     constexpr int kRB = BN / 16;                  // 16-row weight blocks per workgroup tile
     constexpr int kXChunks = BM * 8;              // 16-byte chunks of one x group tile (BM rows x 64 bf16)
@@ -454,7 +458,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
                   "every wave loads x; every row tile's X_g is summed or loaded");
     __shared__ uint4 g_xs0[kXChunks];             // x group tiles (BM rows x 64: 16 or 32 KiB)
     __shared__ uint4 g_xs1[kXChunks];
-    __shared__ uint4 g_xs2[kXChunks];
+    __shared__ uint4 g_xs2[kXSlots == 3 ? kXChunks : 1];
     __shared__ uint4 g_wp0[kWS + kSPair];         // a pair's weights: 9 or 18 KiB (34 for FORM 2)
     __shared__ uint4 g_wp1[kWS + kSPair];
     // one octet's bias operands: A side for the tile's rows [m16][lane] (written by the
@@ -717,7 +721,9 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     // follows the last read of the previous octet's); (4) multiply, with the loads for
     // group g+2 (and pair (g+2)/2) spread through the products, and keep the lane's
     // X_g.  Every step issues the same loads (past the end they read zeros), so the
-    // counts are fixed.
+    // counts are fixed.  With a two-slot x ring the x of g comes from step g-1 (issued
+    // in its product stream before the pair's words), so (1) leaves only step g-1's
+    // pair words in flight, and (4) loads the x of g+1.
     auto issues_xa = [&](int g) { return (g & 7) == 1 && g > g_begin + 1; };
     auto issued = [&](int g) {  // loads this wave issues at step g
         return kXParts + ((g & 1) == 0 ? (kQ8 ? 4 : 2) + (wave < kSWaves ? 1 : 0) : 0) +
@@ -738,7 +744,11 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         if (g == g_begin) {
             wait_vm_lds<0>();
         } else {
-            switch (issued(g - 1)) {
+            // three slots: the loads of step g - 1 may stay in flight; two: only those it
+            // issued after its x loads (the next pair's words, after product tile kTW)
+            const int pending = kXSlots == 3 ? issued(g - 1) : ((g - 1) & 1) == 0 ? (kQ8 ? 4 : 2) : 0;
+            switch (pending) {
+                case 0: wait_vm_lds<0>(); break;
                 case 1: wait_vm_lds<1>(); break;
                 case 2: wait_vm_lds<2>(); break;
                 case 3: wait_vm_lds<3>(); break;
@@ -761,7 +771,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
         if ((g & 1) == 0 && wave < kSWaves) dma_s((g + 2) >> 1, wp2);
         const bool pair = (g & 1) == 0;
         compute(xs, wp, g & 1, [&](int t) {
-            if ((t & 1) && (t >> 1) < kXParts) dma_x(g + 2, t >> 1, xs2);
+            if ((t & 1) && (t >> 1) < kXParts) dma_x(g + kXSlots - 1, t >> 1, xs2);
             // the pair's two weight loads after tiles kTW and kTW + 2 (inside the stream
             // of kMT x kNT tiles: 8 of them for 64-row tiles)
             if (pair && (t == kTW || t == kTW + 2)) dma_w((g + 2) >> 1, (t - kTW) >> 1, wp2);
@@ -777,7 +787,7 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
 #pragma unroll
     for (int part = 0; part < kXParts; ++part) {
         dma_x(g_begin, part, g_xs0);
-        dma_x(g_begin + 1, part, g_xs1);
+        if constexpr (kXSlots == 3) dma_x(g_begin + 1, part, g_xs1);
     }
     dma_w(g_begin >> 1, 0, g_wp0);
     dma_w(g_begin >> 1, 1, g_wp0);
@@ -786,19 +796,39 @@ __global__ __launch_bounds__(BN * 2) void gemm_kernel(const uint4* __restrict__ 
     wait_vm<0>();
 
     // twelve steps per iteration: the x ring turns every 3 groups, the pair ring every 4
-    for (int g = g_begin; g < g_end; g += 12) {
-        step(g, g_xs0, g_wp0, g_xs2, g_wp1);
-        if (g + 1 < g_end) step(g + 1, g_xs1, g_wp0, g_xs0, g_wp1);
-        if (g + 2 < g_end) step(g + 2, g_xs2, g_wp1, g_xs1, g_wp0);
-        if (g + 3 < g_end) step(g + 3, g_xs0, g_wp1, g_xs2, g_wp0);
-        if (g + 4 < g_end) step(g + 4, g_xs1, g_wp0, g_xs0, g_wp1);
-        if (g + 5 < g_end) step(g + 5, g_xs2, g_wp0, g_xs1, g_wp1);
-        if (g + 6 < g_end) step(g + 6, g_xs0, g_wp1, g_xs2, g_wp0);
-        if (g + 7 < g_end) step(g + 7, g_xs1, g_wp1, g_xs0, g_wp0);
-        if (g + 8 < g_end) step(g + 8, g_xs2, g_wp0, g_xs1, g_wp1);
-        if (g + 9 < g_end) step(g + 9, g_xs0, g_wp0, g_xs2, g_wp1);
-        if (g + 10 < g_end) step(g + 10, g_xs1, g_wp1, g_xs0, g_wp0);
-        if (g + 11 < g_end) step(g + 11, g_xs2, g_wp1, g_xs1, g_wp0);
+    if constexpr (kXSlots == 2) {
+        // the x ring turns every 2 groups, the pair ring every 4; twelve steps per
+        // iteration as below (a four-step body spilled: 256 VGPRs and scratch, against
+        // 200 with twelve)
+        for (int g = g_begin; g < g_end; g += 12) {
+            step(g, g_xs0, g_wp0, g_xs1, g_wp1);
+            if (g + 1 < g_end) step(g + 1, g_xs1, g_wp0, g_xs0, g_wp1);
+            if (g + 2 < g_end) step(g + 2, g_xs0, g_wp1, g_xs1, g_wp0);
+            if (g + 3 < g_end) step(g + 3, g_xs1, g_wp1, g_xs0, g_wp0);
+            if (g + 4 < g_end) step(g + 4, g_xs0, g_wp0, g_xs1, g_wp1);
+            if (g + 5 < g_end) step(g + 5, g_xs1, g_wp0, g_xs0, g_wp1);
+            if (g + 6 < g_end) step(g + 6, g_xs0, g_wp1, g_xs1, g_wp0);
+            if (g + 7 < g_end) step(g + 7, g_xs1, g_wp1, g_xs0, g_wp0);
+            if (g + 8 < g_end) step(g + 8, g_xs0, g_wp0, g_xs1, g_wp1);
+            if (g + 9 < g_end) step(g + 9, g_xs1, g_wp0, g_xs0, g_wp1);
+            if (g + 10 < g_end) step(g + 10, g_xs0, g_wp1, g_xs1, g_wp0);
+            if (g + 11 < g_end) step(g + 11, g_xs1, g_wp1, g_xs0, g_wp0);
+        }
+    } else {
+        for (int g = g_begin; g < g_end; g += 12) {
+            step(g, g_xs0, g_wp0, g_xs2, g_wp1);
+            if (g + 1 < g_end) step(g + 1, g_xs1, g_wp0, g_xs0, g_wp1);
+            if (g + 2 < g_end) step(g + 2, g_xs2, g_wp1, g_xs1, g_wp0);
+            if (g + 3 < g_end) step(g + 3, g_xs0, g_wp1, g_xs2, g_wp0);
+            if (g + 4 < g_end) step(g + 4, g_xs1, g_wp0, g_xs0, g_wp1);
+            if (g + 5 < g_end) step(g + 5, g_xs2, g_wp0, g_xs1, g_wp1);
+            if (g + 6 < g_end) step(g + 6, g_xs0, g_wp1, g_xs2, g_wp0);
+            if (g + 7 < g_end) step(g + 7, g_xs1, g_wp1, g_xs0, g_wp0);
+            if (g + 8 < g_end) step(g + 8, g_xs2, g_wp0, g_xs1, g_wp1);
+            if (g + 9 < g_end) step(g + 9, g_xs0, g_wp0, g_xs2, g_wp1);
+            if (g + 10 < g_end) step(g + 10, g_xs1, g_wp1, g_xs0, g_wp0);
+            if (g + 11 < g_end) step(g + 11, g_xs2, g_wp1, g_xs1, g_wp0);
+        }
     }
     // the last octet's bias term.  Its scale/bias words were loaded at step 8o + 1,
     // except for a last octet of one group (no such step): then they are loaded here;
@@ -1034,9 +1064,9 @@ constexpr double kPrePassUs = 3.0;             // the 256-row tile's group-sum p
 // time per byte of x16 (12.3 us against the group-sum pre-pass's 5.0 for 15.7 MB)
 constexpr double kF16StepScale = 0.965;
 constexpr double kPrepBytesPerUs = 2.15e6;
-// one-pass 8-bit (128-row tiles): its group step (over K, not 2K) against the 4-bit
-// 128-row tile's (8-bit gate 15360x3840 at 2048 rows: 325 us with the pre-pass, 240
-// steps per CU)
+// one-pass 8-bit: its group step (over K, not 2K) against the 4-bit tile's of the
+// same height (8-bit gate 15360x3840 at 2048 rows with the pre-pass: 262 us on 256-row
+// tiles, 120 steps per CU: 1.16; 325 on 128-row tiles, 240 steps: 1.19)
 constexpr double kQ8StepScale = 1.2;
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 }  // namespace
@@ -1078,9 +1108,9 @@ GemmPlan plan_gemm(int m, const Layout& l, size_t max_workspace) {
         const int bm = ts.bm, bn = ts.bn;
         const long tiles = (long)((m + bm - 1) / bm) * ((l.n + bn - 1) / bn);
         // form 0: the bf16 form; 1: the fp16 form (256-row tiles of handles whose scales
-        // allow it); 2: one-pass 8-bit (128-row tiles)
+        // allow it); 2: one-pass 8-bit (128- and 256-row tiles)
         for (int form = 2; form >= 0; --form) {
-            if ((form == 1 && !(bm == 256 && l.f16 && l.prepass_forms)) || (form == 2 && !(bm == 128 && q8_ok)))
+            if ((form == 1 && !(bm == 256 && l.f16 && l.prepass_forms)) || (form == 2 && !(bm >= 128 && q8_ok)))
                 continue;
             const bool pre = form != 0;
             const int groups = form == 2 ? l.g / 2 : l.g;
@@ -1192,6 +1222,9 @@ hipError_t launch_gemm(const uint4* tiles, const uint2* sb, const uint16_t* x, v
                                Q4_GEMM_ARGS(YPTR, STRIDE));                                                      \
         else if (plan.bm == 128 && plan.q8)                                                                      \
             hipLaunchKernelGGL((gemm_kernel<MODE, 128, 256, 2>), grid, block, 0, stream,                         \
+                               Q4_GEMM_ARGS(YPTR, STRIDE));                                                      \
+        else if (plan.bm == 256 && plan.q8)                                                                      \
+            hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256, 2>), grid, block, 0, stream,                         \
                                Q4_GEMM_ARGS(YPTR, STRIDE));                                                      \
         else if (plan.bm == 256)                                                                                 \
             hipLaunchKernelGGL((gemm_kernel<MODE, 256, 256>), grid, block, 0, stream, Q4_GEMM_ARGS(YPTR, STRIDE)); \

@@ -202,8 +202,10 @@ def audit_gemm(m, n, k, BM, splits, BN=256, kx=None, q8=False):
         gb = sp * g_split
         ge = min(G, gb + g_split)
         assert gb < ge and gb % 8 == 0
-    # LDS: three x slots, two weight slots, the bias slot; two 128 x 128 workgroups per CU
-    lds = 3 * BM * 8 * 16 + 2 * (KWS + KSP) * 16 + BIAS_SLOT * 16
+    # LDS: three x slots (two for one-pass 8-bit at 256 rows), two weight slots, the bias
+    # slot; two 128 x 128 workgroups per CU
+    xslots = 2 if (q8 and BM == 256) else 3
+    lds = xslots * BM * 8 * 16 + 2 * (KWS + KSP) * 16 + BIAS_SLOT * 16
     assert lds <= (LDS_BYTES if BN == 256 else LDS_BYTES // 2)
 
 
@@ -232,15 +234,17 @@ def test_gemm_accesses_two_plane(m, n, k, bm, bn):
             audit_gemm(m, n, 2 * k, bm, s, bn, kx=k)
 
 
-# two-plane 8-bit handles in one pass (128-row tiles): groups of K, both planes' words
+# two-plane 8-bit handles in one pass (128- and 256-row tiles): groups of K, both
+# planes' words
 @pytest.mark.parametrize("m,n,k", [(2048, 15360, 3840), (300, 130, 1152), (33, 48, 256), (64, 96, 3840),
                                    (2048, 3840, 15360)])
-def test_gemm_accesses_one_pass_eight_bit(m, n, k):
+@pytest.mark.parametrize("bm", [128, 256])
+def test_gemm_accesses_one_pass_eight_bit(m, n, k, bm):
     octets = (k // 64 + 7) // 8
     for s in sorted({1, 2, min(8, octets), octets}):
         per = (octets + s - 1) // s
         if (octets + per - 1) // per == s:
-            audit_gemm(m, n, 2 * k, 128, s, 256, kx=k, q8=True)
+            audit_gemm(m, n, 2 * k, bm, s, 256, kx=k, q8=True)
 
 
 # ----------------------------------------------------------------------- decode

@@ -2,8 +2,8 @@
 bf16 form.
 
 An 8-bit handle is stored as two 4-bit planes over K' = 2K (q >> 4 with scale 16 s and
-bias b, q & 15 with scale s).  The one-pass form (128-row tiles, an even number of
-groups per plane) reads both planes' words of each group and expands 1024 + q in fp16
+bias b, q & 15 with scale s).  The one-pass form (128- and 256-row tiles, an even number
+of groups per plane) reads both planes' words of each group and expands 1024 + q in fp16
 (exact), against x scaled per row into fp16 by the pre-pass: one pass over K with the
 bf16 form's per-group scale step, instead of two 4-bit passes over 2K.
 gemma4_qmm_set_gemm_form(1) pins the two-plane bf16 form, so both run on the same

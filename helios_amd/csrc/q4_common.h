@@ -162,6 +162,34 @@ __device__ __forceinline__ uint32_t word_nibble(uint32_t u, int i) {
     return (i & 1) ? ((r >> 19) & 0xFu) : ((r >> 3) & 0xFu);
 }
 
+// Reductions over the eight lanes of an aligned octet (lanes 8i..8i+7) by DPP lane moves
+// inside the wave, with no trip through the LDS crossbar (ds_bpermute, which is what
+// __shfl_xor becomes): partners at distance 1 and 2 (quad permutes), then the other quad
+// (row_half_mirror pairs lane j of the octet with lane 7 - j, which by then holds that
+// quad's value).  Every lane ends with the result; the adds are those of the xor 1, 2, 4
+// butterfly, in the same order, so the sums are the same bits.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppSwap1 = 0xB1;       // quad_perm [1, 0, 3, 2]
+constexpr int kDppSwap2 = 0x4E;       // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+__device__ __forceinline__ uint32_t octet_max(uint32_t v) {
+    uint32_t o = dpp_mov<kDppSwap1>(v);
+    v = v > o ? v : o;
+    o = dpp_mov<kDppSwap2>(v);
+    v = v > o ? v : o;
+    o = dpp_mov<kDppHalfMirror>(v);
+    return v > o ? v : o;
+}
+__device__ __forceinline__ float octet_sum(float v) {
+    v += __uint_as_float(dpp_mov<kDppSwap1>(__float_as_uint(v)));
+    v += __uint_as_float(dpp_mov<kDppSwap2>(__float_as_uint(v)));
+    v += __uint_as_float(dpp_mov<kDppHalfMirror>(__float_as_uint(v)));
+    return v;
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
 

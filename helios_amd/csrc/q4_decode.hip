@@ -290,9 +290,7 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
                 float sum = 0.f;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) sum += bf16_lo(w4[j]) + bf16_hi(w4[j]);
-                sum += __shfl_xor(sum, 1);
-                sum += __shfl_xor(sum, 2);
-                sum += __shfl_xor(sum, 4);
+                sum = octet_sum(sum);
                 if (c < xchunks && (lane & 7) == 0) negx[(cr >> 3) * 16 + row] = -sum;
             }
         };
@@ -463,9 +461,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(
                 float sum = 0.f;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) sum += bf16_lo(w4[j]) + bf16_hi(w4[j]);
-                sum += __shfl_xor(sum, 1);
-                sum += __shfl_xor(sum, 2);
-                sum += __shfl_xor(sum, 4);
+                sum = octet_sum(sum);
                 if (c < xchunks && (lane & 7) == 0) xtab[(cr >> 3) * 16 + row] = -sum;
             }
         };

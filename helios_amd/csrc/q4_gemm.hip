@@ -113,9 +113,7 @@ __global__ __launch_bounds__(512) void xaug_kernel(const uint16_t* __restrict__ 
         const int p = (t >> 3) + 64 * r;
         float sum = ((bf16_lo(v[r].x) + bf16_hi(v[r].x)) + (bf16_lo(v[r].y) + bf16_hi(v[r].y))) +
                     ((bf16_lo(v[r].z) + bf16_hi(v[r].z)) + (bf16_lo(v[r].w) + bf16_hi(v[r].w)));
-        sum += __shfl_xor(sum, 1);
-        sum += __shfl_xor(sum, 2);
-        sum += __shfl_xor(sum, 4);
+        sum = octet_sum(sum);
         if (c == 0) gsum[p >> 4][p & 15] = sum;
     }
     __syncthreads();
@@ -209,9 +207,7 @@ __global__ __launch_bounds__(64 * kPrepRows) void xprep_kernel(const uint16_t* _
                 sum += (float)hi;
                 o[j] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
             }
-            sum += __shfl_xor(sum, 1);
-            sum += __shfl_xor(sum, 2);
-            sum += __shfl_xor(sum, 4);
+            sum = octet_sum(sum);
             if (u < units) {
                 yr[u] = make_uint4(o[0], o[1], o[2], o[3]);
                 if ((u & 7) == 0) gsum[u >> 3] = sum;

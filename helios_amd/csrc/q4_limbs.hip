@@ -149,11 +149,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_kernel(const uint4* __
             mb = mb > lo ? mb : lo;
             mb = mb > hi ? mb : hi;
         }
-#pragma unroll
-        for (int d = 1; d < 8; d <<= 1) {
-            const uint32_t o = (uint32_t)__shfl_xor((int)mb, d);
-            mb = mb > o ? mb : o;
-        }
+        mb = octet_max(mb);
         const int ex = (int)(mb >> 7);  // biased exponent of the group maximum
         const int e = ex < 19 ? 19 : ex > 254 ? 254 : ex;
         const float scale = __uint_as_float((uint32_t)(273 - e) << 23);   // 2^(146 - e)
@@ -173,8 +169,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_kernel(const uint4* __
             l1[i] = bits >> 7;                                          // (V >> 7) & 127 after the mask
             l0[i] = (uint32_t)__builtin_amdgcn_sbfe((int)bits, 14, 8);  // V >> 14
         }
-#pragma unroll
-        for (int d = 1; d < 8; d <<= 1) sum += __shfl_xor(sum, d);
+        sum = octet_sum(sum);
         // slot order within a half: nibbles (0, 4, 1, 5), (2, 6, 3, 7)
         const uint2 p0 = make_uint2(pack_bytes(l0[0], l0[4], l0[1], l0[5]), pack_bytes(l0[2], l0[6], l0[3], l0[7]));
         const uint2 p1 = make_uint2(pack_bytes(l1[0], l1[4], l1[1], l1[5]) & 0x7F7F7F7Fu,
@@ -393,11 +388,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint
             mb = mb > lo ? mb : lo;
             mb = mb > hi ? mb : hi;
         }
-#pragma unroll
-        for (int d = 1; d < 8; d <<= 1) {
-            const uint32_t o = (uint32_t)__shfl_xor((int)mb, d);
-            mb = mb > o ? mb : o;
-        }
+        mb = octet_max(mb);
         const int ex = (int)(mb >> 7);
         const int e = ex < 19 ? 19 : ex > 254 ? 254 : ex;
         const float scale = __uint_as_float((uint32_t)(273 - e) << 23);  // 2^(146 - e)
@@ -413,8 +404,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint
             l1[i] = bits >> 7;
             l0[i] = (uint32_t)__builtin_amdgcn_sbfe((int)bits, 14, 8);
         }
-#pragma unroll
-        for (int d = 1; d < 8; d <<= 1) sum += __shfl_xor(sum, d);
+        sum = octet_sum(sum);
         const uint2 p0 = make_uint2(pack_bytes(l0[0], l0[4], l0[1], l0[5]), pack_bytes(l0[2], l0[6], l0[3], l0[7]));
         const uint2 p1 = make_uint2(pack_bytes(l1[0], l1[4], l1[1], l1[5]) & 0x7F7F7F7Fu,
                                     pack_bytes(l1[2], l1[6], l1[3], l1[7]) & 0x7F7F7F7Fu);

@@ -195,7 +195,8 @@ Gemma4Status gemma4_qlinear_forward(const Gemma4QLinear* linear, void* stream, c
 
 /* Scratch bytes gemma4_qlinear_forward (or gemma4_qgeglu_forward, for a pair) takes
  * for `rows` rows under the current path choice: 0 on the decode path, else the GEMM
- * plan's group sums and split-K partial sums.  No counterpart in the reference.  When
+ * plan's group sums, its pre-pass forms' fp16 copy of x and row exponents, and its
+ * split-K partial sums.  No counterpart in the reference.  When
  * it is at most 64 MiB, gemma4_qlinear_forward_noalloc runs the same plan, so the two
  * calls give identical bits. */
 Gemma4Status gemma4_qlinear_scratch_bytes(const Gemma4QLinear* linear, uint32_t rows, uint64_t* out);
@@ -208,11 +209,13 @@ Gemma4Status gemma4_qlinear_scratch_bytes(const Gemma4QLinear* linear, uint32_t 
  * It calls no hipMalloc, hipFree or allocating library routine.  Scratch needs:
  * none on the decode path (gemma4_qmm_set_gemm_min_rows); on the GEMM path the
  * 256-row tile's table of x's group sums (1 KiB per 16 rows, rounded up to 256, and
- * per 512 columns of K) and split-K partial
- * sums, only as far as the array has room (a cheaper tile or fewer splits than
- * gemma4_qlinear_forward may choose, so the fp32 summation order, and with it the
- * last bits of some outputs, can differ from that call's; unsplit plans on the 64-
- * and 128-row tiles need none), so no call is refused for want of scratch.  Every call
+ * per 512 columns of K), the pre-pass forms' fp16 copy of x (2 bytes per element) and
+ * row exponents (4 bytes per row), and split-K partial
+ * sums, only as far as the array has room (a cheaper tile, another form or fewer
+ * splits than gemma4_qlinear_forward may choose, so the fp32 summation order, and with
+ * it the last bits of some outputs, can differ from that call's; unsplit bf16-form
+ * plans on the 64- and 128-row tiles need none), so no call is refused for want of
+ * scratch.  Every call
  * on a GPU shares that GPU's array: calls that overlap in time on one GPU (other
  * streams, other threads) race and must be serialized by the caller. */
 Gemma4Status gemma4_qlinear_forward_noalloc(const Gemma4QLinear* linear, void* stream, const uint16_t* x_dev,

@@ -336,10 +336,12 @@ def summarize_profiles(stats_dir: str, fetch_dir: str, write_dir: str, line_file
     def short(name: str) -> str:
         return name.replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0][:90]
 
-    def per_dispatch(rows, counter, match):
+    def per_dispatch(rows, counter, match, largest=False):
         vals = [float(r["Counter_Value"]) for r in rows if r["Counter_Name"] == counter and match(r["Kernel_Name"])]
         if not vals:
             raise SystemExit(f"no {counter} rows for the kernel")
+        if largest:  # the 1 GiB copies, not the runtime's small blits (handle creation's)
+            vals = [v for v in vals if v >= 0.5 * max(vals)]
         return sum(vals) / len(vals), len(vals)
 
     is_dom = lambda n: DOM_KERNEL in n  # noqa: E731
@@ -349,9 +351,9 @@ def summarize_profiles(stats_dir: str, fetch_dir: str, write_dir: str, line_file
     fetch_rows = _csv_rows(fetch_dir, "counter_collection.csv")
     write_rows = _csv_rows(write_dir, "counter_collection.csv")
     f_dom, n_fd = per_dispatch(fetch_rows, "FETCH_SIZE", is_dom)
-    f_cpy, n_fc = per_dispatch(fetch_rows, "FETCH_SIZE", is_copy)
+    f_cpy, n_fc = per_dispatch(fetch_rows, "FETCH_SIZE", is_copy, largest=True)
     w_dom, n_wd = per_dispatch(write_rows, "WRITE_SIZE", is_dom)
-    w_cpy, n_wc = per_dispatch(write_rows, "WRITE_SIZE", is_copy)
+    w_cpy, n_wc = per_dispatch(write_rows, "WRITE_SIZE", is_copy, largest=True)
     f_scale = line["copy_bytes"] / (f_cpy * 1024)
     w_scale = line["copy_bytes"] / (w_cpy * 1024)
     # a second, independent calibration of the read counter: the read-only probe
@@ -634,6 +636,8 @@ def summarize_decode(db_path: str, fetch_dir: str, write_dir: str, line_file: st
                     per.append([])
             elif short(n).startswith("decode") and per:
                 per[-1].append(float(r["Counter_Value"]))
+        # the 1 GiB copies, not the runtime's small blits (handle creation's)
+        cpy = [c for c in cpy if c >= 0.5 * max(cpy)] if cpy else cpy
         return [sum(v) / len(v) if v else None for v in per], (sum(cpy) / len(cpy) if cpy else None)
 
     fetch, f_cpy = counter_shapes(fetch_dir, "FETCH_SIZE")

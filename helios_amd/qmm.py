@@ -172,8 +172,8 @@ def release_scratch(stream=None) -> None:
 
 def set_decode_kernel(variant: int) -> int:
     """Pins the decode kernel family for this process: 0 (the default) chooses by
-    shape, 1 the int8 matrix-core kernel for every one-row call it can run, 2 the bf16
-    kernels only.  Returns the previous setting."""
+    shape, 1 the int8 matrix-core kernels for every call of 1-8 rows they can run, 2
+    the bf16 kernels only.  Returns the previous setting."""
     if int(variant) not in (0, 1, 2):
         raise ValueError(f"variant must be 0, 1 or 2, got {variant}")
     return int(load_library().gemma4_qmm_set_decode_kernel(int(variant)))

@@ -135,8 +135,9 @@ uint32_t gemma4_qmm_set_gemm_min_rows(uint32_t rows);
 /* Decode kernel family of the forward calls in this process.  No counterpart in the
  * reference; for tests and benchmarks that pin a kernel.
  *   0 (the default): automatic, chosen per shape.
- *   1: the int8 matrix-core kernel (x split exactly into three int8 limbs per
- *      64-column group) for every one-row call it can run.
+ *   1: the int8 matrix-core kernels (x split exactly into three int8 limbs per
+ *      64-column group) for every call of 1-8 rows they can run (x's limbs and the
+ *      kernel's sums within a CU's LDS).
  *   2: the bf16 matrix-core kernels only.
  * All meet the same accuracy contract and sum in different orders.  Values above 2
  * are taken as 0.  Returns the previous setting; takes effect for calls issued after

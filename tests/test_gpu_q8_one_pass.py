@@ -12,7 +12,8 @@ ulp/2 of the float64 oracle, fp32 within GEMM_REL = 5e-4 RMS, the two forms' fp3
 outputs within GEMM_REL RMS of each other.  Cases: the MLP shapes at 2048 rows, gate at
 512, ragged rows and row blocks, a last octet of two groups, rows of x with extreme
 ranges and an inf; a plane with an odd number of groups (K = 192) stays two-plane;
-graph replays equal eager calls.
+graph replays equal eager calls; twelve seeded random shapes (4 and 8 bits, odd and
+even group counts) on whatever form the plan picks.
 """
 
 import numpy as np
@@ -170,4 +171,39 @@ def test_one_pass_eight_bit_graph_replays(gpu_lib):
             torch.cuda.synchronize()
             assert torch.equal(outs[i], y), f"replay {rep} call {i} differs from eager"
     del g
+    lin.close()
+
+
+def _shapes(seed, count):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        n = int(rng.integers(1000, 20001))
+        k = 64 * int(rng.integers(2, 121))  # 2-120 groups: odd and even plane group counts
+        m = int(rng.integers(256, 2049))
+        bits = int(rng.choice([4, 8]))
+        out.append((n, k, m, bits))
+    return out
+
+
+@pytest.mark.parametrize("n,k,m,bits", _shapes(8600, 12))
+def test_prepass_forms_random_shapes(gpu_lib, n, k, m, bits):
+    """Seeded random shapes (N 1000-20000, K 128-7680, M 256-2048, 4 and 8 bits) on
+    whatever plan the cost model picks (the fp16 form, one-pass 8-bit, or the bf16 form)
+    against the oracle on sampled rows, and against the pinned bf16 form."""
+    import torch
+
+    if bits == 4:
+        rng = np.random.default_rng(n + k)
+        w = A.round_to_bf16((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        tri = C.quantize(w)
+    else:
+        tri = _q8(n, k, seed=n + k)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(*tri), bits=bits)
+    x = A.make_activations(m, k, seed=m + k, outliers=True)
+    rows = np.unique(np.linspace(0, m - 1, 5).astype(np.int64))
+    rt = torch.from_numpy(rows).cuda()
+    want = C.qmm_f64(np.ascontiguousarray(x[rows]), *tri, bits=bits)
+    y1, y2 = _forms(lin, dev_x(x), torch.float32)
+    _check(y1, y2, want, rt, f"{bits}-bit {n}x{k} m={m}")
     lin.close()

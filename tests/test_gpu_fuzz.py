@@ -10,7 +10,8 @@ group pair partly empty).  Sampled rows are checked with the bars of
 test_gpu_parity.py (bf16 max |err| <= 1e-2 RMS + ulp/2, fp32 <= 2e-3 RMS) and, for
 pairs, test_gpu_geglu.py.  LoRA (rank 1-96) and the greedy head (M 1-16, softcap 0
 or 30) get random shapes of their own, with the bars of test_gpu_lora.py and
-test_gpu_greedy.py.
+test_gpu_greedy.py.  The int8 decode kernels, pinned, get random shapes of 1-8 rows
+of their own (every output checked).
 """
 
 import numpy as np
@@ -130,6 +131,60 @@ def test_random_shapes(gpu_lib, case):
         check_geglu(y[rt], g, u, what)
     else:
         assert_close(y[rt], C.qmm_f64(xs, *tri, bits=bits), what)
+
+
+def _limb_cases(count=24, seed=20261206):
+    """The int8 matrix-core decode kernels pinned (gemma4_qmm_set_decode_kernel 1) on
+    random shapes of 1-8 rows: every launch shape of the one-row and the 2-8 row
+    kernels, 4 and 8 bits, pairs, bf16 and fp32; every fourth case wide enough (more
+    than 4096 row blocks) for the phased launch at 3-8 rows."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        m = 1 + i % 8
+        pair = bool(rng.random() < 0.25)
+        bits = 8 if rng.random() < 0.25 else 4
+        f32 = bool(rng.random() < 0.4)
+        if i % 4 == 3:
+            k = 64 * int(rng.integers(1, 9))
+            n = int(rng.integers(65_600, 80_001)) // (2 if pair else 1)
+            bits = 4
+        else:
+            k = 64 * int(rng.integers(1, 129))
+            per_row = k * (2 if bits == 8 else 1) * (2 if pair else 1)
+            n = int(rng.integers(1, max(2, min(6000 if not pair else 3000, MAX_WEIGHTS // per_row)) + 1))
+        cases.append(dict(i=400 + i, n=n, k=k, m=m, pair=pair, bits=bits, f32=f32, outliers=i % 3 != 0))
+    return cases
+
+
+@pytest.mark.parametrize("case", _limb_cases(), ids=lambda c: f"{c['i']}-{'pair' if c['pair'] else 'lin'}{c['bits']}"
+                         f"-N{c['n']}-K{c['k']}-M{c['m']}{'-f32' if c['f32'] else ''}")
+def test_random_shapes_int8_kernels(gpu_lib, case):
+    import torch
+
+    n, k, m, bits = case["n"], case["k"], case["m"], case["bits"]
+    what = f"int8 case {case['i']}: {'pair' if case['pair'] else 'linear'} bits={bits} N={n} K={k} M={m} f32={case['f32']}"
+    print(what, flush=True)
+    x = A.make_activations(m, k, seed=2000 + case["i"], outliers=case["outliers"])
+    dtype = torch.float32 if case["f32"] else torch.bfloat16
+    seed = 66_000 + 10 * case["i"]
+    with gpu_lib.decode_kernel(1):
+        if case["pair"]:
+            gate, up = _triple(n, k, bits, seed), _triple(n, k, bits, seed + 1)
+            obj = gpu_lib.QuantizedGeGLU(dev_triple(*gate), dev_triple(*up), bits=bits)
+        else:
+            tri = _triple(n, k, bits, seed)
+            obj = gpu_lib.QuantizedLinear(*dev_triple(*tri), bits=bits)
+        y = obj.forward(dev_x(x), out_dtype=dtype)
+        torch.cuda.synchronize()
+    obj.close()
+    assert tuple(y.shape) == (m, n) and y.dtype == dtype, what
+    if case["pair"]:
+        g = C.qmm_f64(x, *gate, bits=bits).astype(np.float32)
+        u = C.qmm_f64(x, *up, bits=bits).astype(np.float32)
+        check_geglu(y, g, u, what)
+    else:
+        assert_close(y, C.qmm_f64(x, *tri, bits=bits), what)
 
 
 def _lora_cases(count=12, seed=20261204):

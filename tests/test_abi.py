@@ -110,6 +110,34 @@ def test_geglu_pair_argument_checks(lib):
     assert "invalid handle" in qmm.last_error()
 
 
+def test_process_wide_settings(lib):
+    """gemma4_qmm_set_decode_kernel, _set_gemm_form and _set_gemm_min_rows return the
+    previous setting; a value out of range selects the default (0) and a row count past
+    INT_MAX is clamped to it; the Python mirror rejects out-of-range values instead."""
+    for setter, top in ((lib.gemma4_qmm_set_decode_kernel, 2), (lib.gemma4_qmm_set_gemm_form, 1)):
+        prev = setter(top)
+        try:
+            assert setter(top + 5) == top   # out of range: stored as the default
+            assert setter(1) == 0
+            assert setter(0) == 1
+        finally:
+            setter(prev)
+    prev = lib.gemma4_qmm_set_gemm_min_rows(2 ** 32 - 1)
+    try:
+        assert lib.gemma4_qmm_set_gemm_min_rows(64) == 2 ** 31 - 1
+        assert lib.gemma4_qmm_set_gemm_min_rows(0) == 64
+    finally:
+        lib.gemma4_qmm_set_gemm_min_rows(prev)
+    for fn, bad in ((qmm.set_decode_kernel, 3), (qmm.set_gemm_form, 2), (qmm.set_gemm_min_rows, -1)):
+        with pytest.raises(ValueError):
+            fn(bad)
+    with qmm.decode_kernel(2), qmm.gemm_form(1), qmm.gemm_min_rows(32):
+        assert lib.gemma4_qmm_set_decode_kernel(2) == 2 and lib.gemma4_qmm_set_gemm_form(1) == 1
+        assert lib.gemma4_qmm_set_gemm_min_rows(32) == 32
+    assert lib.gemma4_qmm_set_decode_kernel(0) == 0 and lib.gemma4_qmm_set_gemm_form(0) == 0
+    assert lib.gemma4_qmm_set_gemm_min_rows(0) == 0
+
+
 def test_last_error_is_thread_local(lib):
     out = ctypes.c_void_p()
     assert lib.gemma4_qlinear_create(None, None, None, None, ctypes.byref(out)) != 0

@@ -41,11 +41,12 @@
 // 0-6%).  The kernel is written
 // for tiles of BN = 128 too (four waves, 78 KiB of LDS: two workgroups per CU); a
 // forced-plan sweep over the benchmark's shapes measured it within 6% of the two
-// tiles above where it helped at all, so the plan does not use it.  Everything streams through LDS by direct-to-LDS buffer loads
-// (no staging registers): per 64-wide group the x tile (rows swizzled so the MFMA
+// tiles above where it helped at all, so the plan does not use it.  Everything streams
+// through LDS by direct-to-LDS buffer loads (no staging registers): per 64-wide group the x tile (rows swizzled so the MFMA
 // operand reads are bank-conflict free), the group's weight words and scale words;
-// the bias operands once per 8 groups.  The rings have three slots, so each load has
-// two steps of arithmetic to arrive in.
+// the bias operands once per 8 groups.  The x ring has three slots, so each load has
+// two steps of arithmetic to arrive in (two slots, one step, for the one-pass 8-bit
+// form on 256-row tiles, whose weight slots hold both planes).
 #include <type_traits>
 
 #include "q4_common.h"
@@ -395,7 +396,8 @@ __device__ __forceinline__ void lora_store(const f32x4 (&acc)[kMT][kNT], const L
 
 // LDS rings (declared per instantiation inside the kernel, sized by its tile).
 // x: three slots of one group each (group g in slot g % 3; the loads for g+2 are in
-// flight while g is multiplied).  Weights: two slots of one group pair each (pair p
+// flight while g is multiplied; two slots, g % 2, for the one-pass 8-bit form on
+// 256-row tiles).  Weights: two slots of one group pair each (pair p
 // in slot p % 2, loaded with the x of its first group), holding the tiled words of
 // the workgroup's row blocks [row block][lane] followed by their scale/bias words
 // [row block][row] as uint2.  Every load is a 16-byte-per-lane DMA: 4-byte LDS DMAs

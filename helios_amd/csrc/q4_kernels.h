@@ -129,10 +129,11 @@ hipError_t launch_scale_range(const uint2* sb, const Layout& l, int* out, hipStr
 void set_f16_form(Layout& l, const int range[3]);
 
 // Prefill path: fp32-exact factored GEMM on the matrix cores.  `workspace` holds,
-// for the 256-row tile, the group sums of x (and in the fp16 form x as fp16 and each
-// row's power of two) and, when K is split over workgroups, the fp32 partial sums
-// (device memory, 256-byte aligned); an unsplit plan of 64- or 128-row tiles needs
-// none.  The plan is the cheapest whose workspace fits in
+// for the 256-row tile and the pre-pass forms (fp16 on 256-row tiles, one-pass 8-bit
+// on 128- and 256-row tiles), the group sums of x (and in the pre-pass forms x as
+// fp16 and each row's power of two) and, when K is split over workgroups, the fp32
+// partial sums (device memory, 256-byte aligned); an unsplit bf16-form plan of 64- or
+// 128-row tiles needs none.  The plan is the cheapest whose workspace fits in
 // `workspace_bytes`; gemm_workspace_bytes(m, l) is what the unconstrained plan
 // needs, and with that much the launch runs the unconstrained plan.
 struct GemmPlan {

@@ -208,10 +208,11 @@ Gemma4Status gemma4_qlinear_scratch_bytes(const Gemma4QLinear* linear, uint32_t 
  * 64 MiB device array that the library holds on each GPU it runs on until the
  * process ends.  No counterpart in the reference (its MLX ops allocate per call).
  * It calls no hipMalloc, hipFree or allocating library routine.  Scratch needs:
- * none on the decode path (gemma4_qmm_set_gemm_min_rows); on the GEMM path the
- * 256-row tile's table of x's group sums (1 KiB per 16 rows, rounded up to 256, and
- * per 512 columns of K), the pre-pass forms' fp16 copy of x (2 bytes per element) and
- * row exponents (4 bytes per row), and split-K partial
+ * none on the decode path (gemma4_qmm_set_gemm_min_rows); on the GEMM path the table
+ * of x's group sums that the 256-row tile and the pre-pass forms (fp16, one-pass
+ * 8-bit) read (1 KiB per 16 rows, rounded up to the tile, and per 512 columns of K),
+ * the pre-pass forms' fp16 copy of x (2 bytes per element) and row exponents (4 bytes
+ * per row), and split-K partial
  * sums, only as far as the array has room (a cheaper tile, another form or fewer
  * splits than gemma4_qlinear_forward may choose, so the fp32 summation order, and with
  * it the last bits of some outputs, can differ from that call's; unsplit bf16-form

@@ -242,7 +242,7 @@ __global__ __launch_bounds__(64 * kPrepRows) void xprep_kernel(const uint16_t* _
 // Scale range of a handle: thread per (record, row), one atomic per wave.
 __global__ void scale_range_kernel(const uint2* __restrict__ sb, long records, int* __restrict__ out) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    int emax = 0, emin = 255, bad = 0;
+    int emax = -1, emin = 255, bad = 0;  // (a subnormal scale counts as exponent 0)
     if (i < records * 16) {
         const uint2 w = sb[(i >> 4) * kRecU2 + (i & 15)];
         const uint32_t mags[2] = {w.x & 0x7FFFu, w.y & 0x7FFFu};
@@ -1073,12 +1073,13 @@ void set_f16_form(Layout& l, const int range[3]) {
     l.f16 = false;
     l.f16_p = 0;
     if (range[2] != 0 || l.kx / 64 > kPrepMaxGroups) return;
-    if (range[0] == 0) {  // every scale zero
+    if (range[0] < 0) {  // every scale zero
         l.f16 = true;
         return;
     }
     // the largest scale times 2^p in [2^12, 2^13); the smallest nonzero then >= 2^-14
-    // when the exponents span at most 26
+    // when the exponents span at most 26 (subnormal scales, exponent 0, need p > 64:
+    // those handles keep the bf16 form)
     const int p = 12 - (range[0] - 127);
     if (range[0] - range[1] > 26 || p > 64 || p < -64) return;
     l.f16 = true;

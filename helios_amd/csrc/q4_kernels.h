@@ -122,8 +122,9 @@ hipError_t launch_greedy_reduce(const unsigned long long* part, int nb, int rows
 // many groups.
 constexpr int kPrepMaxGroups = 8192;
 // Scale range of a built handle (the GEMM's fp16 form): out[0] the largest and out[1]
-// the smallest biased exponent of its nonzero scales, out[2] the count of inf or NaN
-// scales.  `out` is device memory the caller sets to {0, 255, 0} first.
+// the smallest biased exponent of its nonzero scales (a subnormal scale counts as 0;
+// out[0] stays -1 when every scale is zero), out[2] the count of inf or NaN scales.
+// `out` is device memory the caller sets to {-1, 255, 0} first.
 hipError_t launch_scale_range(const uint2* sb, const Layout& l, int* out, hipStream_t stream);
 // Sets l.f16 and l.f16_p from those three numbers.
 void set_f16_form(Layout& l, const int range[3]);

@@ -386,7 +386,7 @@ hipError_t scale_form(Gemma4QLinear* h, hipStream_t stream) {
     int* d = nullptr;
     hipError_t e = hipMalloc(&d, 3 * sizeof(int));
     if (e != hipSuccess) return e;
-    const int init[3] = {0, 255, 0};
+    const int init[3] = {-1, 255, 0};
     int range[3] = {0, 0, 1};
     e = hipMemcpyAsync(d, init, sizeof(init), hipMemcpyHostToDevice, stream);
     if (e == hipSuccess) e = q4::launch_scale_range(h->sb, h->layout, d, stream);

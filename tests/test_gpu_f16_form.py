@@ -141,9 +141,16 @@ def test_fp16_form_scale_ranges(gpu_lib):
         "wide": (s.copy(), b, False),
         # one scale inf
         "inf": (s.copy(), b, False),
+        # every scale a bf16 subnormal (exponent field 0) and no biases: the fp16 form
+        # would flush them, so the handle keeps the bf16 form
+        "subnormal": (A.f32_to_bf16_bits(sf * 2.0 ** -123), np.zeros_like(b), False),
+        # every scale zero: the products are the biases' alone, in either form
+        "zero": (np.zeros_like(s), b, True),
     }
     cases["wide"][0][5, 7] = A.f32_to_bf16_bits(np.array([sf[5, 7] * 2.0 ** -40], np.float32))[0]
     cases["inf"][0][9, 3] = 0x7F80
+    sub = cases["subnormal"][0]
+    assert ((sub & 0x7F80) == 0).all() and (sub & 0x7F).any()  # subnormal or zero, some nonzero
     for what, (s2, b2, f16) in cases.items():
         tri = (wq, s2, b2)
         lin = gpu_lib.QuantizedLinear(*dev_triple(*tri))

@@ -127,8 +127,10 @@ __global__ __launch_bounds__(512) void xaug_kernel(const uint16_t* __restrict__ 
 // The fp16 form's pre-pass: one wave per row m of the tiles, four rows per workgroup
 // (rows past M write zero bias operands only):
 //  * k = 142 - e, e the largest biased exponent of the row's finite |x|, so that the
-//    largest |x| 2^k lies in [2^15, 2^16), with 8 significant bits below 65504 (k = 0
-//    for a row of zeros; inf and NaN stay inf and NaN and reach y so);
+//    largest |x| 2^k lies in [2^15, 2^16), with 8 significant bits below 65504 (a row
+//    whose finite values are all bf16 subnormals, e = 0: k = 142, and m 2^-133 2^142
+//    = 512 m < 65504 is exact; k = 0 for a row of zeros; inf and NaN stay inf and NaN
+//    and reach y so);
 //  * x16[m] = fp16(x 2^k), exact for every x within 2^32 of the largest;
 //  * X_g = the fp32 sum of the group's x16 values (in element order, then over the
 //    group's eight 16-byte units in a fixed tree), and the 256-row tile's bias A
@@ -193,7 +195,7 @@ __global__ __launch_bounds__(64 * kPrepRows) void xprep_kernel(const uint16_t* _
             mb = o > mb ? o : mb;
         }
         const int e = (int)(mb >> 7);
-        const int k = e == 0 ? 0 : 142 - e;
+        const int k = mb == 0 ? 0 : 142 - e;
         // x16 of one 16-byte unit and its group's sum (the eight units of a group are
         // eight consecutive lanes; every lane of the wave takes part in the shuffles)
         auto conv = [&](uint4 v, int u) {

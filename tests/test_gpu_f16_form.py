@@ -183,6 +183,7 @@ def test_fp16_form_extreme_rows(gpu_lib):
     xf[2] = 0.0                                               # zeros
     xf[3] = rng.standard_normal(k) * 2.0 ** rng.integers(-40, 41, k)  # spread over 2^-40..2^40
     xf[5, 100] = np.inf                                       # inf: this row's outputs not finite
+    xf[6] = rng.standard_normal(k) * 2.0 ** -130              # bf16 subnormals only (exponent 0)
     x = A.f32_to_bf16_bits(xf.astype(np.float32))
     xd = dev_x(x)
     checked = [0, 1, 3, 4, 6, 2047]

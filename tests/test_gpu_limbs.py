@@ -18,7 +18,7 @@ import pytest
 from oracle import affine as A
 from oracle import c_oracle as C
 
-from test_gpu_parity import ACC_REL, PROJ, assert_close, assert_rounded, dev_triple, dev_x, host_bits, random_triple
+from test_gpu_parity import ACC_REL, F32_REL, PROJ, assert_close, assert_rounded, dev_triple, dev_x, host_bits, random_triple
 
 pytestmark = pytest.mark.gpu
 
@@ -151,6 +151,48 @@ def test_non_finite_x_reaches_y(gpu_lib, value):
     lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
     y = host_bits(run(lin, x, True, 1, gpu_lib))
     assert not np.isfinite(y).any()
+    lin.close()
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+@pytest.mark.parametrize("n,k", [(4096 + 8, 3840), (3840, 15360)])
+def test_rows_of_tiny_values(gpu_lib, n, k, m):
+    """Rows whose every value is tiny: normal values near 2^-115 (below the 2^-108 where
+    the int8 kernels' split exponent is clamped), bf16 subnormals only (group exponent 0),
+    and groups of each mixed within a row, fp32 output, each row against the oracle.
+    The bf16 kernels meet the accumulation bar on every row.  The int8 kernels clamp the
+    split exponent at 19, i.e. they round x to a multiple of 2^-127 in a group whose
+    largest |x| lies below 2^-108 (a group of bf16 subnormals only reads as zeros), so
+    their error is held to that rounding's bound, 2^-128 sum_k |W[n, k]| on top of the
+    accumulation bar, and on the normal rows that is still below 2e-3 of the row's RMS."""
+    wq, s, b = random_triple(n, k, seed=n + k + 11 * m)
+    rng = np.random.default_rng(900 + m)
+    lin = gpu_lib.QuantizedLinear(*dev_triple(wq, s, b))
+    w_abs = np.abs(C.dequantize(wq, s, b).astype(np.float64)).sum(axis=1)
+    scales = [2.0 ** -115, 2.0 ** -130]
+    for case in ("normal", "subnormal", "mixed"):
+        xf = rng.standard_normal((m, k))
+        if case == "mixed":
+            xf = xf * np.where((np.arange(k) // 64) % 2 == 0, scales[0], scales[1])
+        else:
+            xf = xf * scales[case == "subnormal"]
+        x = A.f32_to_bf16_bits(xf.astype(np.float32))
+        if case == "subnormal":
+            assert ((x & 0x7F80) == 0).all() and (x & 0x7F).any()
+        y_exact = C.qmm_f64(x, wq, s, b)
+        for variant in (1, 2):
+            y = host_bits(run(lin, x, True, variant, gpu_lib)).astype(np.float64)
+            for r in range(m):
+                rms = float(np.sqrt(np.mean(y_exact[r] ** 2)))
+                what = f"{case} rows {n}x{k} m={m} kernel {variant} row {r}"
+                err = np.abs(y[r] - y_exact[r])
+                if variant == 2:
+                    assert float(err.max()) < ACC_REL * rms, f"{what}: {err.max() / rms:.3e} x RMS"
+                else:
+                    bound = ACC_REL * rms + 2.0 ** -128 * w_abs
+                    assert (err <= bound).all(), f"{what}: {float(np.max(err / bound)):.3f} x the bound"
+                    if case != "subnormal":
+                        assert float(err.max()) < F32_REL * rms, f"{what}: {err.max() / rms:.3e} x RMS"
     lin.close()
 
 

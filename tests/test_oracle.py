@@ -328,7 +328,7 @@ def test_bf16_rounding_helper_pins_one_rounding_of_a_near_exact_value():
     # a tiny output carrying an error of 1e-3 RMS (far above its half ulp)
     j = np.unravel_index(np.argmin(np.abs(y)), y.shape)
     tiny = rne.copy()
-    tiny[j] = A.f32_to_bf16_bits(np.float32(y[j] + 1e-3 * rms))
+    tiny[j] = A.f32_to_bf16_bits(np.float32(y[j] + 1e-3 * rms))[0]
     assert not A.check_bf16_rounding(tiny, y)[0]
 
 

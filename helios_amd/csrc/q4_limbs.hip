@@ -423,13 +423,19 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint
             }
         }
     };
-    const uint4 xa = load_unit((int)threadIdx.x);
-    const uint4 xb = load_unit(nthr + (int)threadIdx.x);
+    // the first kPre passes of x are requested before the weights (loads complete in
+    // order: an x load issued after them waits for every weight load in flight); 8
+    // rows of K = 3840-4096 take four passes of 1024 threads
+    constexpr int kPre = MT == 8 ? 4 : 2;
+    uint4 xp[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) xp[i] = load_unit(i * nthr + (int)threadIdx.x);
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) issue(b);
-    stage(xa, (int)threadIdx.x);
-    if (nthr < units) stage(xb, nthr + (int)threadIdx.x);
-    for (int f0 = 2 * nthr; f0 < units; f0 += nthr) stage(load_unit(f0 + (int)threadIdx.x), f0 + (int)threadIdx.x);
+#pragma unroll
+    for (int i = 0; i < kPre; ++i)
+        if (i == 0 || i * nthr < units) stage(xp[i], i * nthr + (int)threadIdx.x);
+    for (int f0 = kPre * nthr; f0 < units; f0 += nthr) stage(load_unit(f0 + (int)threadIdx.x), f0 + (int)threadIdx.x);
     for (int c = (int)threadIdx.x; c < nch; c += nthr)
         *reinterpret_cast<uint4*>(limbs + c * kChunkStride + kChunkBytes) = make_uint4(0, 0, 0, 0);
     for (int t = (int)threadIdx.x; t < slot_rbs * WAVES * MT * 16; t += nthr) slots[t] = 0.f;

@@ -705,11 +705,17 @@ size_t limb_rows_lds_bytes(const Layout& l, int m) { return limb_rows_plan(l, ro
 
 bool limb_rows_preferred(const Layout& l, int m) {
     if (m == 2) return true;
-    // 3-8 rows: only wide 4-bit outputs gain (qkv and o lose at 8 rows; the lm_head at
-    // 8 rows 102-104.6 us phased against 114 for the bf16 kernels); the two-plane 8-bit
-    // handles were not measured on these shapes
+    // 3-8 rows: wide 4-bit outputs gain (the lm_head at 8 rows 102-104.6 us phased
+    // against 114 for the bf16 kernels); narrower ones at 4 rows with K up to 4096 (qkv
+    // 8192x3840 6.8 against 7.3 us, o 3840x4096 5.2 against 5.4, q 5.2 against 5.4, k
+    // 2048x3840 4.9 against 5.0; 1024-wide K even; o of K = 8192 8.3 against 7.8) and
+    // at 3 rows from 512 row blocks (qkv 6.8 against 7.1; q 5.3 against 5.2).  From 5
+    // rows those lose (qkv 8.2 against 7.6-7.9 us, o 6.9 against 5.7).  The two-plane
+    // 8-bit handles were not measured on these shapes.
+    if (l.kx != l.k) return false;
     const int cus = device_cus();
-    return l.kx == l.k && l.nb >= 3 * cus;
+    if (l.nb >= 3 * cus) return true;
+    return l.gp <= 32 && ((m == 4 && l.nb >= 128) || (m == 3 && l.nb >= 2 * cus));
 }
 
 hipError_t launch_decode_limb_rows(const uint4* tiles, const uint16_t* x, const OutParams& op, int m,

@@ -641,7 +641,9 @@ namespace {
 //  * up to four row blocks per CU: one workgroup per CU, two chunks in flight,
 //    contiguous runs: gate 15360x3840 9.5 / 11.6 (12.3 / 13.5);
 //  * more, up to 16 per CU: two workgroups per CU, one chunk in flight, blocks dealt
-//    round the grid: the gate|up pair 14.6 / 18.4 (19.1 / 20.4);
+//    round the grid: the gate|up pair 14.6 / 18.4 (19.1 / 20.4); at 8 rows the LDS
+//    admits one workgroup per CU and two chunks are in flight (16.3-16.7 against
+//    16.7-17.2 us with one, x's passes all requested first);
 //  * more still (the lm_head): one 16-wave workgroup per CU, two chunks in flight,
 //    blocks dealt round the grid, the run walked in phases of two row blocks (the
 //    kernel's BATCH): 90.3-91.2 / 102-104.6 (98.2 / 114-119.5);
@@ -681,7 +683,7 @@ LimbRowsPlan limb_rows_plan(const Layout& l, int mt) {
     else if (l.nb <= 4 * cus)
         p.c = {16, 1, 2, false};
     else if (l.nb <= 16 * cus)
-        p.c = {16, 2, 1, true};
+        p.c = {16, 2, mt == 8 ? 2 : 1, true};
     else
         p.c = {8, 2, 2, true};
     int per_cu = p.c.per_cu;
@@ -752,7 +754,7 @@ hipError_t launch_decode_limb_rows(const uint4* tiles, const uint16_t* x, const 
         if (!p.c.strided)
             Q4_LR(8, 2, 16, false);
         else if (p.c.waves == 16)
-            Q4_LR(8, 1, 16, true);
+            Q4_LR(8, 2, 16, true);
         else
             Q4_LR(8, 2, 8, true);
     }

@@ -512,7 +512,7 @@ def limb_rows_plan(nb, gp, mt, cus=256):
     elif nb <= 4 * cus:
         waves, per_cu, nbuf, strided = 16, 1, 2, False
     elif nb <= 16 * cus:
-        waves, per_cu, nbuf, strided = 16, 2, 1, True
+        waves, per_cu, nbuf, strided = 16, 2, 2 if mt == 8 else 1, True
     else:
         waves, per_cu, nbuf, strided = 8, 2, 2, True
     nch = (gp + 1) // 2

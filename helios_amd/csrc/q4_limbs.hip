@@ -425,8 +425,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_limb_rows_kernel(const uint
     };
     // the first kPre passes of x are requested before the weights (loads complete in
     // order: an x load issued after them waits for every weight load in flight); 8
-    // rows of K = 3840-4096 take four passes of 1024 threads
-    constexpr int kPre = MT == 8 ? 4 : 2;
+    // rows of K = 3840-4096, and 2 rows of K = 15360 (the 16-wave launches of long K),
+    // take four passes of 1024 threads.  (Four for the other launches cost their
+    // registers: the pair at 2 rows 13.13 -> 13.46 us.)
+    constexpr int kPre = MT == 8 || (MT == 2 && WAVES == 16) ? 4 : 2;
     uint4 xp[kPre];
 #pragma unroll
     for (int i = 0; i < kPre; ++i) xp[i] = load_unit(i * nthr + (int)threadIdx.x);

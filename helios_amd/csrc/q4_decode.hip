@@ -271,22 +271,26 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
         const int rowc = k >> 3;
         const int nthr = waves * 64;
         const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)kx * 2u);
-        uint4 tmp[4];
-        auto load_x = [&](int c0) {
+        // up to kXB batches of four x units per thread are requested before the weights
+        // (loads complete in order: x requested after them waits for every weight load
+        // in flight); 16 rows of K = 3840 take 15 units per thread of 512
+        constexpr int kXB = 4;
+        uint4 tmp[kXB][4];
+        auto load_x = [&](uint4* t, int c0) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = c0 + u * nthr + (int)threadIdx.x;
-                tmp[u] = buffer_load16(xrs, c < xchunks ? xprime_offset(c, k, kx) : kOutOfRange);
+                t[u] = buffer_load16(xrs, c < xchunks ? xprime_offset(c, k, kx) : kOutOfRange);
             }
         };
-        auto store_x = [&](int c0) {
+        auto store_x = [&](const uint4* t, int c0) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = c0 + u * nthr + (int)threadIdx.x;
                 const int row = c / rowc;
                 const int cr = c - row * rowc;
-                if (c < xchunks) lds[row * row16 + cr] = tmp[u];
-                const uint32_t w4[4] = {tmp[u].x, tmp[u].y, tmp[u].z, tmp[u].w};
+                if (c < xchunks) lds[row * row16 + cr] = t[u];
+                const uint32_t w4[4] = {t[u].x, t[u].y, t[u].z, t[u].w};
                 float sum = 0.f;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) sum += bf16_lo(w4[j]) + bf16_hi(w4[j]);
@@ -294,15 +298,20 @@ __global__ __launch_bounds__(512) void decode_stream_kernel(
                 if (c < xchunks && (lane & 7) == 0) negx[(cr >> 3) * 16 + row] = -sum;
             }
         };
-        // first batch of x, then every weight buffer, then the batch is stored: in
-        // straight-line code, so waiting for x leaves the weight loads in flight
-        load_x(0);
+        // the first batches of x, then every weight buffer, then the batches are stored:
+        // in straight-line code, so waiting for x leaves the weight loads in flight
+        const int xb = (xchunks + 4 * nthr - 1) / (4 * nthr) < kXB ? (xchunks + 4 * nthr - 1) / (4 * nthr) : kXB;
+#pragma unroll
+        for (int b = 0; b < kXB; ++b)
+            if (b == 0 || b < xb) load_x(tmp[b], b * 4 * nthr);
 #pragma unroll
         for (int b = 0; b < NBUF; ++b) issue(w[b], sv[b], b);
-        store_x(0);
-        for (int c0 = 4 * nthr; c0 < xchunks; c0 += 4 * nthr) {  // rows past 2048 elements per thread
-            load_x(c0);
-            store_x(c0);
+#pragma unroll
+        for (int b = 0; b < kXB; ++b)
+            if (b == 0 || b < xb) store_x(tmp[b], b * 4 * nthr);
+        for (int c0 = kXB * 4 * nthr; c0 < xchunks; c0 += 4 * nthr) {  // rows past 8192 elements per thread
+            load_x(tmp[0], c0);
+            store_x(tmp[0], c0);
         }
         for (int c = threadIdx.x; c < m_rows * (kPad >> 3); c += nthr)
             lds[(c / (kPad >> 3)) * row16 + rowc + (c % (kPad >> 3))] = make_uint4(0, 0, 0, 0);

@@ -125,8 +125,10 @@ __global__ __launch_bounds__(1024) void decode_kernel(
         }
 
         // x operands for one group pair: [group][half]; columns past the row (padding
-        // or beyond this pass's pairs) read as zero
-        uint4 a[2][4];
+        // or beyond this pass's pairs) read as zero.  kAhead pairs are in flight: from
+        // L2 (XLDS = false) each is a round trip, and 8-pair passes chain eight
+        constexpr int kAhead = !XLDS && GPW == 8 ? 2 : 1;
+        uint4 a[kAhead + 1][4];
         auto load_x = [&](uint4* dst, int i) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -143,12 +145,13 @@ __global__ __launch_bounds__(1024) void decode_kernel(
                 }
             }
         };
-        load_x(a[0], 0);
+#pragma unroll
+        for (int i = 0; i < kAhead; ++i) load_x(a[i], i);
 
 #pragma unroll
         for (int i = 0; i < GPW; ++i) {
-            if (i + 1 < GPW) load_x(a[(i + 1) & 1], i + 1);
-            const uint4* ax = a[i & 1];
+            if (i + kAhead < GPW) load_x(a[(i + kAhead) % (kAhead + 1)], i + kAhead);
+            const uint4* ax = a[i % (kAhead + 1)];
 #pragma unroll
             for (int gi = 0; gi < 2; ++gi) {
                 const bf16x8 x0 = __builtin_bit_cast(bf16x8, ax[2 * gi]);

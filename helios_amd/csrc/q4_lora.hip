@@ -57,13 +57,27 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restri
     const uint16_t* hp = ah + (long)r * k + 8 * kq;
     const uint16_t* lp = al + (long)r * k + 8 * kq;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int st = w0; st < w1; ++st) {
-        const bf16x8 xa = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xp + 32 * st));
-        const bf16x8 bh = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(hp + 32 * st));
-        const bf16x8 bl = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(lp + 32 * st));
-        acc = mfma16x16x32(xa, bh, acc);
-        acc = mfma16x16x32(xa, bl, acc);
+    // the steps' loads go out in batches of kBatch before their MFMAs (a wave has one
+    // or two batches, so one or two round trips instead of one per few steps; steps
+    // past the wave's range reload its last step and skip the MFMAs)
+    constexpr int kBatch = 8;
+    for (int st0 = w0; st0 < w1; st0 += kBatch) {
+        uint4 xv[kBatch], hv[kBatch], lv[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int st = st0 + i < w1 ? st0 + i : w1 - 1;
+            xv[i] = *reinterpret_cast<const uint4*>(xp + 32 * st);
+            hv[i] = *reinterpret_cast<const uint4*>(hp + 32 * st);
+            lv[i] = *reinterpret_cast<const uint4*>(lp + 32 * st);
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            if (st0 + i < w1) {
+                const bf16x8 xa = __builtin_bit_cast(bf16x8, xv[i]);
+                acc = mfma16x16x32(xa, __builtin_bit_cast(bf16x8, hv[i]), acc);
+                acc = mfma16x16x32(xa, __builtin_bit_cast(bf16x8, lv[i]), acc);
+            }
+        }
     }
     __shared__ f32x4 red[kDownWaves][64];
     red[wave][lane] = acc;

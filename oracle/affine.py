@@ -263,11 +263,12 @@ def geglu_ops(gate, up, bf16: bool) -> np.ndarray:
     r = round_to_bf16 if bf16 else (lambda v: np.asarray(v, dtype=np.float32))
     c_tanh, c_cubic = r(f32(GEGLU_C_TANH)), r(f32(GEGLU_C_CUBIC))
     g, u = r(g), r(u)
-    g3 = r(g * g * g)
-    a = r(g + r(c_cubic * g3))
-    t = r(np.tanh(r(c_tanh * a)))
-    gelu = r(r(f32(0.5) * g) * r(f32(1.0) + t))
-    return r(gelu * u)
+    with np.errstate(over="ignore"):  # g**3 past the float32 range is inf, as in the reference's ops
+        g3 = r(g * g * g)
+        a = r(g + r(c_cubic * g3))
+        t = r(np.tanh(r(c_tanh * a)))
+        gelu = r(r(f32(0.5) * g) * r(f32(1.0) + t))
+        return r(gelu * u)
 
 
 def gelu_tanh_times(gate_bits, up_bits) -> np.ndarray:

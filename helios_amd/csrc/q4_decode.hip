@@ -90,15 +90,18 @@ __global__ __launch_bounds__(1024) void decode_kernel(
         // cooperative copy x -> LDS
         const int chunks = (int)(xbytes >> 4);
         const int nthr = waves * 64;
-        uint4 tmp[4];
-        for (int c0 = 0; c0 < chunks; c0 += 4 * nthr) {
+        // eight units per thread in flight (x of 8 rows x 3840 on 512 threads is 7.5),
+        // so the copy is one round trip
+        constexpr int kCopy = 8;
+        uint4 tmp[kCopy];
+        for (int c0 = 0; c0 < chunks; c0 += kCopy * nthr) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < kCopy; ++u) {
                 const int c = c0 + u * nthr + (int)threadIdx.x;
                 tmp[u] = buffer_load16(xrs, c < chunks ? xprime_offset(c, k, kx) : kOutOfRange);
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < kCopy; ++u) {
                 const int c = c0 + u * nthr + (int)threadIdx.x;
                 if (c < chunks) xs_lds[c] = tmp[u];
             }
